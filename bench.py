@@ -1,0 +1,270 @@
+"""Benchmark of the spira_amd hot path on one MI355X.
+
+Headline (BASELINE.json metric): end-to-end latency of the config-4 workload
+-- SparseResUNet42, fp16, random-init weights, on a 200k-voxel synthetic
+indoor scene -- timed like the reference (scripts/end_to_end_experiment.py:
+156-252): kernel-map cache reset, then `order()` (pack + sort), the
+network-wide kernel-map build (`add_all_kernel_maps`) and the forward pass
+inside one event-timed region.  Also reported on the same run:
+  * kmap_build_us: one kernel-map search (config 2, ~100k LiDAR voxels,
+    k=3, 64-bit keys, output-stationary layout) as in mapping_experiment.py;
+  * layer_ms: one output-stationary fp16 layer (config 3, C=64);
+  * roofline: the dominant kernel (output-stationary MFMA conv) against the
+    fp16 MFMA peak, and kmap_roofline: the map search against HBM peak;
+  * cpu_baseline: the same end-to-end pipeline run by the OpenMP CPU
+    restatement (oracle/) on the host cores (one scene).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--dataflow", type=int, default=0, help="map dataflow used by every layer")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP-event timing on the current stream (the one the kernels run on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def __call__(self, fn, reps: int, warmup: int = 2):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = []
+        for _ in range(reps):
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            times.append(s.elapsed_time(e))
+        return float(np.mean(times)), float(np.min(times))
+
+
+def e2e_leg(torch, args, coords_np):
+    import spira_amd
+    from spira_amd.networks import SparseResUNet42, kmap_schedule
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = SparseResUNet42(in_channels=3).to(dev).half().eval()
+    cache = spira_amd.nn.KernelMapCache()
+    spira_amd.set_kernel_map_cache(model, cache)
+    for m in model.modules():
+        if isinstance(m, spira_amd.nn.SparseConv):
+            m._tunable_config["map_dataflow"] = args.dataflow
+    ts, ks, ss = kmap_schedule("UNet")
+    coords = torch.from_numpy(coords_np).to(dev)
+    feats = torch.randn(coords.shape[0], 3, device=dev, dtype=torch.float16)
+
+    def step():
+        cache.reset()
+        x = spira_amd.SparseTensor(coordinates=coords, features=feats, double=True)
+        x.order()
+        cache.add_all_kernel_maps(x._coordinates, ks, ss, ts, (1, 1, 1), [args.dataflow] * len(ks))
+        return model(x)
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        s.record()
+        for _ in range(args.steps):
+            out = step()
+        e.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / args.steps
+        ms = s.elapsed_time(e) / args.steps
+    return ms, wall, model, [o._features for o in out]
+
+
+def kmap_leg(torch, keys_np):
+    from spira_amd.nn import functional as F
+    dev = torch.device("cuda:0")
+    keys = torch.from_numpy(keys_np).to(dev)
+    timer = Timer(torch)
+    S = T = keys.shape[0]
+    out = {}
+    for k in (3, 5):
+        mean_ms, min_ms = timer(lambda: F.build_kmap(keys, keys, k, 1, 0), reps=20, warmup=3)
+        K = k ** 3
+        nbytes = 8 * S + 8 * T + 4 * K * T
+        out[k] = {"us": mean_ms * 1e3, "min_us": min_ms * 1e3, "bytes": nbytes,
+                  "gbs": nbytes / (mean_ms * 1e-3) / 1e9}
+    return out
+
+
+def layer_leg(torch, keys_np, C=64):
+    from oracle import oracle as orc  # noqa: F401  (not used on the timed path)
+    from spira_amd.nn import functional as F
+    dev = torch.device("cuda:0")
+    keys = torch.from_numpy(keys_np).to(dev)
+    m = F.build_kmap(keys, keys, 3, 1, 0)
+    S = T = keys.shape[0]
+    X = torch.randn(S, C, device=dev, dtype=torch.float16)
+    W = (torch.randn(27, C, C, device=dev) / np.sqrt(27 * C)).half()
+    P = int((m[2][:T] >= 0).sum().item())
+    timer = Timer(torch)
+    mean_ms, min_ms = timer(lambda: F.sparse_convolution_forward_os(S, T, m[2], X, W), reps=20, warmup=3)
+    flops = 2.0 * P * C * C
+    return {"ms": mean_ms, "min_ms": min_ms, "pairs": P, "flops": flops,
+            "tflops": flops / (mean_ms * 1e-3) / 1e12, "C": C, "voxels": S}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the same end-to-end pipeline on the host through the oracle
+# ---------------------------------------------------------------------------
+def cpu_e2e(model, coords_np, feats_np):
+    import torch
+    from oracle import oracle as orc
+    from spira_amd import nn as spnn
+    from spira_amd.networks import SparseResBlock
+
+    keys, perm = orc.flatten_sort(coords_np, True)
+    x = np.ascontiguousarray(feats_np[perm], dtype=np.float32)
+    vox = {(1, 1, 1): keys}
+    maps = {}
+
+    def coords_of(stride):
+        if stride not in vox:
+            vox[stride] = orc.downsample(keys, stride)
+        return vox[stride]
+
+    def conv(layer, feats, stride):
+        W = layer.kernel.detach().float().cpu().numpy()
+        if layer.is_trivial:
+            return feats @ W[0], stride
+        if layer.transposed:
+            out_stride = tuple(a // b for a, b in zip(stride, layer.stride))
+            key = (out_stride, stride, layer.kernel_size)
+            if key not in maps:
+                maps[key] = orc.search(coords_of(out_stride), coords_of(stride), layer.kernel_size, out_stride, orc.OS)
+            tmap = orc.convert_transposed_os(maps[key], len(coords_of(out_stride)))
+            return orc.conv_os_f32(tmap, len(coords_of(out_stride)), feats, W), out_stride
+        out_stride = tuple(a * b for a, b in zip(stride, layer.stride))
+        key = (stride, out_stride, layer.kernel_size)
+        if key not in maps:
+            maps[key] = orc.search(coords_of(stride), coords_of(out_stride), layer.kernel_size, stride, orc.OS)
+        return orc.conv_os_f32(maps[key], len(coords_of(out_stride)), feats, W), out_stride
+
+    def run(mod, feats, stride):
+        if isinstance(mod, spnn.SparseConv):
+            return conv(mod, feats, stride)
+        if isinstance(mod, spnn.BatchNorm):
+            rm, rv = mod.running_mean.float().cpu().numpy(), mod.running_var.float().cpu().numpy()
+            g, b = mod.weight.detach().float().cpu().numpy(), mod.bias.detach().float().cpu().numpy()
+            return (feats - rm) / np.sqrt(rv + mod.eps) * g + b, stride
+        if isinstance(mod, (spnn.ReLU,)):
+            return np.maximum(feats, 0), stride
+        if isinstance(mod, torch.nn.Identity):
+            return feats, stride
+        if isinstance(mod, SparseResBlock):
+            a, s1 = run(mod.main, feats, stride)
+            b, _ = run(mod.shortcut, feats, stride)
+            return np.maximum(a + b, 0), s1
+        if isinstance(mod, torch.nn.Sequential):
+            for sub in mod:
+                feats, stride = run(sub, feats, stride)
+            return feats, stride
+        raise TypeError(type(mod))
+
+    def level(feats, stride, encoders, decoders):
+        if len(encoders) == 0:
+            return [(feats, stride)]
+        f2, s2 = run(encoders[0], feats, stride)
+        outs = level(f2, s2, encoders[1:], decoders[:-1])
+        up, su = run(decoders[-1]["upsample"], *outs[-1])
+        y, sy = run(decoders[-1]["fuse"], np.concatenate([up, feats], axis=1), su)
+        return [(feats, stride)] + outs + [(y, sy)]
+
+    f, s = run(model.stem, x, (1, 1, 1))
+    return level(f, s, list(model.encoders), list(model.decoders))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one MI355X; "
+                                   "use --gpus 1"}))
+        sys.exit(2)
+    import torch
+    from spira_amd import scenes
+
+    legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer"}
+    with open(os.path.join(ROOT, "BASELINE.json")) as f:
+        baseline = json.load(f)
+
+    indoor = scenes.indoor()
+    res = {"metric": baseline["metric"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+           "data": "synthetic (seeded scenes, random-init weights)"}
+    cfg = {"workload": "config4: SparseResUNet42 fp16, 200k-voxel indoor scene, end-to-end "
+                       "(order + network-wide kernel maps + forward)",
+           "voxels": int(indoor.shape[0]), "key_bits": 64, "map_dataflow": args.dataflow}
+    model = None
+    if "e2e" in legs:
+        ms, wall, model, _ = e2e_leg(torch, args, indoor)
+        res["value"] = ms
+        res["ms_per_step"] = ms
+        res["wall_ms_per_step"] = wall
+    lidar = scenes.lidar()
+    from oracle import oracle as orc
+    lkeys, _ = orc.flatten_sort(lidar, True)
+    if "kmap" in legs:
+        km = kmap_leg(torch, lkeys)
+        res["kmap_build_us"] = km[3]["us"]
+        res["kmap_build_us_k5"] = km[5]["us"]
+        res["kmap_roofline"] = {"bound": "hbm", "achieved": km[3]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": km[3]["gbs"] / HBM_PEAK_GBS, "traffic": None,
+                                "kernel": "kmap_search_kernel (config 2, k=3, OS layout)",
+                                "algorithmic_bytes": km[3]["bytes"]}
+        res["kmap_roofline_k5"] = {"achieved": km[5]["gbs"], "frac": km[5]["gbs"] / HBM_PEAK_GBS,
+                                   "algorithmic_bytes": km[5]["bytes"]}
+        cfg["kmap_voxels"] = int(lkeys.shape[0])
+    if "layer" in legs:
+        ly = layer_leg(torch, lkeys)
+        res["layer_ms"] = ly["ms"]
+        res["roofline"] = {"bound": "mfma", "achieved": ly["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": ly["tflops"] / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+                           "kernel": "os_f16_kernel (config 3, C=64, k=3, 100k LiDAR voxels)",
+                           "algorithmic_flops": ly["flops"], "valid_pairs": ly["pairs"]}
+    if not args.no_cpu and model is not None:
+        feats = np.random.default_rng(0).standard_normal((indoor.shape[0], 3)).astype(np.float32)
+        t0 = time.perf_counter()
+        cpu_e2e(model, indoor, feats)
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        res["cpu_baseline"] = {"value": cpu_ms, "unit": "ms", "cores": orc.threads(), "kind": "port",
+                               "sample": "one full config-4 scene end-to-end (sort, downsample, all maps, "
+                                         "all 42 layers, fp32) by the OpenMP oracle"}
+    res["config"] = cfg
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

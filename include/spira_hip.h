@@ -1,0 +1,194 @@
+/*
+ * spira_hip.h -- C ABI of libspira_hip.so, the gfx950 (MI355X) kernel library
+ * behind the spira sparse-convolution extension.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is device memory on
+ * the current HIP device unless stated otherwise; `stream` is a hipStream_t.
+ * Every function returns 0 on success or a non-zero status; the message of
+ * the last failure on the calling thread is spira_hip_last_error().
+ *
+ * Keys are packed voxel coordinates: key_bits = 64 packs x24|y24|z16,
+ * key_bits = 32 packs x12|y12|z8 (reference compress_layout.h:11-44).
+ * Key arrays are uint64_t / uint32_t bit patterns (torch int64 / int32).
+ *
+ * Each declaration names the reference interface it replaces; reference
+ * paths are under source/csrc/spira/ of SPIN-Research-Group/Spira.
+ */
+#ifndef SPIRA_HIP_H_
+#define SPIRA_HIP_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread (reference: SpiraException,
+ * common/exception.h:9-28). */
+const char *spira_hip_last_error(void);
+
+/* ---------------------------------------------------------------- coords */
+
+/* coords [n,3] int32 -> keys [n] (reference: kernels Compress,
+ * cuda/kernels/compress.cuh:9-23). */
+int spira_hip_pack(const int32_t *coords, int64_t n, int key_bits, void *keys, hipStream_t stream);
+
+/* keys [n] -> coords [n,3] int32 (reference: cuda_unflatten,
+ * torch/cuda_arg_sort_coordinates.cu:41-65; kernel UnCompress compress.cuh:28-46). */
+int spira_hip_unpack(const void *keys, int64_t n, int key_bits, int32_t *coords, hipStream_t stream);
+
+/* Workspace bytes for spira_hip_flatten_sort. */
+int spira_hip_flatten_sort_workspace(int64_t n, int key_bits, size_t *bytes);
+
+/* Pack, then stable ascending sort on the unsigned key; perm_out[i] is the
+ * input row of sorted key i (reference: cuda_flatten_sort,
+ * torch/cuda_arg_sort_coordinates.cu:11-39; FlattenSort arg_sort_coodrinates.cu:36-88). */
+int spira_hip_flatten_sort(const int32_t *coords, int64_t n, int key_bits, void *keys_out, int32_t *perm_out,
+                           void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes for spira_hip_downsample. */
+int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes);
+
+/* out = sorted unique (keys & stride mask); *d_count (device) = number of
+ * unique keys.  Strides must be powers of two (reference: cuda_downsample,
+ * torch/cuda_arg_sort_coordinates.cu:68-105; SortUnique arg_sort_coodrinates.cu:139-192). */
+int spira_hip_downsample(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz, void *out_keys,
+                         uint32_t *d_count, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ----------------------------------------------------------- kernel maps */
+
+#define SPIRA_KMAP_OS 0     /* [Tp, K] int32, column iz*O + o (z-major)            */
+#define SPIRA_KMAP_WS 1     /* [K, Tp] int32, row o*kz + iz (canonical)             */
+#define SPIRA_KMAP_HYBRID 2 /* [K, Tp] int32, row row_perm[o*kz + iz]               */
+#define SPIRA_KMAP_NOZ 3    /* [Tp, K] int32, canonical columns, no z-scan          */
+
+/* Kernel-map search of sorted unique `sources` for every target and kernel
+ * offset; Tp = round_up(num_targets, 128), O = kx*ky, K = O*kz.  row_perm is a
+ * HOST array of K entries (hybrid layout only, else NULL).  tile_counts
+ * (nullable, [K, Tp/64], WS / HYBRID layouts) receives the number of valid
+ * entries of every (row, 64-target tile) for spira_hip_kmap_scan.
+ * (reference: kernels BinarySearch_kz_{ostationary,wstationary,hybrid} and
+ * BinarySearch_no_z_ostationary, cuda/kernels/query_sorted.cuh:8-297, launched
+ * by cuda/functions/query_sorted_index.cu:12-143, 912-937; offsets from
+ * torch/cuda_sparse_convolution_mapping.cu:10-50, 114-157). */
+int spira_hip_kmap_search(const void *sources, int64_t num_sources, const void *targets, int64_t num_targets,
+                          int key_bits, int kx, int ky, int kz, int sx, int sy, int sz, int layout,
+                          const int32_t *row_perm, int32_t *kernel_map, int32_t *tile_counts, hipStream_t stream);
+
+/* Workspace bytes for spira_hip_kmap_scan over num_counts tile counts. */
+int spira_hip_kmap_scan_workspace(int64_t num_counts, size_t *bytes);
+
+/* Exclusive scan of `rows` x `ntiles` tile counts (row-major) into
+ * tile_offsets, plus per-row totals nbsizes [rows], their exclusive scan
+ * naddrs [rows+1] and the scan of the totals rounded up to `quantum`,
+ * qnaddrs [rows+1]; sizes [2] = {total, quantised total}.  naddrs, qnaddrs and
+ * sizes may be NULL.  (reference: cub ReduceByKey / DeviceSelect sizing and
+ * exclusive_scan_for_kernel(_quantified), cuda/functions/query_sorted_index.cu:146-209,
+ * cuda/kernels/quantifier_wstat.cuh:8-66). */
+int spira_hip_kmap_scan(const int32_t *tile_counts, int rows, int64_t ntiles, int quantum, int32_t *tile_offsets,
+                        int32_t *nbsizes, int32_t *naddrs, int32_t *qnaddrs, int32_t *sizes, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+/* Stable compaction of rows [row0, row0+rows) of a [*, Tp] map into
+ * in_idx[p] = source, out_idx[p] = target in (row, target) order, using the
+ * tile offsets of spira_hip_kmap_scan (reference: cub::DeviceSelect::If with
+ * GetEntryPair, cuda/functions/query_sorted_index.cu:170-188, plus the
+ * narrow/transpose to nbmaps [2, P], torch/cuda_sparse_convolution_mapping.cu:361-364). */
+int spira_hip_kmap_emit_pairs(const int32_t *kernel_map, int64_t aligned_targets, int row0, int rows,
+                              const int32_t *tile_offsets, int32_t *in_idx, int32_t *out_idx, hipStream_t stream);
+
+/* Gather / scatter masks [mask_rows, S] and [mask_rows, T]: -1, or the rank
+ * of the entry within its row; `half` also fills the mirrored rows
+ * mask_rows-1-r with sources and targets swapped (reference:
+ * GenerateMasksFromKernelMap(_Half), cuda/kernels/generate_masks_from_kernel_map.cuh:10-62,
+ * launched by cuda/functions/query_sorted_index.cu:424-495, 703-776). */
+int spira_hip_kmap_emit_masks(const int32_t *kernel_map, int64_t num_sources, int64_t num_targets,
+                              int64_t aligned_targets, int row0, int rows, int mask_rows, int half,
+                              const int32_t *tile_offsets, int32_t *source_masks, int32_t *target_masks,
+                              hipStream_t stream);
+
+/* Inverse of an output-stationary map for transposed layers:
+ * out [aligned_sources, K] = -1 except out[s, k] = t where map[t, k] = s
+ * (reference: cuda_convert_transposed_os, torch/cuda_sparse_convolution_mapping.cu:1809-1830;
+ * kernel Convert_out_in_map_kernel, cuda/kernels/convert_transposed_os.cuh:7-16). */
+int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_targets, int num_offsets,
+                                    int64_t aligned_sources, int32_t *out, hipStream_t stream);
+
+/* ptr[0..n) = value (reference: the cudaMemsetAsync(-1) mask initialisation,
+ * cuda/functions/query_sorted_index.cu:475-477). */
+int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t stream);
+
+/* -------------------------------------------------------------- features */
+
+#define SPIRA_F16 0 /* feature / weight storage dtype: IEEE half */
+#define SPIRA_F32 1 /* feature / weight storage dtype: float    */
+
+#define SPIRA_OUT_STORE 0     /* write the output in the storage dtype */
+#define SPIRA_OUT_STORE_F32 1 /* write an fp32 buffer                  */
+#define SPIRA_OUT_ADD_F32 2   /* add into an fp32 buffer               */
+
+/* Workspace bytes of the conv entry points for K offsets (transposed fp16
+ * weights for the MFMA path; 0 otherwise). */
+int spira_hip_conv_workspace(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes);
+
+/* Output-stationary implicit GEMM: targets[t] = sum_j sources[map[t, j]] @
+ * weights[j] for map entries >= 0; map is [>= num_targets, num_offsets],
+ * weights [num_offsets, c_in, c_out]; fp32 accumulation.
+ * (reference: cuda_sparse_convolution_forward_os,
+ * torch/cuda_sparse_convolution_forward.cu:448-496; SparseConvolutionForward_OS
+ * cuda/functions/sparse_convolution.cu:1354-1393; kernels
+ * conv_forward_cuda_setting{1,2,3}_mode0_*, cuda/kernels/output_stat.cuh:20-1031). */
+int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const void *sources,
+                      int64_t num_sources, int c_in, const void *weights, int c_out, int dtype, void *targets,
+                      int out_mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Fused weight-stationary pass over a compacted pair list: for compacted row r
+ * (pairs naddrs[r]..naddrs[r+1] of in_idx/out_idx) target_acc[out] +=
+ * sources[in] @ weights[weight_offset + r]; with mirror_rows = Kw > 0 also
+ * target_acc[in] += sources[out] @ weights[weight_offset + Kw-1-r] for every
+ * r with 2r+1 != Kw.  qnaddrs / quantized_pairs are the 128-rounded scans.
+ * target_acc is fp32 [num_targets, c_out], accumulated atomically.
+ * (reference: cuda_sparse_convolution_forward_ws_merged,
+ * torch/cuda_sparse_convolution_forward.cu:186-250; SparseConvolutionForward_WS_Merged
+ * cuda/functions/sparse_convolution.cu:1267-1295; kernels fetch_on_demand_gemm_*,
+ * cuda/kernels/weight_stat.cuh:33-1221). */
+int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int32_t *in_idx, const int32_t *out_idx,
+                            int rows, const int32_t *naddrs, const int32_t *qnaddrs, int64_t num_pairs,
+                            int64_t quantized_pairs, int weight_offset, int mirror_rows, const void *sources,
+                            int c_in, const void *weights, int num_weights, int c_out, int dtype, float *target_acc,
+                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Gather: buffer[padded_offsets[k] + source_masks[k, s]] = sources[s] for
+ * mask entries >= 0.  padded_offsets is a HOST array of num_offsets entries.
+ * (reference: Gather / PaddedGatherWarpOptimized,
+ * cuda/functions/sparse_convolution.cu:655-697, cuda/kernels/padded_gather_warp_optimized.cuh:11-63). */
+int spira_hip_ws_gather(int64_t num_sources, int c_in, int num_offsets, int dtype, const void *sources,
+                        const int32_t *source_masks, const int64_t *padded_offsets, void *buffer, hipStream_t stream);
+
+/* Grouped GEMM: buffer_out[rows of offset k] (fp32) = buffer_in[rows of
+ * offset k] @ weights[k]; rows / padded_offsets are HOST arrays.
+ * (reference: bucketed cublas{H,S}gemmStridedBatched, BatchedMatMul
+ * cuda/helpers.cu:104-161, driven by cuda/functions/sparse_convolution.cu:1048-1117). */
+int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padded_offsets, int c_in, int c_out,
+                      int dtype, const void *buffer_in, const void *weights, float *buffer_out, void *workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* Scatter: targets[t] = base[t] + sum_k buffer[padded_offsets[k] + target_masks[k, t]]
+ * (base: nullable fp32 [num_targets, c_out])
+ * (reference: Scatter / PaddedScatterWarpOptimized,
+ * cuda/functions/sparse_convolution.cu:699-742, cuda/kernels/padded_scatter_warp_optimized.cuh:11-63). */
+int spira_hip_ws_scatter(int64_t num_targets, int c_out, int num_offsets, int dtype, const int32_t *target_masks,
+                         const int64_t *padded_offsets, const float *buffer, const float *base, void *targets,
+                         hipStream_t stream);
+
+/* dst (storage dtype) = src (fp32), n elements (reference: the half outputs of
+ * the weight-stationary kernels, cuda/kernels/weight_stat.cuh:914). */
+int spira_hip_cast_f32(const float *src, int64_t n, int dtype, void *dst, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPIRA_HIP_H_ */

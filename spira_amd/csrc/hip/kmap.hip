@@ -1,0 +1,532 @@
+// Kernel-map search and kernel-map post-processing for gfx950.
+//
+// Search (reference semantics: query_sorted.cuh:8-297, binary_search.cuh:10-21):
+// for target t and xy-offset o, c = tgt[t] + off[o] (mod 2^bits),
+// idx = lower_bound(src, c); entry(iz=0) = idx if src[idx] == c, then for
+// iz = 1..kz-1: idx += (src[idx] <= c); c += sz; entry(iz) = idx if
+// src[idx] == c.  Indices at or past the end of src give -1.
+//
+// MI355X design: one wave64 owns a tile of 64 consecutive (sorted) targets.
+//  1. For every dx-group of offsets the wave reduces the min / max query key
+//     (all queries of the group lie between them, so their lower bounds lie
+//     between the lower bounds of min and max, whatever modular wrap occurs).
+//  2. All 2*G bounds are found together by a wave-cooperative 64-ary search:
+//     each step every lane probes one evenly spaced key per bound and a
+//     ballot picks the sub-range, so a bound costs ~log64(S) dependent L2
+//     round trips instead of log2(S).
+//  3. The source window [lb(min), lb(max)+kz) is staged in LDS with
+//     coalesced loads; each lane then runs its lower-bound search and z-scan
+//     out of LDS.  Windows larger than the LDS cap fall back to a per-lane
+//     search in global memory restricted to the window (same results).
+//  4. [K, Tp] layouts store rows with coalesced 256-byte wave stores and emit
+//     per-(row, tile) valid counts for compaction (ballot + popcount);
+//     [Tp, K] layouts stage the tile's 64 x K block in LDS and write it out
+//     contiguously.
+#include "common.hpp"
+#include "../../../include/spira_hip.h"
+
+#include <rocprim/rocprim.hpp>
+
+#include <vector>
+
+namespace spira_hip {
+
+constexpr int kGroupMax = 8;      // dx groups (kx <= 8)
+constexpr int kOffsetsMax = 128;  // offsets per map (K <= 128 for the no-z layout)
+constexpr int kWindowCap = 1024;  // LDS window entries per wave
+
+template <typename CT> struct SearchParams {
+  const CT *src;
+  const CT *tgt;
+  int32_t *map;
+  int32_t *tile_counts;
+  int64_t S, T, Tp, ntiles;
+  int G, GS, O, K;
+  int os_layout;  // 1: [Tp, K]; 0: [K, Tp]
+  int zmajor;     // column iz*O + o in the [Tp, K] layout
+  int use_perm;
+  CT sz;
+  CT off[kOffsetsMax];
+  int32_t perm[kOffsetsMax];
+};
+
+template <typename CT> __device__ __forceinline__ CT max_key() { return static_cast<CT>(~static_cast<CT>(0)); }
+
+// Wave-cooperative lower bounds of up to 2*kGroupMax values (wave-uniform).
+template <typename CT>
+__device__ __forceinline__ void wave_lower_bounds(const CT *__restrict__ src, int64_t S, const CT *vals, int ns,
+                                                  int64_t *out) {
+  const int lane = lane_id();
+  int64_t lo[2 * kGroupMax], hi[2 * kGroupMax];
+#pragma unroll
+  for (int s = 0; s < 2 * kGroupMax; ++s) {
+    lo[s] = 0;
+    hi[s] = S;
+  }
+  while (true) {
+    bool more = false;
+#pragma unroll
+    for (int s = 0; s < 2 * kGroupMax; ++s)
+      if (s < ns && hi[s] - lo[s] > 64) more = true;
+    if (!more) break;
+    CT sample[2 * kGroupMax];
+    int64_t step[2 * kGroupMax];
+#pragma unroll
+    for (int s = 0; s < 2 * kGroupMax; ++s) {
+      step[s] = (hi[s] - lo[s] + 63) >> 6;
+      int64_t p = lo[s] + lane * step[s];
+      sample[s] = (s < ns && hi[s] - lo[s] > 64 && p < hi[s]) ? src[p] : max_key<CT>();
+    }
+#pragma unroll
+    for (int s = 0; s < 2 * kGroupMax; ++s) {
+      if (s < ns && hi[s] - lo[s] > 64) {
+        int64_t p = lo[s] + lane * step[s];
+        bool ge = (p >= hi[s]) || (sample[s] >= vals[s]);
+        uint64_t m = ballot(ge);
+        int f = m ? __builtin_ctzll(m) : 64;
+        int64_t nlo = f == 0 ? lo[s] : lo[s] + (f - 1) * step[s] + 1;
+        int64_t nhi = f == 64 ? hi[s] : lo[s] + f * step[s];
+        if (nhi > hi[s]) nhi = hi[s];
+        lo[s] = nlo;
+        hi[s] = nhi;
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 2 * kGroupMax; ++s) {
+    if (s < ns) {
+      int64_t p = lo[s] + lane;
+      bool ge = (p >= hi[s]) || (src[p] >= vals[s]);
+      uint64_t m = ballot(ge);
+      out[s] = m ? lo[s] + __builtin_ctzll(m) : hi[s];
+    }
+  }
+}
+
+template <typename CT>
+__device__ __forceinline__ int lds_lower_bound(const CT *win, int n, CT v) {
+  int base = 0, len = n;
+  while (len > 0) {
+    int half = len >> 1;
+    if (win[base + half] < v) {
+      base += half + 1;
+      len -= half + 1;
+    } else {
+      len = half;
+    }
+  }
+  return base;
+}
+
+template <typename CT>
+__device__ __forceinline__ int64_t global_lower_bound(const CT *__restrict__ src, int64_t lo, int64_t hi, CT v) {
+  while (lo < hi) {
+    int64_t m = (lo + hi) >> 1;
+    if (src[m] >= v) hi = m;
+    else lo = m + 1;
+  }
+  return lo;
+}
+
+template <typename CT, int KZ>
+__global__ __launch_bounds__(64) void kmap_search_kernel(const SearchParams<CT> p) {
+  extern __shared__ __align__(16) char smem[];
+  CT *win = reinterpret_cast<CT *>(smem);
+  int32_t *stage = reinterpret_cast<int32_t *>(smem + kWindowCap * sizeof(CT));
+
+  const int lane = threadIdx.x;
+  const int64_t tile = blockIdx.x;
+  const int64_t t = tile * 64 + lane;
+  const bool valid = t < p.T;
+  const CT key = valid ? p.tgt[t] : CT(0);
+  const CT sz = p.sz;
+
+  if (ballot(valid) == 0) {
+    // fully padded tile: every entry is -1
+    if (p.os_layout) {
+      for (int i = lane; i < 64 * p.K; i += 64) p.map[tile * 64 * p.K + i] = -1;
+    } else {
+      for (int r = 0; r < p.K; ++r) {
+        p.map[r * p.Tp + t] = -1;
+        if (p.tile_counts && lane == 0) p.tile_counts[r * p.ntiles + tile] = 0;
+      }
+    }
+    return;
+  }
+
+  // 1. query bounds per dx-group
+  CT vals[2 * kGroupMax];
+#pragma unroll
+  for (int g = 0; g < kGroupMax; ++g) {
+    if (g < p.G) {
+      CT mn = max_key<CT>(), mx = CT(0);
+      for (int j = 0; j < p.GS; ++j) {
+        CT q = key + p.off[g * p.GS + j];
+        if (valid) {
+          mn = q < mn ? q : mn;
+          mx = q > mx ? q : mx;
+        }
+      }
+      vals[2 * g] = wave_min(mn);
+      vals[2 * g + 1] = wave_max(mx);
+    }
+  }
+  // 2. all bounds at once
+  int64_t lb[2 * kGroupMax];
+  wave_lower_bounds<CT>(p.src, p.S, vals, 2 * p.G, lb);
+
+  // 3. per group: stage the window, search, z-scan, store
+  for (int g = 0; g < p.G; ++g) {
+    const int64_t lo = lb[2 * g];
+    int64_t hi = lb[2 * g + 1] + KZ;
+    if (hi > p.S) hi = p.S;
+    const int n = static_cast<int>(hi - lo);
+    const bool in_lds = (hi - lo) <= kWindowCap;
+    if (in_lds) {
+      for (int i = lane; i < n; i += 64) win[i] = p.src[lo + i];
+      __syncthreads();
+    }
+    for (int j = 0; j < p.GS; ++j) {
+      const int o = g * p.GS + j;
+      // padded lanes query the group minimum so that every index stays inside the window
+      CT c = valid ? CT(key + p.off[o]) : vals[2 * g];
+      int64_t idx = in_lds ? lo + lds_lower_bound(win, n, c) : global_lower_bound(p.src, lo, hi, c);
+      int32_t res[KZ];
+      {
+        CT v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
+        res[0] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
+#pragma unroll
+        for (int iz = 1; iz < KZ; ++iz) {
+          if (idx < p.S && v <= c) ++idx;
+          c += sz;
+          v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
+          res[iz] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
+        }
+      }
+#pragma unroll
+      for (int iz = 0; iz < KZ; ++iz) {
+        const int32_t r = valid ? res[iz] : -1;
+        const int k = o * KZ + iz;
+        if (p.os_layout) {
+          const int col = p.zmajor ? iz * p.O + o : k;
+          stage[lane * p.K + col] = r;
+        } else {
+          const int row = p.use_perm ? p.perm[k] : k;
+          p.map[row * p.Tp + t] = r;
+          if (p.tile_counts) {
+            uint64_t m = ballot(r >= 0);
+            if (lane == 0) p.tile_counts[row * p.ntiles + tile] = __builtin_popcountll(m);
+          }
+        }
+      }
+    }
+    if (in_lds) __syncthreads();
+  }
+
+  if (p.os_layout) {
+    __syncthreads();
+    int32_t *dst = p.map + tile * 64 * p.K;
+    const int total = 64 * p.K;  // multiple of 4
+    const int4 *s4 = reinterpret_cast<const int4 *>(stage);
+    int4 *d4 = reinterpret_cast<int4 *>(dst);
+    for (int i = lane; i < total / 4; i += 64) d4[i] = s4[i];
+  }
+}
+
+template <typename CT> static void make_offsets(int kx, int ky, int kz, int sx, int sy, int sz, bool full, CT *out) {
+  // offset tables of torch/cuda_sparse_convolution_mapping.cu:10-50 (xy only,
+  // z pinned to kz_min*sz) and :114-157 (full): x outer, y, z inner; packed
+  // with modular arithmetic exactly like the key arithmetic.
+  auto kmin = [](int k) { return (k % 2 == 1) ? -(k / 2) : -(k / 2) + 1; };
+  int idx = 0;
+  for (int ix = kmin(kx); ix <= kx / 2; ++ix)
+    for (int iy = kmin(ky); iy <= ky / 2; ++iy) {
+      if (full) {
+        for (int iz = kmin(kz); iz <= kz / 2; ++iz)
+          out[idx++] = static_cast<CT>(static_cast<CT>(ix * sx) * (CT(1) << Layout<CT>::XS) +
+                                       static_cast<CT>(iy * sy) * (CT(1) << Layout<CT>::YS) +
+                                       static_cast<CT>(iz * sz));
+      } else {
+        out[idx++] = static_cast<CT>(static_cast<CT>(ix * sx) * (CT(1) << Layout<CT>::XS) +
+                                     static_cast<CT>(iy * sy) * (CT(1) << Layout<CT>::YS) +
+                                     static_cast<CT>(kmin(kz) * sz));
+      }
+    }
+}
+
+template <typename CT>
+static int search_impl(const CT *src, int64_t S, const CT *tgt, int64_t T, int kx, int ky, int kz, int sx, int sy,
+                       int sz, int layout, const int32_t *row_perm, int32_t *map, int32_t *tile_counts,
+                       hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(S >= 0 && T >= 0 && S < (int64_t(1) << 31) && T < (int64_t(1) << 31),
+                    "kmap_search: sizes out of range");
+  SPIRA_HIP_REQUIRE(kx >= 1 && ky >= 1 && kz >= 1, "kmap_search: kernel size must be positive");
+  SPIRA_HIP_REQUIRE(kx <= kGroupMax, "kmap_search: kernel size along x is limited to 8");
+  SPIRA_HIP_REQUIRE(layout >= SPIRA_KMAP_OS && layout <= SPIRA_KMAP_NOZ, "kmap_search: unknown layout");
+  const int K = kx * ky * kz;
+  SPIRA_HIP_REQUIRE(K <= kOffsetsMax, "kmap_search: kernel volume is limited to 128 offsets");
+  SearchParams<CT> p{};
+  p.src = src;
+  p.tgt = tgt;
+  p.map = map;
+  p.S = S;
+  p.T = T;
+  p.Tp = round_up(T, 128);
+  p.ntiles = p.Tp / 64;
+  p.K = K;
+  p.sz = static_cast<CT>(static_cast<uint32_t>(sz));
+  int KZ = kz;
+  if (layout == SPIRA_KMAP_NOZ) {
+    make_offsets<CT>(kx, ky, kz, sx, sy, sz, true, p.off);
+    p.G = kx;
+    p.GS = ky * kz;
+    p.O = K;
+    KZ = 1;
+    p.os_layout = 1;
+    p.zmajor = 0;
+  } else {
+    SPIRA_HIP_REQUIRE(kz <= 5, "Currently Kernel Size in Z axis can only be 1..5");
+    make_offsets<CT>(kx, ky, kz, sx, sy, sz, false, p.off);
+    p.G = kx;
+    p.GS = ky;
+    p.O = kx * ky;
+    p.os_layout = layout == SPIRA_KMAP_OS;
+    p.zmajor = layout == SPIRA_KMAP_OS;
+  }
+  if (layout == SPIRA_KMAP_HYBRID) {
+    SPIRA_HIP_REQUIRE(row_perm != nullptr, "kmap_search: hybrid layout needs a row permutation");
+    for (int k = 0; k < K; ++k) {
+      SPIRA_HIP_REQUIRE(row_perm[k] >= 0 && row_perm[k] < K, "kmap_search: bad row permutation");
+      p.perm[k] = row_perm[k];
+    }
+    p.use_perm = 1;
+  }
+  p.tile_counts = p.os_layout ? nullptr : tile_counts;
+  if (p.Tp == 0) return kOk;
+  const size_t lds = kWindowCap * sizeof(CT) + (p.os_layout ? 64 * K * sizeof(int32_t) : 0);
+  dim3 grid(static_cast<unsigned>(p.ntiles)), block(64);
+  switch (KZ) {
+    case 1: hipLaunchKernelGGL((kmap_search_kernel<CT, 1>), grid, block, lds, stream, p); break;
+    case 2: hipLaunchKernelGGL((kmap_search_kernel<CT, 2>), grid, block, lds, stream, p); break;
+    case 3: hipLaunchKernelGGL((kmap_search_kernel<CT, 3>), grid, block, lds, stream, p); break;
+    case 4: hipLaunchKernelGGL((kmap_search_kernel<CT, 4>), grid, block, lds, stream, p); break;
+    case 5: hipLaunchKernelGGL((kmap_search_kernel<CT, 5>), grid, block, lds, stream, p); break;
+    default: SPIRA_HIP_REQUIRE(false, "Currently Kernel Size in Z axis can only be 1..5");
+  }
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// post-processing
+// ---------------------------------------------------------------------------
+__global__ void fill_i32_kernel(int32_t *__restrict__ p, int64_t n, int32_t v) {
+  int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    *reinterpret_cast<int4 *>(p + i) = make_int4(v, v, v, v);
+  } else {
+    for (int64_t j = i; j < n && j < i + 4; ++j) p[j] = v;
+  }
+}
+
+static int fill_i32(int32_t *p, int64_t n, int32_t v, hipStream_t s) {
+  if (n <= 0) return kOk;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(div_up(div_up(n, 4), 256)), dim3(256), 0, s, p, n, v);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+// nbsizes[r] = per-row totals; naddrs / qnaddrs exclusive scans (quantum q)
+// (query_sorted_index.cu:146-209 with quantifier_wstat.cuh:8-41).
+__global__ void row_totals_kernel(const int32_t *__restrict__ tile_counts, const int32_t *__restrict__ tile_offsets,
+                                  int R, int64_t ntiles, int q, int32_t *__restrict__ nbsizes,
+                                  int32_t *__restrict__ naddrs, int32_t *__restrict__ qnaddrs,
+                                  int32_t *__restrict__ sizes) {
+  // one block; R <= 128
+  __shared__ int32_t tot[kOffsetsMax];
+  int r = threadIdx.x;
+  if (r < R) {
+    int64_t last = (static_cast<int64_t>(r) + 1) * ntiles - 1;
+    int32_t end = tile_offsets[last] + tile_counts[last];
+    int32_t beg = tile_offsets[static_cast<int64_t>(r) * ntiles];
+    tot[r] = end - beg;
+    nbsizes[r] = end - beg;
+  }
+  __syncthreads();
+  if (r == 0) {
+    int32_t acc = 0, qacc = 0;
+    for (int i = 0; i < R; ++i) {
+      if (naddrs) naddrs[i] = acc;
+      if (qnaddrs) qnaddrs[i] = qacc;
+      acc += tot[i];
+      qacc += (tot[i] + q - 1) / q * q;
+    }
+    if (naddrs) naddrs[R] = acc;
+    if (qnaddrs) qnaddrs[R] = qacc;
+    if (sizes) {
+      sizes[0] = acc;
+      sizes[1] = qacc;
+    }
+  }
+}
+
+// one wave per (row, tile): stable compaction in (row, t) order
+__global__ __launch_bounds__(256) void emit_pairs_kernel(const int32_t *__restrict__ map, int64_t Tp, int row0,
+                                                         int R, int64_t ntiles,
+                                                         const int32_t *__restrict__ tile_offsets,
+                                                         int32_t *__restrict__ in_idx,
+                                                         int32_t *__restrict__ out_idx) {
+  const int64_t w = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  if (w >= R * ntiles) return;
+  const int lane = lane_id();
+  const int64_t r = w / ntiles, tile = w % ntiles;
+  const int64_t t = tile * 64 + lane;
+  const int32_t v = map[(row0 + r) * Tp + t];
+  const bool ok = v != -1;
+  const uint64_t m = ballot(ok);
+  if (ok) {
+    const int64_t pos = tile_offsets[w] + lane_prefix(m);
+    in_idx[pos] = v;
+    out_idx[pos] = static_cast<int32_t>(t);
+  }
+}
+
+// masks: rank of each valid entry within its row (generate_masks_from_kernel_map.cuh:10-62)
+__global__ __launch_bounds__(256) void emit_masks_kernel(const int32_t *__restrict__ map, int64_t S, int64_t T,
+                                                         int64_t Tp, int row0, int R, int Km, int half,
+                                                         int64_t ntiles, const int32_t *__restrict__ tile_offsets,
+                                                         int32_t *__restrict__ smask, int32_t *__restrict__ tmask) {
+  const int64_t w = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  if (w >= R * ntiles) return;
+  const int lane = lane_id();
+  const int64_t r = w / ntiles, tile = w % ntiles;
+  const int64_t t = tile * 64 + lane;
+  const int32_t v = map[(row0 + r) * Tp + t];
+  const bool ok = v != -1;
+  const uint64_t m = ballot(ok);
+  if (ok) {
+    const int32_t rank = tile_offsets[w] - tile_offsets[r * ntiles] + lane_prefix(m);
+    smask[r * S + v] = rank;
+    tmask[r * T + t] = rank;
+    if (half && 2 * r + 1 != Km) {
+      smask[(Km - 1 - r) * S + t] = rank;
+      tmask[(Km - 1 - r) * T + v] = rank;
+    }
+  }
+}
+
+// transposed OS map: out[s, k] = t where map[t, k] = s (convert_transposed_os.cuh:7-16)
+__global__ void convert_transposed_kernel(const int32_t *__restrict__ map, int64_t n, int K,
+                                          int32_t *__restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int32_t s = map[i];
+  if (s < 0) return;
+  out[static_cast<int64_t>(s) * K + i % K] = static_cast<int32_t>(i / K);
+}
+
+static size_t scan_temp_bytes(int64_t n) {
+  size_t b = 0;
+  (void)rocprim::exclusive_scan(nullptr, b, static_cast<const int32_t *>(nullptr), static_cast<int32_t *>(nullptr), 0,
+                          static_cast<size_t>(n), rocprim::plus<int32_t>());
+  return b;
+}
+
+}  // namespace spira_hip
+
+using namespace spira_hip;
+
+extern "C" {
+
+int spira_hip_kmap_search(const void *sources, int64_t num_sources, const void *targets, int64_t num_targets,
+                          int key_bits, int kx, int ky, int kz, int sx, int sy, int sz, int layout,
+                          const int32_t *row_perm, int32_t *kernel_map, int32_t *tile_counts, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "kmap_search: key_bits must be 32 or 64");
+  if (key_bits == 64)
+    return search_impl<uint64_t>(static_cast<const uint64_t *>(sources), num_sources,
+                                 static_cast<const uint64_t *>(targets), num_targets, kx, ky, kz, sx, sy, sz, layout,
+                                 row_perm, kernel_map, tile_counts, stream);
+  return search_impl<uint32_t>(static_cast<const uint32_t *>(sources), num_sources,
+                               static_cast<const uint32_t *>(targets), num_targets, kx, ky, kz, sx, sy, sz, layout,
+                               row_perm, kernel_map, tile_counts, stream);
+}
+
+int spira_hip_kmap_scan_workspace(int64_t num_counts, size_t *bytes) {
+  *bytes = num_counts <= 0 ? 0 : scan_temp_bytes(num_counts);
+  return kOk;
+}
+
+int spira_hip_kmap_scan(const int32_t *tile_counts, int rows, int64_t ntiles, int quantum, int32_t *tile_offsets,
+                        int32_t *nbsizes, int32_t *naddrs, int32_t *qnaddrs, int32_t *sizes, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(rows >= 0 && rows <= kOffsetsMax, "kmap_scan: rows out of range");
+  SPIRA_HIP_REQUIRE(quantum >= 1, "kmap_scan: quantum must be positive");
+  const int64_t n = static_cast<int64_t>(rows) * ntiles;
+  if (n == 0) {
+    // empty: every size is zero
+    if (naddrs) { int rc = fill_i32(naddrs, rows + 1, 0, stream); if (rc) return rc; }
+    if (qnaddrs) { int rc = fill_i32(qnaddrs, rows + 1, 0, stream); if (rc) return rc; }
+    if (nbsizes) { int rc = fill_i32(nbsizes, rows, 0, stream); if (rc) return rc; }
+    if (sizes) return fill_i32(sizes, 2, 0, stream);
+    return kOk;
+  }
+  size_t need = scan_temp_bytes(n);
+  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= need, "kmap_scan: workspace too small");
+  SPIRA_HIP_TRY(rocprim::exclusive_scan(workspace, need, tile_counts, tile_offsets, 0, static_cast<size_t>(n),
+                                        rocprim::plus<int32_t>(), stream));
+  hipLaunchKernelGGL(row_totals_kernel, dim3(1), dim3(kOffsetsMax), 0, stream, tile_counts, tile_offsets, rows,
+                     ntiles, quantum, nbsizes, naddrs, qnaddrs, sizes);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+int spira_hip_kmap_emit_pairs(const int32_t *kernel_map, int64_t aligned_targets, int row0, int rows,
+                              const int32_t *tile_offsets, int32_t *in_idx, int32_t *out_idx, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(aligned_targets % 128 == 0, "kmap_emit_pairs: aligned_targets must be a multiple of 128");
+  const int64_t ntiles = aligned_targets / 64;
+  const int64_t waves = static_cast<int64_t>(rows) * ntiles;
+  if (waves == 0) return kOk;
+  hipLaunchKernelGGL(emit_pairs_kernel, dim3(div_up(waves, 4)), dim3(256), 0, stream, kernel_map, aligned_targets,
+                     row0, rows, ntiles, tile_offsets, in_idx, out_idx);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+int spira_hip_kmap_emit_masks(const int32_t *kernel_map, int64_t num_sources, int64_t num_targets,
+                              int64_t aligned_targets, int row0, int rows, int mask_rows, int half,
+                              const int32_t *tile_offsets, int32_t *source_masks, int32_t *target_masks,
+                              hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(aligned_targets % 128 == 0, "kmap_emit_masks: aligned_targets must be a multiple of 128");
+  SPIRA_HIP_REQUIRE(!half || num_sources == num_targets, "kmap_emit_masks: half masks need S == T");
+  SPIRA_HIP_REQUIRE(rows <= mask_rows, "kmap_emit_masks: more compacted rows than mask rows");
+  int rc = fill_i32(source_masks, static_cast<int64_t>(mask_rows) * num_sources, -1, stream);
+  if (rc) return rc;
+  rc = fill_i32(target_masks, static_cast<int64_t>(mask_rows) * num_targets, -1, stream);
+  if (rc) return rc;
+  const int64_t ntiles = aligned_targets / 64;
+  const int64_t waves = static_cast<int64_t>(rows) * ntiles;
+  if (waves == 0) return kOk;
+  hipLaunchKernelGGL(emit_masks_kernel, dim3(div_up(waves, 4)), dim3(256), 0, stream, kernel_map, num_sources,
+                     num_targets, aligned_targets, row0, rows, mask_rows, half, ntiles, tile_offsets, source_masks,
+                     target_masks);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_targets, int num_offsets,
+                                    int64_t aligned_sources, int32_t *out, hipStream_t stream) {
+  int rc = fill_i32(out, aligned_sources * num_offsets, -1, stream);
+  if (rc) return rc;
+  const int64_t n = aligned_targets * num_offsets;
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(convert_transposed_kernel, dim3(div_up(n, 256)), dim3(256), 0, stream, out_in_map, n,
+                     num_offsets, out);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t stream) {
+  return fill_i32(ptr, n, value, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,352 @@
+// Feature entry points of `_C`: the output-stationary, weight-stationary
+// (fused and gather-GEMM-scatter) and hybrid dataflows, the selector's timing
+// probes and the buffer / error utilities.
+// Reference: torch/cuda_sparse_convolution_forward.cu:7-507,
+// torch/cuda_memory_buffer.cu:7-16.
+#include "host_common.h"
+
+#include <c10/hip/HIPCachingAllocator.h>
+
+#include <algorithm>
+#include <cmath>
+
+namespace spira_host {
+
+static int dtype_of(const torch::Tensor &t) {
+  if (t.scalar_type() == torch::kHalf) return SPIRA_F16;
+  if (t.scalar_type() == torch::kFloat) return SPIRA_F32;
+  fail("Cannot find implementation for feature dtype ", t.scalar_type());
+}
+
+static torch::Tensor conv_workspace(int K, int cin, int cout, int dtype, const torch::Device &dev, size_t *bytes) {
+  check_rc(spira_hip_conv_workspace(K, cin, cout, dtype, bytes), "conv");
+  return workspace(*bytes, dev);
+}
+
+static void check_features(const torch::Tensor &X, const torch::Tensor &W) {
+  SPIRA_CHECK_ARG(X.dim() == 2, "sources must be [N, C_in]");
+  SPIRA_CHECK_ARG(W.dim() == 3, "weights must be [K, C_in, C_out]");
+  require_device(X, "sources");
+  require_device(W, "weights");
+  SPIRA_CHECK_ARG(X.scalar_type() == W.scalar_type(), "sources and weights must share a dtype");
+  SPIRA_CHECK_ARG(X.size(1) == W.size(1), "sources have ", X.size(1), " channels, weights expect ", W.size(1));
+  dtype_of(X);
+}
+
+// Output-stationary pass over weights W[0:K] into `out` (mode: SPIRA_OUT_*).
+// A missing map is the identity map (a submanifold layer whose only dense
+// offset is the centre: sparse_convolution.cu:1368-1380).
+static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
+                   int K, void *out, int mode) {
+  const auto dev = X.device();
+  const int dtype = dtype_of(X);
+  torch::Tensor ident;
+  const int32_t *mp = nullptr;
+  if (map) {
+    SPIRA_CHECK_ARG(map->dim() == 2 && map->scalar_type() == torch::kInt32, "out_in_map must be 2-D int32");
+    require_device(*map, "out_in_map");
+    SPIRA_CHECK_ARG(map->size(0) >= T, "out_in_map has fewer rows than targets");
+    SPIRA_CHECK_ARG(map->size(1) == K, "out_in_map has ", map->size(1), " columns, expected ", K);
+    mp = map->data_ptr<int32_t>();
+  } else {
+    SPIRA_CHECK_ARG(S == T, "the identity dense part needs as many sources as targets");
+    ident = torch::arange(T, torch::TensorOptions(dev).dtype(torch::kInt32)).view({T, 1});
+    mp = ident.data_ptr<int32_t>();
+  }
+  size_t wsb = 0;
+  auto ws = conv_workspace(K, W.size(1), W.size(2), dtype, dev, &wsb);
+  check_rc(spira_hip_conv_os(T, K, mp, X.data_ptr(), S, W.size(1), W.data_ptr(), W.size(2), dtype, out, mode,
+                             ws.data_ptr(), wsb, current_stream()),
+           "sparse_convolution_forward_os");
+}
+
+// (reference: CUDASparseConvolutionForward_OS, :448-496)
+torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const torch::Tensor &X,
+                         const torch::Tensor &W) {
+  check_features(X, W);
+  SPIRA_CHECK_ARG(out_in_map.dim() == 2, "out_in_map must be 2-D");
+  SPIRA_CHECK_ARG(W.size(0) == out_in_map.size(1), "weights have ", W.size(0), " offsets, map has ",
+                  out_in_map.size(1));
+  auto Y = torch::empty({T, W.size(2)}, X.options());
+  run_os(&out_in_map, S, T, X, W, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE);
+  return Y;
+}
+
+// Host sizes of the per-offset lists, the mirrored half filled in when only
+// the first half was compacted (sparse_convolution.cu:1020-1037, 1150-1157).
+static std::vector<int32_t> host_sizes(const torch::Tensor &nbsizes, int Km, bool half) {
+  auto h = nbsizes.to(torch::kCPU).to(torch::kInt32).contiguous();
+  const int32_t *p = h.data_ptr<int32_t>();
+  std::vector<int32_t> s(Km, 0);
+  const int nh = half ? (Km + 1) / 2 : Km;
+  SPIRA_CHECK_ARG(h.numel() >= nh, "kernel_map_sizes has ", h.numel(), " entries, expected ", nh);
+  for (int i = 0; i < nh; ++i) s[i] = p[i];
+  for (int i = nh; i < Km; ++i) s[i] = s[Km - 1 - i];
+  return s;
+}
+
+// Greedy bucketing of adjacent offsets while the padding redundancy stays
+// within `threshold` (nullopt: merge all, negative: never merge), returning
+// each offset's first row in the padded buffer (Km + 1 entries)
+// (reference: GeneratePaddingBuckets / ComputeCumsumKernelPaddedSizes,
+// cuda/functions/sparse_convolution.cu:488-515, 744-764).
+static std::vector<int64_t> padded_offsets(const std::vector<int32_t> &sizes, const std::optional<double> &threshold) {
+  const int K = static_cast<int>(sizes.size());
+  std::vector<int> bounds{0};
+  for (int i = 0; i < K; ++i) {
+    const int j = i;
+    uint64_t actual = sizes[i], summit = sizes[i];
+    while (i + 1 < K) {
+      actual += sizes[i + 1];
+      summit = std::max<uint64_t>(summit, sizes[i + 1]);
+      const uint64_t padded = summit * static_cast<uint64_t>((i + 1) - j + 1);
+      const double red = static_cast<double>(padded - actual) / static_cast<double>(actual);
+      if (threshold.has_value() && (*threshold < 0 || red > *threshold)) break;
+      ++i;
+    }
+    bounds.push_back(i + 1);
+  }
+  std::vector<int64_t> off(K + 1, 0);
+  for (size_t b = 0; b + 1 < bounds.size(); ++b) {
+    int64_t summit = 0;
+    for (int k = bounds[b]; k < bounds[b + 1]; ++k) summit = std::max<int64_t>(summit, sizes[k]);
+    for (int k = bounds[b]; k < bounds[b + 1]; ++k) off[k + 1] = off[k] + summit;
+  }
+  return off;
+}
+
+// A planned gather -> GEMM -> scatter over Km offsets.
+struct GsPlan {
+  int Km = 0;
+  int64_t S = 0, T = 0;
+  std::vector<int32_t> sizes;
+  std::vector<int64_t> off;
+  const int32_t *smask = nullptr, *tmask = nullptr;
+  torch::Tensor bin, bout;
+};
+
+static GsPlan plan_gs(int64_t S, int64_t T, const torch::Tensor &source_masks, const torch::Tensor &target_masks,
+                      const torch::Tensor &nbsizes, bool half, const std::optional<double> &threshold, int cin,
+                      int cout, const torch::TensorOptions &fopt) {
+  SPIRA_CHECK_ARG(source_masks.dim() == 2 && target_masks.dim() == 2, "masks must be 2-D");
+  SPIRA_CHECK_ARG(source_masks.scalar_type() == torch::kInt32 && target_masks.scalar_type() == torch::kInt32,
+                  "masks must be int32");
+  require_device(source_masks, "source_masks");
+  require_device(target_masks, "target_masks");
+  SPIRA_CHECK_ARG(source_masks.size(0) == target_masks.size(0), "source and target masks disagree on offsets");
+  SPIRA_CHECK_ARG(source_masks.size(1) == S && target_masks.size(1) == T, "masks do not match S / T");
+  GsPlan p;
+  p.Km = static_cast<int>(target_masks.size(0));
+  p.S = S;
+  p.T = T;
+  p.sizes = host_sizes(nbsizes, p.Km, half);
+  p.off = padded_offsets(p.sizes, threshold);
+  p.smask = source_masks.data_ptr<int32_t>();
+  p.tmask = target_masks.data_ptr<int32_t>();
+  const int64_t total = std::max<int64_t>(p.off[p.Km], 1);
+  p.bin = torch::empty({total, cin}, fopt);
+  p.bout = torch::empty({total, cout}, fopt.dtype(torch::kFloat));
+  return p;
+}
+
+static void gs_gather(GsPlan &p, const torch::Tensor &X, hipStream_t s) {
+  check_rc(spira_hip_ws_gather(p.S, X.size(1), p.Km, dtype_of(X), X.data_ptr(), p.smask, p.off.data(),
+                               p.bin.data_ptr(), s),
+           "gather");
+}
+
+static void gs_gemm(GsPlan &p, const torch::Tensor &W, int woff, hipStream_t s) {
+  const int dtype = dtype_of(W);
+  const int cin = W.size(1), cout = W.size(2);
+  size_t wsb = 0;
+  auto ws = conv_workspace(p.Km, cin, cout, dtype, W.device(), &wsb);
+  const int64_t wstep = static_cast<int64_t>(cin) * cout * W.element_size();
+  const char *wbase = static_cast<const char *>(W.data_ptr()) + woff * wstep;
+  check_rc(spira_hip_ws_gemm(p.Km, p.sizes.data(), p.off.data(), cin, cout, dtype, p.bin.data_ptr(), wbase,
+                             p.bout.data_ptr<float>(), ws.data_ptr(), wsb, s),
+           "gemm");
+}
+
+static void gs_scatter(GsPlan &p, int cout, int dtype, const float *base, void *Y, hipStream_t s) {
+  check_rc(spira_hip_ws_scatter(p.T, cout, p.Km, dtype, p.tmask, p.off.data(), p.bout.data_ptr<float>(), base, Y, s),
+           "scatter");
+}
+
+// (reference: CUDASparseConvolutionForward_WS, :130-184)
+torch::Tensor forward_ws(int64_t S, int64_t T, int64_t gather_tile, int64_t scatter_tile, int64_t parallel,
+                         const std::optional<double> &threshold, const torch::Tensor &X, const torch::Tensor &W,
+                         const torch::Tensor &source_masks, const torch::Tensor &target_masks,
+                         const torch::Tensor &nbsizes) {
+  (void)gather_tile;
+  (void)scatter_tile;
+  (void)parallel;
+  check_features(X, W);
+  SPIRA_CHECK_ARG(W.size(0) == target_masks.size(0), "weights have ", W.size(0), " offsets, masks have ",
+                  target_masks.size(0));
+  const int Km = static_cast<int>(target_masks.size(0));
+  const bool half = (Km % 2 == 1) && S == T;
+  auto p = plan_gs(S, T, source_masks, target_masks, nbsizes, half, threshold, W.size(1), W.size(2), X.options());
+  auto Y = torch::empty({T, W.size(2)}, X.options());
+  auto s = current_stream();
+  gs_gather(p, X, s);
+  gs_gemm(p, W, 0, s);
+  gs_scatter(p, W.size(2), dtype_of(X), nullptr, Y.data_ptr(), s);
+  return Y;
+}
+
+// fused pass + fp32 -> storage dtype
+static void ws_fused_into(int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
+                          const torch::Tensor &naddrs, const torch::Tensor &qnaddrs, const torch::Tensor &nbmaps,
+                          int64_t mapsize, int64_t qmapsize, bool transpose, int woff, int mirror_rows,
+                          float *acc) {
+  SPIRA_CHECK_ARG(nbmaps.dim() == 2 && nbmaps.size(0) == 2, "nbmaps must be [2, P]");
+  SPIRA_CHECK_ARG(nbmaps.size(1) == mapsize, "nbmaps holds ", nbmaps.size(1), " pairs, mapsize is ", mapsize);
+  require_device(nbmaps, "nbmaps");
+  require_device(naddrs, "naddrs");
+  require_device(qnaddrs, "qnaddrs");
+  const int rows = static_cast<int>(naddrs.size(0) - 1);
+  const int32_t *base = nbmaps.data_ptr<int32_t>();
+  const int32_t *imap = transpose ? base + mapsize : base;
+  const int32_t *omap = transpose ? base : base + mapsize;
+  const int dtype = dtype_of(X);
+  size_t wsb = 0;
+  auto ws = conv_workspace(W.size(0), W.size(1), W.size(2), dtype, X.device(), &wsb);
+  check_rc(spira_hip_conv_ws_fused(S, T, imap, omap, rows, naddrs.data_ptr<int32_t>(), qnaddrs.data_ptr<int32_t>(),
+                                   mapsize, qmapsize, woff, mirror_rows, X.data_ptr(), W.size(1), W.data_ptr(),
+                                   W.size(0), W.size(2), dtype, acc, ws.data_ptr(), wsb, current_stream()),
+           "sparse_convolution_forward_ws_merged");
+}
+
+static torch::Tensor finish_acc(const torch::Tensor &acc, const torch::Tensor &X) {
+  if (X.scalar_type() == torch::kFloat) return acc;
+  auto Y = torch::empty(acc.sizes(), X.options());
+  check_rc(spira_hip_cast_f32(acc.data_ptr<float>(), acc.numel(), dtype_of(X), Y.data_ptr(), current_stream()),
+           "cast");
+  return Y;
+}
+
+// (reference: CUDASparseConvolutionForward_WS_Merged, :186-250)
+torch::Tensor forward_ws_merged(int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
+                                const torch::Tensor &naddrs, const torch::Tensor &qnaddrs, const torch::Tensor &nbmaps,
+                                int64_t mapsize, int64_t qmapsize, bool transpose) {
+  check_features(X, W);
+  const int K = static_cast<int>(W.size(0));
+  // mirrored pass for submanifold maps with an odd kernel volume
+  // (sparse_convolution.cu:1287-1293)
+  const int mirror = (S == T && K % 2 == 1) ? K : 0;
+  auto acc = torch::zeros({T, W.size(2)}, X.options().dtype(torch::kFloat));
+  ws_fused_into(S, T, X, W, naddrs, qnaddrs, nbmaps, mapsize, qmapsize, transpose, 0, mirror, acc.data_ptr<float>());
+  return finish_acc(acc, X);
+}
+
+// (reference: CUDASparseConvolutionForward_HS, :254-342)
+torch::Tensor forward_hs(int64_t S, int64_t T, int64_t gather_tile, int64_t scatter_tile, int64_t parallel,
+                         const std::optional<double> &threshold, const torch::Tensor &X, const torch::Tensor &W,
+                         const torch::Tensor &source_masks, const torch::Tensor &target_masks,
+                         const torch::Tensor &nbsizes, const std::optional<torch::Tensor> &out_in_map) {
+  (void)gather_tile;
+  (void)scatter_tile;
+  (void)parallel;
+  check_features(X, W);
+  const int Kws = static_cast<int>(target_masks.size(0));
+  const int Kos = out_in_map.has_value() ? static_cast<int>(out_in_map->size(1)) : 1;
+  SPIRA_CHECK_ARG(W.size(0) == Kws + Kos, "weights have ", W.size(0), " offsets, expected ", Kws + Kos);
+  auto acc = torch::empty({T, W.size(2)}, X.options().dtype(torch::kFloat));
+  run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W.narrow(0, 0, Kos).contiguous(), Kos,
+         acc.data_ptr<float>(), SPIRA_OUT_STORE_F32);
+  auto p = plan_gs(S, T, source_masks, target_masks, nbsizes, true, threshold, W.size(1), W.size(2), X.options());
+  auto Y = torch::empty({T, W.size(2)}, X.options());
+  auto s = current_stream();
+  gs_gather(p, X, s);
+  gs_gemm(p, W, Kos, s);
+  gs_scatter(p, W.size(2), dtype_of(X), acc.data_ptr<float>(), Y.data_ptr(), s);
+  return Y;
+}
+
+// (reference: CUDASparseConvolutionForward_HS_Merged, :346-443)
+torch::Tensor forward_hs_merged(int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
+                                const torch::Tensor &naddrs, const torch::Tensor &qnaddrs, const torch::Tensor &nbmaps,
+                                const std::optional<torch::Tensor> &out_in_map, int64_t mapsize, int64_t qmapsize,
+                                bool transpose) {
+  check_features(X, W);
+  const int Kws = static_cast<int>((naddrs.size(0) - 1) * 2);
+  const int Kos = out_in_map.has_value() ? static_cast<int>(out_in_map->size(1)) : 1;
+  SPIRA_CHECK_ARG(W.size(0) == Kws + Kos, "weights have ", W.size(0), " offsets, expected ", Kws + Kos);
+  auto acc = torch::empty({T, W.size(2)}, X.options().dtype(torch::kFloat));
+  run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W.narrow(0, 0, Kos).contiguous(), Kos,
+         acc.data_ptr<float>(), SPIRA_OUT_STORE_F32);
+  ws_fused_into(S, T, X, W, naddrs, qnaddrs, nbmaps, mapsize, qmapsize, transpose, Kos, Kws, acc.data_ptr<float>());
+  return finish_acc(acc, X);
+}
+
+// ---- selector probes: time one phase of the gather-GEMM-scatter path ----
+
+enum class Phase { kGather, kGemm, kScatter };
+
+static float time_phase(Phase ph, const std::optional<double> &threshold, bool is_hybrid, const torch::Tensor &W,
+                        const torch::Tensor &source_masks, const torch::Tensor &target_masks,
+                        const torch::Tensor &nbsizes) {
+  SPIRA_CHECK_ARG(W.dim() == 3, "weights must be [K, C_in, C_out]");
+  require_device(W, "weights");
+  const int64_t S = source_masks.size(1), T = target_masks.size(1);
+  const int Km = static_cast<int>(target_masks.size(0));
+  const bool half = is_hybrid || (Km % 2 == 1 && S == T);
+  auto p = plan_gs(S, T, source_masks, target_masks, nbsizes, half, threshold, W.size(1), W.size(2), W.options());
+  auto X = torch::zeros({S, W.size(1)}, W.options());
+  auto Y = torch::empty({T, W.size(2)}, W.options());
+  auto s = current_stream();
+  // the weights probed are the last Km offsets (the WS part of a hybrid map)
+  const int woff = static_cast<int>(W.size(0)) - Km;
+  SPIRA_CHECK_ARG(woff >= 0, "weights have fewer offsets than the masks");
+  hipEvent_t a, b;
+  SPIRA_CHECK_ARG(hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess, "event creation failed");
+  if (ph != Phase::kGather) gs_gather(p, X, s);
+  if (ph == Phase::kScatter) gs_gemm(p, W, woff, s);
+  SPIRA_CHECK_ARG(hipEventRecord(a, s) == hipSuccess, "event record failed");
+  if (ph == Phase::kGather) gs_gather(p, X, s);
+  else if (ph == Phase::kGemm) gs_gemm(p, W, woff, s);
+  else gs_scatter(p, W.size(2), dtype_of(W), nullptr, Y.data_ptr(), s);
+  SPIRA_CHECK_ARG(hipEventRecord(b, s) == hipSuccess, "event record failed");
+  SPIRA_CHECK_ARG(hipEventSynchronize(b) == hipSuccess, "event synchronisation failed");
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, a, b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return ms;
+}
+
+// (reference: CUDATimeGEMM / CUDATimeGather / CUDATimeScatter, :7-128)
+float time_gemm(int64_t parallel, const std::optional<double> &threshold, bool is_hybrid, const torch::Tensor &W,
+                const torch::Tensor &sm, const torch::Tensor &tm, const torch::Tensor &nb) {
+  (void)parallel;
+  return time_phase(Phase::kGemm, threshold, is_hybrid, W, sm, tm, nb);
+}
+float time_gather(int64_t tile, const std::optional<double> &threshold, bool is_hybrid, const torch::Tensor &W,
+                  const torch::Tensor &sm, const torch::Tensor &tm, const torch::Tensor &nb) {
+  (void)tile;
+  return time_phase(Phase::kGather, threshold, is_hybrid, W, sm, tm, nb);
+}
+float time_scatter(int64_t tile, const std::optional<double> &threshold, bool is_hybrid, const torch::Tensor &W,
+                   const torch::Tensor &sm, const torch::Tensor &tm, const torch::Tensor &nb) {
+  (void)tile;
+  return time_phase(Phase::kScatter, threshold, is_hybrid, W, sm, tm, nb);
+}
+
+// (reference: cuda_free_buffers / cuda_reset_error, torch/cuda_memory_buffer.cu:7-16)
+void free_buffers() { c10::hip::HIPCachingAllocator::emptyCache(); }
+void reset_error() { (void)hipGetLastError(); }
+
+void register_conv(pybind11::module_ &m) {
+  m.def("cuda_sparse_convolution_forward_os", &forward_os);
+  m.def("cuda_sparse_convolution_forward_ws", &forward_ws);
+  m.def("cuda_sparse_convolution_forward_ws_merged", &forward_ws_merged);
+  m.def("cuda_sparse_convolution_forward_hs", &forward_hs);
+  m.def("cuda_sparse_convolution_forward_hs_merged", &forward_hs_merged);
+  m.def("cuda_time_gemm", &time_gemm);
+  m.def("cuda_time_gather", &time_gather);
+  m.def("cuda_time_scatter", &time_scatter);
+  m.def("cuda_free_buffers", &free_buffers);
+  m.def("cuda_reset_error", &reset_error);
+}
+
+}  // namespace spira_host

@@ -1,0 +1,112 @@
+// Coordinate entry points of `_C`: flatten + sort, unflatten, downsample and
+// the multi-stream downsample of every target stride.
+// Reference: torch/cuda_arg_sort_coordinates.cu:11-208.
+#include "host_common.h"
+
+namespace spira_host {
+
+// (coords [N,3] int32, is_double) -> (sorted keys [N] int64|int32, perm [N] int32)
+// (reference: CUDAFlattenSort, torch/cuda_arg_sort_coordinates.cu:11-39)
+std::pair<torch::Tensor, torch::Tensor> flatten_sort(const torch::Tensor &coordinates, bool is_double) {
+  SPIRA_CHECK_ARG(coordinates.dim() == 2 && coordinates.size(1) == 3, "coordinates must be [N, 3]");
+  SPIRA_CHECK_ARG(coordinates.scalar_type() == torch::kInt32, "coordinates must be int32");
+  require_device(coordinates, "coordinates");
+  const auto dev = coordinates.device();
+  const int64_t n = coordinates.size(0);
+  const int bits = is_double ? 64 : 32;
+  auto keys = torch::empty({n}, torch::TensorOptions(dev).dtype(is_double ? torch::kInt64 : torch::kInt32));
+  auto perm = empty_i32({n}, dev);
+  size_t ws_bytes = 0;
+  check_rc(spira_hip_flatten_sort_workspace(n, bits, &ws_bytes), "flatten_sort");
+  auto ws = workspace(ws_bytes, dev);
+  check_rc(spira_hip_flatten_sort(coordinates.data_ptr<int32_t>(), n, bits, keys.data_ptr(),
+                                  perm.data_ptr<int32_t>(), ws.data_ptr(), ws_bytes, current_stream()),
+           "flatten_sort");
+  return {keys, perm};
+}
+
+// keys [N] -> coords [N,3] int32 (reference: CUDAUnFlatten, :41-65)
+torch::Tensor unflatten(const torch::Tensor &keys) {
+  SPIRA_CHECK_ARG(keys.dim() == 1, "keys must be 1-D");
+  require_device(keys, "keys");
+  const int bits = key_bits_of(keys);
+  auto out = empty_i32({keys.size(0), 3}, keys.device());
+  check_rc(spira_hip_unpack(keys.data_ptr(), keys.size(0), bits, out.data_ptr<int32_t>(), current_stream()),
+           "unflatten");
+  return out;
+}
+
+static void downsample_into(const torch::Tensor &keys, int sx, int sy, int sz, torch::Tensor &out,
+                            uint32_t *d_count, hipStream_t stream) {
+  const int bits = key_bits_of(keys);
+  const int64_t n = keys.size(0);
+  size_t ws_bytes = 0;
+  check_rc(spira_hip_downsample_workspace(n, bits, &ws_bytes), "downsample");
+  auto ws = workspace(ws_bytes, keys.device());
+  check_rc(spira_hip_downsample(keys.data_ptr(), n, bits, sx, sy, sz, out.data_ptr(), d_count, ws.data_ptr(),
+                                ws_bytes, stream),
+           "downsample");
+}
+
+// (keys [N], sx, sy, sz) -> sorted unique downsampled keys [N']
+// (reference: CUDADownsample, :68-105; blocking read of N' like the reference's)
+torch::Tensor downsample(const torch::Tensor &keys, int sx, int sy, int sz) {
+  SPIRA_CHECK_ARG(keys.dim() == 1, "coordinates should be already flattened");
+  require_device(keys, "keys");
+  key_bits_of(keys);
+  auto out = torch::empty_like(keys);
+  auto count = torch::zeros({1}, torch::TensorOptions(keys.device()).dtype(torch::kInt32));
+  downsample_into(keys, sx, sy, sz, out, reinterpret_cast<uint32_t *>(count.data_ptr<int32_t>()),
+                  current_stream());
+  const int64_t nu = count.cpu().item<int32_t>();
+  return out.slice(0, 0, nu);
+}
+
+// One downsample per target stride, each on its own pool stream, one host
+// read of all counts at the end (reference: CUDAStreamedOutputGenerate, :107-200).
+std::vector<torch::Tensor> streamed_output_generate(const torch::Tensor &keys, const std::vector<Int3> &strides) {
+  SPIRA_CHECK_ARG(keys.dim() == 1, "coordinates should be already flattened");
+  require_device(keys, "keys");
+  key_bits_of(keys);
+  const auto dev = keys.device();
+  const size_t B = strides.size();
+  auto counts = torch::zeros({static_cast<int64_t>(std::max<size_t>(B, 1))},
+                             torch::TensorOptions(dev).dtype(torch::kInt32));
+  std::vector<torch::Tensor> outs;
+  // outputs and workspaces are allocated on the current stream before the
+  // fan-out; the current stream waits for every side stream afterwards
+  std::vector<torch::Tensor> wss;
+  std::vector<size_t> ws_sizes;
+  for (size_t i = 0; i < B; ++i) {
+    outs.push_back(torch::empty_like(keys));
+    size_t b = 0;
+    check_rc(spira_hip_downsample_workspace(keys.size(0), key_bits_of(keys), &b), "downsample");
+    ws_sizes.push_back(b);
+    wss.push_back(workspace(b, dev));
+  }
+  {
+    StreamFan fan(dev, B);
+    for (size_t i = 0; i < B; ++i) {
+      auto [sx, sy, sz] = strides[i];
+      check_rc(spira_hip_downsample(keys.data_ptr(), keys.size(0), key_bits_of(keys), sx, sy, sz,
+                                    outs[i].data_ptr(),
+                                    reinterpret_cast<uint32_t *>(counts.data_ptr<int32_t>() + i),
+                                    wss[i].data_ptr(), ws_sizes[i], fan[i]),
+               "streamed_output_generate");
+    }
+    fan.join();
+  }
+  auto h = counts.cpu();
+  std::vector<torch::Tensor> res;
+  for (size_t i = 0; i < B; ++i) res.push_back(outs[i].slice(0, 0, h.data_ptr<int32_t>()[i]));
+  return res;
+}
+
+void register_coords(pybind11::module_ &m) {
+  m.def("cuda_flatten_sort", &flatten_sort);
+  m.def("cuda_unflatten", &unflatten);
+  m.def("cuda_downsample", &downsample);
+  m.def("cuda_streamed_output_generate", &streamed_output_generate);
+}
+
+}  // namespace spira_host

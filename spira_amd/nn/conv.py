@@ -1,0 +1,244 @@
+"""Sparse convolution layer and the kernel-map cache
+(reference: source/spira/nn/conv.py:17-419).
+
+Dataflow numbering (``_tunable_config['map_dataflow']``):
+  0      output-stationary implicit GEMM (map [Tp, K], z-major weight rows)
+  1      fused weight-stationary over compacted pairs (canonical weight rows)
+  2      gather -> GEMM -> scatter over masks (canonical weight rows)
+  3..8   hybrid: offsets with L1 < (d-1)//2 output-stationary, the rest
+         weight-stationary (odd: fused, even: gather-scatter); weight rows
+         ordered dense-first
+``force_os`` runs a weight-stationary map output-stationary by transposing
+it (canonical weight rows).  Transposed layers reuse the map of the matching
+downsampling layer with sources and targets swapped.
+"""
+from __future__ import annotations
+
+import contextlib
+import operator
+from typing import Any, Dict, List, Optional, Tuple, Union
+
+import numpy as np
+import torch
+from torch.nn import Module
+
+from ..tensors import SparseTensor
+from ..utils.helpers import as_tuple
+from ..utils.typing import ScalarOrTuple
+from . import functional as F
+
+__all__ = ["SparseConv", "KernelMapCache"]
+
+
+class KernelMapCache:
+    """Coordinates per tensor stride and kernel maps per
+    ``(source stride, target stride, kernel size)``."""
+
+    def __init__(self):
+        self._kernel_maps_cache: Dict[tuple, list] = {}
+        self._coordinates_cache: Dict[tuple, torch.Tensor] = {}
+
+    def reset(self) -> None:
+        self._coordinates_cache.clear()
+        self._kernel_maps_cache.clear()
+
+    def get_target_coordinates(self, source_coordinates: torch.Tensor, source_stride: ScalarOrTuple[int],
+                               target_stride: ScalarOrTuple[int], transposed: bool = False) -> torch.Tensor:
+        source_stride = as_tuple(source_stride, size=3, name="source_stride")
+        target_stride = as_tuple(target_stride, size=3, name="target_stride")
+        self._coordinates_cache.setdefault(source_stride, source_coordinates)
+        if target_stride in self._coordinates_cache:
+            return self._coordinates_cache[target_stride]
+        if transposed:
+            raise RuntimeError("Layer must transpose=True must have its corresponding "
+                               "non-transposed layer before its execution")
+        target = F.downsample(source_coordinates, target_stride)
+        self._coordinates_cache[target_stride] = target
+        return target
+
+    def get_kernel_map(self, source_coordinates: torch.Tensor, source_stride: ScalarOrTuple[int],
+                       target_coordinates: torch.Tensor, target_stride: ScalarOrTuple[int],
+                       kernel_size: ScalarOrTuple[int], map_dataflow: int, force_os: bool = False,
+                       transposed: bool = False):
+        source_stride = as_tuple(source_stride, size=3, name="source_stride")
+        target_stride = as_tuple(target_stride, size=3, name="target_stride")
+        kernel_size = as_tuple(kernel_size, size=3, name="kernel_size")
+        key = ((target_stride, source_stride) if transposed else (source_stride, target_stride)) + (kernel_size,)
+
+        entry = self._kernel_maps_cache.get(key)
+        if entry is not None:
+            # entry = [transposed-to-[Tp, K] flag, S, T, map, ...]
+            if force_os and not entry[0]:
+                entry[3] = entry[3].T.contiguous()
+                entry[0] = True
+            if (map_dataflow == 0 or force_os) and transposed:
+                out = list(entry[1:])
+                out[2] = F.convert_transposed_os(entry[3], entry[1])
+                return out
+            return entry[1:]
+
+        if transposed:
+            raise RuntimeError("Layer must transpose=True must have its corresponding "
+                               "non-transposed layer before its execution")
+        kmap = F.build_kmap(source_coordinates, target_coordinates, kernel_size, source_stride, map_dataflow)
+        entry = [False, *kmap]
+        if force_os:
+            entry[3] = entry[3].T.contiguous()
+            entry[0] = True
+        self._kernel_maps_cache[key] = entry
+        return entry[1:]
+
+    def add_all_kernel_maps(self, source_coordinates: torch.Tensor, kernel_sizes: List[ScalarOrTuple[int]],
+                            source_strides: List[ScalarOrTuple[int]], target_strides: List[ScalarOrTuple[int]],
+                            init_stride: Union[int, Tuple[int, ...]], dataflow: List[int]) -> "KernelMapCache":
+        """Network-wide precompute: all downsampled coordinate sets, then every
+        layer map concurrently (map i: sources voxels[i//2], targets
+        voxels[(i+1)//2])."""
+        outputs = F.streamed_output_generate(source_coordinates, target_strides)
+        voxels = [source_coordinates] + list(outputs)
+        s_stride = as_tuple(init_stride, size=3)
+        self._coordinates_cache[s_stride] = voxels[0]
+        for i, ts in enumerate(target_strides):
+            self._coordinates_cache[as_tuple(ts, size=3)] = voxels[i + 1]
+        kmaps = F.build_kmap_streamed(voxels, kernel_sizes, list(source_strides)[:-1], dataflow)
+        for i in range(len(kernel_sizes)):
+            t_stride = as_tuple(source_strides[i + 1], size=3)
+            self._kernel_maps_cache[(s_stride, t_stride, as_tuple(kernel_sizes[i], size=3))] = [False, *kmaps[i]]
+            s_stride = t_stride
+        return self
+
+
+class SparseConv(Module):
+    __AVAILABLE_THRESHOLD__ = [-1, *list(np.linspace(0, 2, num=50)), None]
+    __NUM_TUNING_ROUNDS__ = 5
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: ScalarOrTuple[int],
+                 stride: ScalarOrTuple[int] = 1, bias: bool = False, transposed: bool = False):
+        super().__init__()
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_size = as_tuple(kernel_size, size=3, name="kernel_size")
+        self.stride = as_tuple(stride, size=3, name="stride")
+        self.transposed = transposed
+        volume = int(np.prod(self.kernel_size))
+        self.kernel = torch.nn.Parameter(torch.empty(volume, in_channels, out_channels))
+        if bias:
+            self.bias = torch.nn.Parameter(torch.empty(out_channels))
+        else:
+            self.register_parameter("bias", None)
+        self.reset_parameters()
+        self._kernel_map_cache: Optional[KernelMapCache] = None
+        self._tunable_config: Dict[str, Any] = {
+            "threshold": -1,
+            "gather_tile_size": min(in_channels, 16),
+            "scatter_tile_size": min(out_channels, 16),
+            "map_dataflow": 2,
+            "force_os": False,
+        }
+        self._tuning_data = None
+
+    @property
+    def tunable_config(self) -> Dict[str, Any]:
+        return self._tunable_config
+
+    def reset_parameters(self) -> None:
+        fan = self.out_channels if self.transposed else self.in_channels
+        bound = 1.0 / np.sqrt(fan * len(self.kernel))
+        self.kernel.data.uniform_(-bound, bound)
+        if self.bias is not None:
+            self.bias.data.uniform_(-bound, bound)
+
+    def set_kernel_map_cache(self, cache: KernelMapCache) -> None:
+        self._kernel_map_cache = cache
+
+    @property
+    def is_trivial(self) -> bool:
+        return all(x == 1 for x in self.stride) and all(x == 1 for x in self.kernel_size)
+
+    @contextlib.contextmanager
+    def tune_gs(self, free_buffers: bool = True):
+        """Record (masks, sizes) of gather-scatter runs while inside, then sweep
+        the bucket threshold and the gather / scatter tile sizes by timing
+        (reference conv.py:217-307)."""
+        try:
+            self._tuning_data = []
+            if free_buffers:
+                F.cuda_free_buffers()
+            yield
+            if free_buffers:
+                F.cuda_free_buffers()
+            if self.is_trivial or not self._tuning_data:
+                return
+            best = None
+            for thr in self.__AVAILABLE_THRESHOLD__:
+                try:
+                    t = [F.cuda_time_gemm(threshold=thr, weights=self.kernel, source_masks=sm, target_masks=tm,
+                                          kernel_map_sizes=nb)
+                         for _ in range(self.__NUM_TUNING_ROUNDS__) for sm, tm, nb in self._tuning_data]
+                except RuntimeError:
+                    F.cuda_reset_error()
+                    break
+                t = float(np.average(t))
+                if best is None or t < best:
+                    best, self._tunable_config["threshold"] = t, thr
+            for key, channels, probe in (("gather_tile_size", self.in_channels, F.cuda_time_gather),
+                                         ("scatter_tile_size", self.out_channels, F.cuda_time_scatter)):
+                best = None
+                for tile in range(4, channels + 1, 4):
+                    if channels % tile:
+                        continue
+                    t = float(np.average([
+                        probe(threshold=self._tunable_config["threshold"], tile_size=tile, weights=self.kernel,
+                              source_masks=sm, target_masks=tm, kernel_map_sizes=nb)
+                        for _ in range(self.__NUM_TUNING_ROUNDS__) for sm, tm, nb in self._tuning_data]))
+                    if best is None or t < best:
+                        best, self._tunable_config[key] = t, tile
+            if free_buffers:
+                F.cuda_free_buffers()
+        finally:
+            self._tuning_data = None
+
+    def forward(self, inputs: SparseTensor) -> SparseTensor:
+        x = inputs._features
+        if self.is_trivial:
+            y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
+            coords, stride = inputs._coordinates, inputs._stride
+        else:
+            if self._kernel_map_cache is None:
+                raise ValueError("Kernel map cache must be specified")
+            op = operator.floordiv if self.transposed else operator.mul
+            stride = tuple(op(a, b) for a, b in zip(inputs._stride, self.stride))
+            cache = self._kernel_map_cache
+            coords = cache.get_target_coordinates(inputs._coordinates, inputs._stride, stride, self.transposed)
+            d = self._tunable_config["map_dataflow"]
+            force_os = self._tunable_config["force_os"]
+            m = cache.get_kernel_map(inputs._coordinates, inputs._stride, coords, stride, self.kernel_size, d,
+                                     force_os, self.transposed)
+            # m = (S, T, map, t3, t4, t5, t6, mapsize, qmapsize) of the forward
+            # (non-transposed) layer; a transposed layer swaps S and T
+            S, T = (m[1], m[0]) if self.transposed else (m[0], m[1])
+            cfg = self._tunable_config
+            if d == 0 or force_os:
+                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel)
+            elif d == 1:
+                y = F.sparse_convolution_forward_ws_merged(S, T, x, self.kernel, m[5], m[6], m[3], m[7], m[8],
+                                                           self.transposed)
+            elif d == 2:
+                sm, tm = (m[4], m[3]) if self.transposed else (m[3], m[4])
+                if self._tuning_data is not None:
+                    self._tuning_data.append((sm, tm, m[5]))
+                y = F.sparse_convolution_forward_ws(S, T, x, self.kernel, sm, tm, m[5], cfg["gather_tile_size"],
+                                                    cfg["scatter_tile_size"], None, cfg["threshold"])
+            elif d % 2 == 1:
+                dense = None if d == 3 else m[2]
+                y = F.sparse_convolution_forward_hs_merged(S, T, x, self.kernel, m[5], m[6], m[3], dense, m[7],
+                                                           m[8], self.transposed)
+            else:
+                sm, tm = (m[4], m[3]) if self.transposed else (m[3], m[4])
+                dense = None if d == 4 else m[2]
+                y = F.sparse_convolution_forward_hs(S, T, x, self.kernel, sm, tm, m[5], dense,
+                                                    cfg["gather_tile_size"], cfg["scatter_tile_size"], None,
+                                                    cfg["threshold"])
+        if self.bias is not None:
+            y += self.bias
+        return SparseTensor(features=y, coordinates=coords, stride=stride)

@@ -1,0 +1,102 @@
+"""Feature dataflows (reference: source/spira/nn/functional/convolution.py:1-177).
+
+``gather_tile_size`` / ``scatter_tile_size`` / ``parallel`` are accepted for
+API compatibility; the gfx950 kernels pick their own tiling and run the
+per-offset GEMMs as one grouped launch.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._native import _C
+
+__all__ = [
+    "cuda_time_gather", "cuda_time_scatter", "sparse_convolution_forward_ws",
+    "sparse_convolution_forward_ws_merged", "sparse_convolution_forward_os",
+    "sparse_convolution_forward_hs", "sparse_convolution_forward_hs_merged", "cuda_time_gemm",
+    "set_gemm_parallel_level",
+]
+
+GEMM_PARALLEL_LEVEL = 4
+
+
+def set_gemm_parallel_level(level: int):
+    global GEMM_PARALLEL_LEVEL
+    GEMM_PARALLEL_LEVEL = level
+
+
+def _c(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.contiguous()
+
+
+def cuda_time_gather(weights, source_masks, target_masks, kernel_map_sizes, tile_size: int,
+                     is_hybrid: bool = False, threshold: Optional[float] = 0) -> float:
+    return _C.cuda_time_gather(tile_size, threshold, is_hybrid, _c(weights), _c(source_masks), _c(target_masks),
+                               _c(kernel_map_sizes))
+
+
+def cuda_time_scatter(weights, source_masks, target_masks, kernel_map_sizes, tile_size: int,
+                      is_hybrid: bool = False, threshold: Optional[float] = 0) -> float:
+    return _C.cuda_time_scatter(tile_size, threshold, is_hybrid, _c(weights), _c(source_masks), _c(target_masks),
+                                _c(kernel_map_sizes))
+
+
+def cuda_time_gemm(weights, source_masks, target_masks, kernel_map_sizes, parallel: Optional[int] = None,
+                   is_hybrid: bool = False, threshold: Optional[float] = 0) -> float:
+    if parallel is None:
+        parallel = GEMM_PARALLEL_LEVEL
+    return _C.cuda_time_gemm(parallel, threshold, is_hybrid, _c(weights), _c(source_masks), _c(target_masks),
+                             _c(kernel_map_sizes))
+
+
+def _gpu(sources: torch.Tensor) -> None:
+    if not sources.is_cuda:
+        raise NotImplementedError("spira_amd runs on the GPU only")
+
+
+def sparse_convolution_forward_ws(num_sources: int, num_targets: int, sources, weights, source_masks,
+                                  target_masks, kernel_map_sizes, gather_tile_size: int, scatter_tile_size: int,
+                                  parallel: Optional[int] = None, threshold: Optional[float] = 0):
+    _gpu(sources)
+    if parallel is None:
+        parallel = GEMM_PARALLEL_LEVEL
+    return _C.cuda_sparse_convolution_forward_ws(num_sources, num_targets, gather_tile_size, scatter_tile_size,
+                                                 parallel, threshold, _c(sources), _c(weights), _c(source_masks),
+                                                 _c(target_masks), _c(kernel_map_sizes))
+
+
+def sparse_convolution_forward_ws_merged(num_sources: int, num_targets: int, sources, weights, naddrs, qnaddrs,
+                                         nbmaps, mapsize: int, qmapsize: int, transpose: Optional[bool] = False):
+    _gpu(sources)
+    return _C.cuda_sparse_convolution_forward_ws_merged(num_sources, num_targets, _c(sources), _c(weights),
+                                                        _c(naddrs), _c(qnaddrs), _c(nbmaps), mapsize, qmapsize,
+                                                        bool(transpose))
+
+
+def sparse_convolution_forward_hs(num_sources: int, num_targets: int, sources, weights, source_masks,
+                                  target_masks, kernel_map_sizes, out_in_map, gather_tile_size: int,
+                                  scatter_tile_size: int, parallel: Optional[int] = None,
+                                  threshold: Optional[float] = 0):
+    _gpu(sources)
+    if parallel is None:
+        parallel = GEMM_PARALLEL_LEVEL
+    return _C.cuda_sparse_convolution_forward_hs(num_sources, num_targets, gather_tile_size, scatter_tile_size,
+                                                 parallel, threshold, _c(sources), _c(weights), _c(source_masks),
+                                                 _c(target_masks), _c(kernel_map_sizes), _c(out_in_map))
+
+
+def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sources, weights, naddrs, qnaddrs,
+                                         nbmaps, out_in_map, mapsize: int, qmapsize: int,
+                                         transpose: Optional[bool] = False):
+    _gpu(sources)
+    return _C.cuda_sparse_convolution_forward_hs_merged(num_sources, num_targets, _c(sources), _c(weights),
+                                                        _c(naddrs), _c(qnaddrs), _c(nbmaps), _c(out_in_map),
+                                                        mapsize, qmapsize, bool(transpose))
+
+
+def sparse_convolution_forward_os(num_sources: int, num_targets: int, out_in_map, sources, weights):
+    _gpu(sources)
+    return _C.cuda_sparse_convolution_forward_os(num_sources, num_targets, _c(out_in_map), _c(sources),
+                                                 _c(weights))

@@ -1,0 +1,91 @@
+"""Coordinate and kernel-map functions
+(reference: source/spira/nn/functional/indexing.py:1-105).
+
+Kernel maps come back as the reference's 9-tuple
+``(S, T, map, t3, t4, t5, t6, mapsize, qmapsize)``; see ``build_kmap``.
+"""
+from __future__ import annotations
+
+from typing import List, Tuple
+
+import torch
+
+from ...utils.helpers import as_tuple
+from ...utils.typing import ScalarOrTuple
+from ._native import _C
+
+__all__ = [
+    "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os",
+    "build_kmap_streamed", "streamed_output_generate", "build_kmap_no_small_z",
+]
+
+
+def _require_gpu(t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise NotImplementedError("spira_amd runs on the GPU only")
+
+
+def flat_sort(coordinates: torch.Tensor, double: bool = False):
+    """Pack ``[N, 3] int32`` voxels into keys and sort them; returns
+    ``(sorted keys, permutation as int64)``."""
+    coordinates = coordinates.contiguous()
+    _require_gpu(coordinates)
+    keys, index = _C.cuda_flatten_sort(coordinates, double)
+    return keys, index.to(torch.int64)
+
+
+def unflatten(coordinates: torch.Tensor) -> torch.Tensor:
+    coordinates = coordinates.contiguous()
+    _require_gpu(coordinates)
+    return _C.cuda_unflatten(coordinates)
+
+
+def streamed_output_generate(coordinates: torch.Tensor, target_strides: List[Tuple[int, int, int]]):
+    coordinates = coordinates.contiguous()
+    _require_gpu(coordinates)
+    return _C.cuda_streamed_output_generate(coordinates, [as_tuple(s, size=3) for s in target_strides])
+
+
+def build_kmap_streamed(voxels: List[torch.Tensor], kernel_sizes: List[ScalarOrTuple[int]],
+                        source_strides: List[ScalarOrTuple[int]], dataflow: List[int]):
+    voxels = [v.contiguous() for v in voxels]
+    kernel_sizes = [as_tuple(k, size=3, name="kernel_size") for k in kernel_sizes]
+    source_strides = [as_tuple(s, size=3, name="kernel_stride") for s in source_strides]
+    if not (len(kernel_sizes) == len(source_strides) == len(dataflow)):
+        raise ValueError("All argument lists must have the same length in build_kmap_streamed")
+    return _C.cuda_binary_search_streamed(voxels, kernel_sizes, source_strides, list(dataflow))
+
+
+def downsample(coordinates: torch.Tensor, target_stride: Tuple[int, int, int]) -> torch.Tensor:
+    coordinates = coordinates.contiguous()
+    _require_gpu(coordinates)
+    return _C.cuda_downsample(coordinates, *as_tuple(target_stride, size=3))
+
+
+def build_kmap(sources: torch.Tensor, targets: torch.Tensor, kernel_size: ScalarOrTuple[int],
+               source_stride: ScalarOrTuple[int], dataflow: int = 0):
+    """Kernel map of sorted unique ``sources`` for ``targets``.
+
+    dataflow 0: ``map [Tp, K]`` (output-stationary, z-major columns);
+    1 / odd: ``map [K, Tp]``, ``nbmaps [2, P]``, ``nbsizes``, ``naddrs``,
+    ``qnaddrs``, ``mapsize``, ``qmapsize``; 2 / even: ``map``,
+    ``source_masks``, ``target_masks``, ``nbsizes``.  Hybrid dataflows (3-8)
+    order rows dense-first by L1 distance; above 4 the first entry is the
+    dense part ``[Tp, dense]``.
+    """
+    sources = sources.contiguous()
+    targets = targets.contiguous()
+    return _C.cuda_binary_search(sources, targets, as_tuple(kernel_size, size=3, name="kernel_size"),
+                                 as_tuple(source_stride, size=3, name="kernel_stride"), dataflow)
+
+
+def convert_transposed_os(out_in_map: torch.Tensor, input_size: int) -> torch.Tensor:
+    return _C.cuda_convert_transposed_os(out_in_map.contiguous(), input_size)
+
+
+def build_kmap_no_small_z(sources: torch.Tensor, targets: torch.Tensor, kernel_size: ScalarOrTuple[int],
+                          source_stride: ScalarOrTuple[int]):
+    """Ablation: one full search per kernel offset, no z-scan; canonical columns."""
+    return _C.cuda_binary_search_no_small_z(sources.contiguous(), targets.contiguous(),
+                                            as_tuple(kernel_size, size=3, name="kernel_size"),
+                                            as_tuple(source_stride, size=3, name="kernel_stride"))

@@ -1,0 +1,69 @@
+"""Sparse tensor container (reference: source/spira/tensors.py:10-65)."""
+from __future__ import annotations
+
+from typing import Tuple, Union
+
+import torch
+
+from .utils.helpers import as_tuple
+
+__all__ = ["SparseTensor"]
+
+
+class SparseTensor:
+    """Voxel coordinates plus per-voxel features.
+
+    ``coordinates`` start as raw ``[N, 3] int32`` voxels; ``order()`` replaces
+    them with sorted packed keys (``int64`` when ``double`` else ``int32``) and
+    permutes the features to match.  ``stride`` is the per-axis tensor stride.
+    """
+
+    def __init__(self, coordinates: torch.Tensor, features: torch.Tensor,
+                 stride: Union[int, Tuple[int, ...]] = 1, double: bool = False):
+        self._coordinates = coordinates
+        self._features = features
+        self._double = double
+        self._stride = as_tuple(stride, size=3, name="strides")
+
+    @property
+    def coordinates(self) -> torch.Tensor:
+        return self._coordinates
+
+    @property
+    def features(self) -> torch.Tensor:
+        return self._features
+
+    @property
+    def stride(self) -> Tuple[int, int, int]:
+        return self._stride
+
+    def cuda(self) -> "SparseTensor":
+        self._coordinates = self._coordinates.cuda()
+        self._features = self._features.cuda()
+        return self
+
+    def to(self, dtype) -> "SparseTensor":
+        self._features = self._features.to(dtype=dtype)
+        return self
+
+    def half(self) -> "SparseTensor":
+        self._features = self._features.half()
+        return self
+
+    def contiguous(self) -> "SparseTensor":
+        self._coordinates = self._coordinates.contiguous()
+        self._features = self._features.contiguous()
+        return self
+
+    def __add__(self, other: "SparseTensor") -> "SparseTensor":
+        return SparseTensor(coordinates=self._coordinates, features=self._features + other._features,
+                            stride=self._stride)
+
+    def order(self) -> "SparseTensor":
+        """Pack and sort the coordinates; features follow the sort."""
+        from .nn.functional.indexing import flat_sort
+
+        keys, index = flat_sort(self._coordinates, self._double)
+        self._coordinates = keys.contiguous()
+        self._features = self._features[index].contiguous()
+        return self

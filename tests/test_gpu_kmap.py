@@ -1,0 +1,186 @@
+"""Kernel-map parity on the GPU: every element of the `_C` 9-tuples must be
+bit-identical to the oracle (oracle/oracle.py, itself pinned by
+tests/test_oracle.py).  Runs through spira_amd's `_C` -> libspira_hip.so."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from spira_amd import scenes
+from spira_amd.nn import functional as F
+
+from helpers import assert_tuple_equal, np_
+
+pytestmark = pytest.mark.gpu
+
+
+def _keys(coords, bits, dev):
+    k, _ = orc.flatten_sort(coords, bits == 64)
+    return k, torch.from_numpy(k).to(dev)
+
+
+@pytest.fixture(scope="module")
+def scene_small():
+    return scenes.spheres_planes(n=6000, grid=64, seed=7)
+
+
+@pytest.fixture(scope="module")
+def scene_lidar():
+    return scenes.lidar()
+
+
+def test_flatten_sort_and_unflatten(dev, scene_small):
+    for double in (False, True):
+        c = torch.from_numpy(scene_small).to(dev)
+        keys, perm = F.flat_sort(c, double)
+        rk, rp = orc.flatten_sort(scene_small, double)
+        assert np.array_equal(np_(keys), rk)
+        assert np.array_equal(np_(perm), rp.astype(np.int64))
+        assert np.array_equal(np_(F.unflatten(keys)), orc.unflatten(rk))
+
+
+def test_flatten_sort_duplicates_are_stable(dev):
+    rng = np.random.default_rng(3)
+    c = rng.integers(0, 6, size=(5000, 3)).astype(np.int32)  # many duplicates
+    keys, perm = F.flat_sort(torch.from_numpy(c).to(dev), True)
+    rk, rp = orc.flatten_sort(c, True)
+    assert np.array_equal(np_(keys), rk)
+    assert np.array_equal(np_(perm), rp.astype(np.int64))
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+@pytest.mark.parametrize("stride", [(2, 2, 2), (4, 4, 4), (1, 1, 2), (8, 8, 16)])
+def test_downsample(dev, scene_small, bits, stride):
+    rk, tk = _keys(scene_small, bits, dev)
+    got = F.downsample(tk, stride)
+    assert np.array_equal(np_(got), orc.downsample(rk, stride))
+
+
+def test_streamed_output_generate(dev, scene_small):
+    rk, tk = _keys(scene_small, 64, dev)
+    strides = [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)]
+    outs = F.streamed_output_generate(tk, strides)
+    for o, s in zip(outs, strides):
+        assert np.array_equal(np_(o), orc.downsample(rk, s))
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+@pytest.mark.parametrize("dataflow", list(range(9)))
+def test_submanifold_all_dataflows(dev, scene_small, bits, dataflow):
+    rk, tk = _keys(scene_small, bits, dev)
+    got = F.build_kmap(tk, tk, 3, 1, dataflow)
+    ref = orc.build_kmap(rk, rk, (3, 3, 3), (1, 1, 1), dataflow)
+    assert_tuple_equal(got, ref, f"bits={bits} dataflow={dataflow}")
+
+
+@pytest.mark.parametrize("dataflow", [0, 1, 2, 3, 4, 5, 6, 7, 8])
+def test_submanifold_k5(dev, scene_small, dataflow):
+    rk, tk = _keys(scene_small, 64, dev)
+    got = F.build_kmap(tk, tk, 5, 1, dataflow)
+    ref = orc.build_kmap(rk, rk, (5, 5, 5), (1, 1, 1), dataflow)
+    assert_tuple_equal(got, ref, f"k5 dataflow={dataflow}")
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+@pytest.mark.parametrize("ksize", [(2, 2, 2), (3, 3, 3), (5, 5, 5), (1, 1, 3)])
+@pytest.mark.parametrize("dataflow", [0, 1, 2])
+def test_downsampling_maps(dev, scene_small, bits, ksize, dataflow):
+    rk, tk = _keys(scene_small, bits, dev)
+    ts = (1, 1, 2) if ksize == (1, 1, 3) else (2, 2, 2)
+    rt = orc.downsample(rk, ts)
+    tt = torch.from_numpy(rt).to(dev)
+    got = F.build_kmap(tk, tt, ksize, 1, dataflow)
+    ref = orc.build_kmap(rk, rt, ksize, (1, 1, 1), dataflow)
+    assert_tuple_equal(got, ref, f"bits={bits} k={ksize} dataflow={dataflow}")
+
+
+def test_strided_source_maps(dev, scene_small):
+    # stride-2 sources (a deeper U-Net level) with k=3 and k=2 maps
+    rk, _ = _keys(scene_small, 64, dev)
+    s2 = orc.downsample(rk, (2, 2, 2))
+    s4 = orc.downsample(rk, (4, 4, 4))
+    t2, t4 = torch.from_numpy(s2).to(dev), torch.from_numpy(s4).to(dev)
+    for d in (0, 1, 2):
+        assert_tuple_equal(F.build_kmap(t2, t2, 3, 2, d), orc.build_kmap(s2, s2, (3, 3, 3), (2, 2, 2), d), "s2 k3")
+        assert_tuple_equal(F.build_kmap(t2, t4, 2, 2, d), orc.build_kmap(s2, s4, (2, 2, 2), (2, 2, 2), d), "s2 k2")
+
+
+@pytest.mark.parametrize("ksize", [3, 5])
+def test_no_small_z(dev, scene_small, ksize):
+    rk, tk = _keys(scene_small, 64, dev)
+    got = F.build_kmap_no_small_z(tk, tk, ksize, 1)
+    ref = orc.build_kmap_no_small_z(rk, rk, (ksize,) * 3, (1, 1, 1))
+    assert_tuple_equal(got, ref, "no_small_z")
+
+
+def test_convert_transposed(dev, scene_small):
+    rk, tk = _keys(scene_small, 64, dev)
+    rt = orc.downsample(rk, (2, 2, 2))
+    tt = torch.from_numpy(rt).to(dev)
+    m = F.build_kmap(tk, tt, 2, 1, 0)
+    got = F.convert_transposed_os(m[2], m[0])
+    assert np.array_equal(np_(got), orc.convert_transposed_os(np_(m[2]), m[0]))
+
+
+@pytest.mark.parametrize("ksize,stride", [(3, 1), (5, 1), (3, 2), (5, 2)])
+def test_lidar_config2_maps(dev, scene_lidar, ksize, stride):
+    """Config 2: the ~100k-voxel LiDAR scene, k in {3,5}, stride in {1,2}."""
+    rk, tk = _keys(scene_lidar, 64, dev)
+    if stride == 1:
+        rt, tt = rk, tk
+    else:
+        rt = orc.downsample(rk, (2, 2, 2))
+        tt = torch.from_numpy(rt).to(dev)
+    got = F.build_kmap(tk, tt, ksize, 1, 0)
+    ref = orc.build_kmap(rk, rt, (ksize,) * 3, (1, 1, 1), 0)
+    assert_tuple_equal(got, ref, f"lidar k={ksize} s={stride}")
+    got = F.build_kmap(tk, tt, ksize, 1, 1)
+    ref = orc.build_kmap(rk, rt, (ksize,) * 3, (1, 1, 1), 1)
+    assert_tuple_equal(got, ref, f"lidar ws k={ksize} s={stride}")
+
+
+def test_edge_cases(dev):
+    # single voxel, coordinates at zero (negative offsets wrap), voxel at the
+    # top of the 32-bit z range, a target absent from the sources, T not a
+    # multiple of 64 / 128
+    pts = np.array([[0, 0, 0], [0, 0, 1], [1, 0, 0], [0, 1, 255], [4095, 4095, 255], [7, 7, 7]], np.int32)
+    for bits in (32, 64):
+        for n in (1, 2, len(pts)):
+            rk, tk = _keys(pts[:n], bits, dev)
+            for d in range(9):
+                got = F.build_kmap(tk, tk, 3, 1, d)
+                assert_tuple_equal(got, orc.build_kmap(rk, rk, (3, 3, 3), (1, 1, 1), d), f"edge n={n} d={d}")
+    # targets that are not sources
+    rk, tk = _keys(pts[:3], 64, dev)
+    rt, tt = _keys(pts[3:], 64, dev)
+    for d in (0, 1, 2):
+        assert_tuple_equal(F.build_kmap(tk, tt, 3, 1, d), orc.build_kmap(rk, rt, (3, 3, 3), (1, 1, 1), d), "disjoint")
+
+
+def test_wide_window_fallback(dev):
+    """Sparse targets over dense sources: the per-wave source window exceeds
+    the LDS cap and the global-memory search path runs."""
+    g = np.stack(np.meshgrid(np.arange(64), np.arange(64), np.arange(16), indexing="ij"), -1).reshape(-1, 3)
+    src = g.astype(np.int32)
+    tgt = g[::97].astype(np.int32)
+    rk, tk = _keys(src, 64, dev)
+    rt, tt = _keys(tgt, 64, dev)
+    for d in (0, 1, 2):
+        got = F.build_kmap(tk, tt, 3, 1, d)
+        assert_tuple_equal(got, orc.build_kmap(rk, rt, (3, 3, 3), (1, 1, 1), d), f"wide d={d}")
+
+
+def test_streamed_build_matches_single(dev, scene_small):
+    """Network-wide build (UNet layer list) equals per-layer builds."""
+    rk, tk = _keys(scene_small, 64, dev)
+    target_strides = [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)]
+    voxels = [tk] + list(F.streamed_output_generate(tk, target_strides))
+    ks = [(3, 3, 3), (2, 2, 2)] * 4 + [(3, 3, 3)]
+    ss = [(1, 1, 1), (1, 1, 1), (2, 2, 2), (2, 2, 2), (4, 4, 4), (4, 4, 4), (8, 8, 8), (8, 8, 8), (16, 16, 16)]
+    for dfs in ([0] * 9, [1] * 9, [2] * 9, [0, 1, 2, 0, 1, 2, 0, 1, 2]):
+        maps = F.build_kmap_streamed(voxels, ks, ss, dfs)
+        for i, m in enumerate(maps):
+            src, tgt = np_(voxels[i // 2]), np_(voxels[(i + 1) // 2])
+            half = (i % 2 == 0) if dfs[i] == 2 else None
+            ref = orc.build_kmap(src, tgt, ks[i], ss[i], dfs[i], half=half)
+            assert_tuple_equal(m, ref, f"streamed map {i} dataflow {dfs[i]}")
