@@ -116,6 +116,20 @@ int spira_hip_kmap_emit_masks(const int32_t *kernel_map, int64_t num_sources, in
 int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_targets, int num_offsets,
                                     int64_t aligned_sources, int32_t *out, hipStream_t stream);
 
+/* Workspace bytes for spira_hip_kmap_row_order. */
+int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes);
+
+/* order = the targets of an output-stationary map [>= num_targets, K] sorted
+ * (stably) by the bitmask of their valid columns, so that rows with the same
+ * neighbour pattern are processed together; row_masks (nullable) receives
+ * the sorted bitmasks (bit j: column j valid for j < 63, bit 63: any column
+ * >= 63 valid) and ordered_map (nullable, [num_targets, K]) the map rows in
+ * that order.  (No reference counterpart: the reference's output-stationary
+ * kernels walk targets in index order, cuda/kernels/output_stat.cuh:20-1031.) */
+int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int num_offsets, int32_t *order,
+                             uint64_t *row_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
 /* ptr[0..n) = value (reference: the cudaMemsetAsync(-1) mask initialisation,
  * cuda/functions/query_sorted_index.cu:475-477). */
 int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t stream);
@@ -129,20 +143,47 @@ int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t strea
 #define SPIRA_OUT_STORE_F32 1 /* write an fp32 buffer                  */
 #define SPIRA_OUT_ADD_F32 2   /* add into an fp32 buffer               */
 
-/* Workspace bytes of the conv entry points for K offsets (transposed fp16
- * weights for the MFMA path; 0 otherwise). */
-int spira_hip_conv_workspace(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes);
+/* Bytes of the prepared (MFMA-ready) copy of weights [K, c_in, c_out]; 0 when
+ * the dtype runs without one (fp32). */
+int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes);
+
+/* Prepare weights [K, c_in, c_out] for the fp16 MFMA kernels: transposed to
+ * [K, c_out, c_in] and zero-padded to 32 output / 16 input channels.  A
+ * prepared copy stays valid until the weights change.  (No reference
+ * counterpart: the reference reads row-major weights in every kernel.) */
+int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, int c_out, int dtype, void *prepared,
+                              hipStream_t stream);
+
+/* Workspace bytes of spira_hip_conv_os (an fp32 partial-sum buffer when a
+ * small layer splits its offsets over blocks). */
+int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
+                                size_t *bytes);
 
 /* Output-stationary implicit GEMM: targets[t] = sum_j sources[map[t, j]] @
  * weights[j] for map entries >= 0; map is [>= num_targets, num_offsets],
- * weights [num_offsets, c_in, c_out]; fp32 accumulation.
+ * weights [num_offsets, c_in, c_out]; fp32 accumulation.  fp16 needs
+ * `prepared` (spira_hip_prepare_weights); fp32 reads `weights`.  With
+ * out_mode SPIRA_OUT_STORE an optional epilogue is applied per element:
+ * v = v * scale[c] + shift[c] + residual[t, c], then max(v, 0) if relu
+ * (scale / shift fp32 [c_out], residual [num_targets, c_out] in the storage
+ * dtype; each nullable).  row_order (nullable, [num_targets]) is a
+ * permutation of the targets (spira_hip_kmap_row_order) that the fp16 path
+ * walks instead of 0..T-1, in which case out_in_map must hold the rows in
+ * that order (row i = target row_order[i]); row_masks (nullable, [num_targets]
+ * in the same order) are the rows' valid-column bitmasks, which let a block
+ * skip offsets none of its rows uses.  Both change the schedule, not the
+ * result.
  * (reference: cuda_sparse_convolution_forward_os,
  * torch/cuda_sparse_convolution_forward.cu:448-496; SparseConvolutionForward_OS
  * cuda/functions/sparse_convolution.cu:1354-1393; kernels
- * conv_forward_cuda_setting{1,2,3}_mode0_*, cuda/kernels/output_stat.cuh:20-1031). */
-int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const void *sources,
-                      int64_t num_sources, int c_in, const void *weights, int c_out, int dtype, void *targets,
-                      int out_mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
+ * conv_forward_cuda_setting{1,2,3}_mode0_*, cuda/kernels/output_stat.cuh:20-1031;
+ * the epilogue replaces the separate bias / batch-norm / ReLU / residual ops of
+ * source/spira/nn/conv.py:415-416 and scripts/models/spira/modules/blocks.py:12-84). */
+int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
+                      const uint64_t *row_masks, const void *sources,
+                      int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
+                      void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
+                      int relu, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Fused weight-stationary pass over a compacted pair list: for compacted row r
  * (pairs naddrs[r]..naddrs[r+1] of in_idx/out_idx) target_acc[out] +=
@@ -157,8 +198,8 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
 int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int32_t *in_idx, const int32_t *out_idx,
                             int rows, const int32_t *naddrs, const int32_t *qnaddrs, int64_t num_pairs,
                             int64_t quantized_pairs, int weight_offset, int mirror_rows, const void *sources,
-                            int c_in, const void *weights, int num_weights, int c_out, int dtype, float *target_acc,
-                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+                            int c_in, const void *weights, const void *prepared, int num_weights, int c_out,
+                            int dtype, float *target_acc, hipStream_t stream);
 
 /* Gather: buffer[padded_offsets[k] + source_masks[k, s]] = sources[s] for
  * mask entries >= 0.  padded_offsets is a HOST array of num_offsets entries.
@@ -168,12 +209,13 @@ int spira_hip_ws_gather(int64_t num_sources, int c_in, int num_offsets, int dtyp
                         const int32_t *source_masks, const int64_t *padded_offsets, void *buffer, hipStream_t stream);
 
 /* Grouped GEMM: buffer_out[rows of offset k] (fp32) = buffer_in[rows of
- * offset k] @ weights[k]; rows / padded_offsets are HOST arrays.
+ * offset k] @ weights[k]; rows / padded_offsets are HOST arrays; fp16 uses
+ * `prepared` weights of these num_offsets offsets.
  * (reference: bucketed cublas{H,S}gemmStridedBatched, BatchedMatMul
  * cuda/helpers.cu:104-161, driven by cuda/functions/sparse_convolution.cu:1048-1117). */
 int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padded_offsets, int c_in, int c_out,
-                      int dtype, const void *buffer_in, const void *weights, float *buffer_out, void *workspace,
-                      size_t workspace_bytes, hipStream_t stream);
+                      int dtype, const void *buffer_in, const void *weights, const void *prepared, float *buffer_out,
+                      hipStream_t stream);
 
 /* Scatter: targets[t] = base[t] + sum_k buffer[padded_offsets[k] + target_masks[k, t]]
  * (base: nullable fp32 [num_targets, c_out])
@@ -183,9 +225,12 @@ int spira_hip_ws_scatter(int64_t num_targets, int c_out, int num_offsets, int dt
                          const int64_t *padded_offsets, const float *buffer, const float *base, void *targets,
                          hipStream_t stream);
 
-/* dst (storage dtype) = src (fp32), n elements (reference: the half outputs of
- * the weight-stationary kernels, cuda/kernels/weight_stat.cuh:914). */
-int spira_hip_cast_f32(const float *src, int64_t n, int dtype, void *dst, hipStream_t stream);
+/* targets (storage dtype) = epilogue(acc) for an fp32 accumulation buffer
+ * [num_targets, c_out], with the epilogue of spira_hip_conv_os (reference:
+ * the half outputs of the weight-stationary kernels, cuda/kernels/weight_stat.cuh:914,
+ * and the hybrid final add, torch/cuda_sparse_convolution_forward.cu:336). */
+int spira_hip_finalize(const float *acc, int64_t num_targets, int c_out, int dtype, const float *scale,
+                       const float *shift, const void *residual, int relu, void *targets, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -8,14 +8,29 @@
 //  * gather -> grouped GEMM -> scatter over per-offset masks
 //    (padded_gather/scatter_warp_optimized.cuh, sparse_convolution.cu:488-1124).
 //
-// MI355X design: fp16 operands on v_mfma_f32_32x32x16_f16 with fp32
-// accumulation.  A block is 4 waves; a wave owns 32 output rows x 32*WN
-// columns (WN accumulators of 16 floats).  A-operand rows are gathered
-// straight from HBM/L2 into registers (each lane loads the 16 bytes its MFMA
-// slot needs, so no LDS round trip for the irregular side); the offset's
-// weight slice is staged once per block in LDS, pre-transposed to
-// [Cout, Cin] so that B operands are 16-byte LDS reads.  Waves whose 32 rows
-// have no neighbour at an offset skip its MFMAs.
+// MI355X design (fp16 storage, fp32 accumulation on v_mfma_f32_32x32x16_f16).
+// All three dataflows share one MMA core:
+//  * a block is 4 waves; a wave owns MT tiles of 32 rows x 32*WN columns
+//    (MT*WN accumulators of 16 floats); WN = 1, 2, 3, 4 or 8 so that 96- and
+//    256-channel layers do not pad to a power of two;
+//  * the K dimension is walked in steps of 32 input channels of one kernel
+//    offset.  Each step's operands land in a 3-stage LDS ring through
+//    global_load_lds_dwordx4 (direct HBM/L2 -> LDS, no register staging): the
+//    gathered rows lane-linearly (lane L of a wave fetches exactly the 16
+//    bytes its MFMA A slot needs, so the A reads are conflict-free), the
+//    offset's weight chunk with an XOR swizzle that makes the B reads
+//    conflict-free.  Loads run two steps ahead of the MFMAs; a step costs one
+//    workgroup barrier and one vmcnt wait, and rows without a neighbour read a
+//    16-byte zero block instead of branching;
+//  * weights are prepared once per weight tensor into [K, CoutP, CinP]
+//    (transposed, zero-padded to 32 output / 16 input channels), so odd
+//    channel counts (the 3-channel stem) take the same path;
+//  * the output-stationary kernel can walk its rows in neighbour-mask order
+//    (rows with the same neighbour pattern together) and visits only the
+//    offsets some row of the block uses; small layers split the offsets over
+//    blocks (fp32 atomics + finalize);
+//  * an optional epilogue folds a per-channel scale / shift (eval-mode batch
+//    norm), a residual add and ReLU into the output write.
 #include "common.hpp"
 #include "../../../include/spira_hip.h"
 
@@ -26,221 +41,540 @@ namespace spira_hip {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
 
-constexpr int kRowsPerBlock = 128;  // 4 waves x 32 rows
-constexpr int kChunk = 64;          // Cin staged per LDS round
-constexpr int kBStride = kChunk + 8;  // halves per staged weight row (bank spread)
 constexpr int kMaxGroups = 128;
 
 enum OutMode { kStoreNative = 0, kStoreF32 = 1, kAddF32 = 2, kAtomicF32 = 3 };
 
-__device__ __forceinline__ half8 zero_h8() {
-  half8 z;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) z[i] = static_cast<_Float16>(0.f);
-  return z;
+struct Epilogue {
+  const float *scale;    // [Cout] or null
+  const float *shift;    // [Cout] or null
+  const void *residual;  // [T, Cout] in the storage dtype, or null
+  int relu;
+};
+
+// 16 zero bytes: the source of every masked lane of an LDS-DMA load
+__device__ __align__(64) _Float16 g_zero16[32];
+
+namespace ring {
+
+constexpr int KC = 32;  // input channels per step
+constexpr int NS = 3;   // LDS ring depth
+
+template <int WN, int MT> struct Cfg {
+  static constexpr int BN = 32 * WN;
+  static constexpr int BM = 128 * MT;
+  static constexpr int A_BYTES = MT * 8192;          // 4 waves x MT x 2 k-halves x 64 lanes x 16 B
+  static constexpr int BVEC = (BN * 4 + 255) / 256;  // 16-byte weight vectors per thread and step
+  static constexpr int B_BYTES = BVEC * 4096;
+  static constexpr int IDX_OFF = A_BYTES + B_BYTES;  // 4 waves x 64 row indices of a later step
+  static constexpr int STAGE = IDX_OFF + 1024;
+  static constexpr int LPS = MT * 2 + BVEC;          // LDS-DMA loads per wave and step
+};
+
+__device__ __forceinline__ void dma16(const void *g, void *lds_wave_base) {
+  // address-space casts (generic -> global / LDS) need C-style casts
+  __builtin_amdgcn_global_load_lds((gbl_void_t *)(const_cast<void *>(g)), (lds_void_t *)(lds_wave_base), 16, 0, 0);
 }
 
-// Stage WT[wrow][n0:n0+BN][kc:kc+kChunk] (transposed weights [K, Cout, Cin])
-// into LDS, zero outside Cout / Cin.
-template <int BN>
-__device__ __forceinline__ void stage_weights(_Float16 *Bs, const _Float16 *__restrict__ WT, int64_t wrow, int n0,
-                                              int Cout, int kc, int Cin) {
-  constexpr int VPR = kChunk / 8;  // 16-byte vectors per row
-  for (int v = threadIdx.x; v < BN * VPR; v += 256) {
-    const int n = v / VPR, kk = (v % VPR) * 8;
-    half8 w = zero_h8();
-    if (n0 + n < Cout && kc + kk < Cin)
-      w = *reinterpret_cast<const half8 *>(WT + (wrow * Cout + n0 + n) * Cin + kc + kk);
-    *reinterpret_cast<half8 *>(Bs + n * kBStride + kk) = w;
+// wait until at most N vector-memory operations of this wave are in flight
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ const _Float16 *zero16() { return g_zero16; }
+
+// B slot of (row n, 16-byte chunk c) inside a stage's weight region: four
+// chunks per row, the chunk index XOR-ed with (n / 4) % 4
+__device__ __forceinline__ int bslot(int n, int c) { return n * 4 + (c ^ ((n >> 2) & 3)); }
+
+// Issue the loads of one step into `stage`: A rows idx[m] (or -1) at channels
+// kb..kb+31, weight row `wrow` (ignored when !live: every wave then issues
+// the same number of loads from the zero block, which keeps vmcnt uniform).
+template <int WN, int MT, bool ALIGNED>
+__device__ __forceinline__ void issue(char *stage, bool live, const int32_t (&idx)[MT], int64_t wrow, int kb,
+                                      const _Float16 *X, int Cin, int CinP,
+                                      const _Float16 *WT, int n0, int CoutP) {
+  using C = Cfg<WN, MT>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kh = lane >> 5;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int k = kb + ks * 16 + kh * 8;
+      const _Float16 *g = zero16();
+      if (live && idx[m] >= 0 && k < Cin) g = X + static_cast<int64_t>(idx[m]) * Cin + k;
+      if constexpr (!ALIGNED) {
+        // rows that are not 16-byte aligned are staged through registers
+        half8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[e] = (live && idx[m] >= 0 && k + e < Cin) ? X[static_cast<int64_t>(idx[m]) * Cin + k + e]
+                                                     : static_cast<_Float16>(0.f);
+        *reinterpret_cast<half8 *>(stage + ((wave * MT + m) * 2 + ks) * 1024 + lane * 16) = v;
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+      } else {
+        dma16(g, stage + ((wave * MT + m) * 2 + ks) * 1024);
+      }
+    }
+  }
+  char *bst = stage + C::A_BYTES;
+#pragma unroll
+  for (int i = 0; i < C::BVEC; ++i) {
+    const int v = i * 256 + tid;
+    const int n = v >> 2, cp = v & 3;
+    const int c = cp ^ ((n >> 2) & 3);
+    const _Float16 *g = zero16();
+    if (live && n < C::BN && n0 + n < CoutP && kb + c * 8 < CinP)
+      g = WT + (wrow * CoutP + n0 + n) * CinP + kb + c * 8;
+    dma16(g, bst + (i * 256 + wave * 64) * 16);
   }
 }
 
-// One staged chunk: acc[wn] += A(rows of this wave) x Bs.
-template <int WN>
-__device__ __forceinline__ void mma_chunk(floatx16 *acc, const _Float16 *Bs, const _Float16 *xrow, bool has_row,
-                                          int kc, int Cin, int r, int kh) {
+// LDS reads of the ring are inline assembly: the compiler then inserts no
+// waits of its own for them (its LDS-DMA tracking loses precision at the loop
+// header and would drain the whole ring there); the ring's explicit
+// vmcnt wait + barrier orders them after the DMA writes, lds_fence() after
+// their own completion.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t *)(const_cast<void *>(p))));
+}
+__device__ __forceinline__ half8 lds_read16(const void *p) {
+  half8 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return v;
+}
+__device__ __forceinline__ int32_t lds_read4(const void *p) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// ties a value read by lds_read* to a point after lds_wait()
+template <class V> __device__ __forceinline__ void pin(V &v) { asm volatile("" : "+v"(v)); }
+
+// MFMAs of one staged step
+template <int WN, int MT>
+__device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const char *stage, unsigned anymask) {
+  using C = Cfg<WN, MT>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, kh = lane >> 5;
+  const char *bst = stage + C::A_BYTES;
 #pragma unroll
-  for (int ks = 0; ks < kChunk / 16; ++ks) {
-    const int k = kc + ks * 16 + kh * 8;
-    if (kc + ks * 16 >= Cin) break;  // wave-uniform
-    half8 a = zero_h8();
-    if (has_row && k < Cin) a = *reinterpret_cast<const half8 *>(xrow + k);
+  for (int ks = 0; ks < 2; ++ks) {
+    half8 b[WN], a[MT];
 #pragma unroll
-    for (int wn = 0; wn < WN; ++wn) {
-      const half8 b = *reinterpret_cast<const half8 *>(Bs + (wn * 32 + r) * kBStride + ks * 16 + kh * 8);
-      acc[wn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[wn], 0, 0, 0);
+    for (int wn = 0; wn < WN; ++wn) b[wn] = lds_read16(bst + bslot(wn * 32 + r, ks * 2 + kh) * 16);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if ((anymask >> m) & 1) a[m] = lds_read16(stage + ((wave * MT + m) * 2 + ks) * 1024 + lane * 16);
+    lds_wait();
+#pragma unroll
+    for (int wn = 0; wn < WN; ++wn) pin(b[wn]);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (!((anymask >> m) & 1)) continue;
+      pin(a[m]);
+#pragma unroll
+      for (int wn = 0; wn < WN; ++wn)
+        acc[m][wn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m], b[wn], acc[m][wn], 0, 0, 0);
     }
   }
 }
 
-// Write one wave's 32 x (32*WN) accumulator tile.  row_of(i) maps the tile row
-// to an output row (or -1).
+// The pipelined step loop over nsteps steps; stage u % 3 of the ring holds
+// step u.  Two callbacks describe the steps:
+//  * fetch(u, st) issues exactly PL LDS-DMA loads per wave that bring step
+//    u's row indices into st + IDX_OFF (also for u >= nsteps, so that the
+//    vmcnt arithmetic is the same in every wave);
+//  * resolve(u, st, idx, wrow, kb) turns them into the gathered rows idx[m]
+//    (or -1), the weight row and the first input channel of step u.
+// Order of vector-memory operations: F0 F1 F2 D0 F3 D1 F4 | D2 F5 | D3 F6 ...
+// (F = fetch, D = the LPS LDS-DMA loads of a step).  Before step s computes,
+// D(s) must be complete while F(s+3) D(s+1) F(s+4) may still be in flight,
+// hence vmcnt(LPS + 2 PL); F(s+2), which step s+2's issue reads, is older
+// than D(s) and is covered by the same wait.  F(u+3) overwrites the index
+// slot that step u's issue has just read (each wave reads only its own).
+template <int WN, int MT, bool ALIGNED, int PL, class Fetch, class Resolve>
+__device__ __forceinline__ void run(floatx16 (&acc)[MT][WN], int nsteps, Fetch fetch, Resolve resolve,
+                                    const _Float16 *X, int Cin, int CinP, const _Float16 *WT, int n0, int CoutP,
+                                    char *s0, char *s1, char *s2) {
+  using C = Cfg<WN, MT>;
+  unsigned any0 = 0, any1 = 0, any2 = 0;  // per-stage "m-tile has a row" bits
+  auto put = [&](int u, char *st, unsigned &anyb) {
+    int32_t idx[MT];
+    int64_t wrow = 0;
+    int kb = 0;
+    const bool live = u < nsteps;
+    if (live) resolve(u, st, idx, wrow, kb);
+    else {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) idx[m] = -1;
+    }
+    anyb = 0;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) anyb |= (ballot(idx[m] >= 0) != 0 ? 1u : 0u) << m;
+    issue<WN, MT, ALIGNED>(st, live, idx, wrow, kb, X, Cin, CinP, WT, n0, CoutP);
+  };
+  fetch(0, s0);
+  fetch(1, s1);
+  fetch(2, s2);
+  if constexpr (PL > 0) wait_vm<2 * PL>();  // F0 is older than F1 F2
+  put(0, s0, any0);
+  fetch(3, s0);
+  if constexpr (PL > 0) wait_vm<C::LPS + 2 * PL>();  // F1 is older than F2 D0 F3
+  put(1, s1, any1);
+  fetch(4, s1);
+  for (int s = 0; s < nsteps; s += 3) {
+    wait_vm<C::LPS + 2 * PL>();
+    __builtin_amdgcn_s_barrier();
+    put(s + 2, s2, any2);
+    fetch(s + 5, s2);
+    compute<WN, MT>(acc, s0, any0);
+    if (s + 1 >= nsteps) break;
+    wait_vm<C::LPS + 2 * PL>();
+    __builtin_amdgcn_s_barrier();
+    put(s + 3, s0, any0);
+    fetch(s + 6, s0);
+    compute<WN, MT>(acc, s1, any1);
+    if (s + 2 >= nsteps) break;
+    wait_vm<C::LPS + 2 * PL>();
+    __builtin_amdgcn_s_barrier();
+    put(s + 4, s1, any1);
+    fetch(s + 7, s1);
+    compute<WN, MT>(acc, s2, any2);
+  }
+  wait_vm<0>();
+}
+
+}  // namespace ring
+
+template <int WN, int MT> __device__ __forceinline__ void zero_acc(floatx16 (&acc)[MT][WN]) {
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int wn = 0; wn < WN; ++wn)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[m][wn][i] = 0.f;
+}
+
+// Write one 32-row MFMA tile; orow[row] is the output row or -1.
 template <int WN, int MODE>
-__device__ __forceinline__ void store_tile(const floatx16 *acc, const int64_t *orow, int n0, int Cout, int r, int kh,
-                                           void *Yv) {
+__device__ __forceinline__ void store_tile(const floatx16 (&acc)[WN], const int32_t *orow, int n0, int Cout, int r,
+                                           int kh, void *Yv, const Epilogue &epi) {
 #pragma unroll
   for (int wn = 0; wn < WN; ++wn) {
     const int col = n0 + wn * 32 + r;
     if (col >= Cout) continue;
+    float sc = 1.f, sh = 0.f;
+    if constexpr (MODE == kStoreNative) {
+      if (epi.scale) sc = epi.scale[col];
+      if (epi.shift) sh = epi.shift[col];
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int row = (i / 4) * 8 + kh * 4 + (i % 4);
-      const int64_t o = orow[row];
+      const int32_t o = orow[row];
       if (o < 0) continue;
-      const float v = acc[wn][i];
+      float v = acc[wn][i];
+      const int64_t at = static_cast<int64_t>(o) * Cout + col;
       if constexpr (MODE == kStoreNative) {
-        static_cast<_Float16 *>(Yv)[o * Cout + col] = static_cast<_Float16>(v);
+        v = v * sc + sh;
+        if (epi.residual) v += static_cast<float>(static_cast<const _Float16 *>(epi.residual)[at]);
+        if (epi.relu) v = v > 0.f ? v : 0.f;
+        static_cast<_Float16 *>(Yv)[at] = static_cast<_Float16>(v);
       } else if constexpr (MODE == kStoreF32) {
-        static_cast<float *>(Yv)[o * Cout + col] = v;
+        static_cast<float *>(Yv)[at] = v;
       } else if constexpr (MODE == kAddF32) {
-        static_cast<float *>(Yv)[o * Cout + col] += v;
+        static_cast<float *>(Yv)[at] += v;
       } else {
-        atomicAdd(static_cast<float *>(Yv) + o * Cout + col, v);
+        atomicAdd(static_cast<float *>(Yv) + at, v);
       }
     }
   }
 }
 
-// Output-stationary implicit GEMM, fp16 in / fp32 accumulate.
-template <int WN, int MODE>
-__global__ __launch_bounds__(256) void os_f16_kernel(const int32_t *__restrict__ map, int64_t T, int Kc,
-                                                     const _Float16 *__restrict__ X, int Cin,
-                                                     const _Float16 *__restrict__ WT, int Cout, void *Y) {
-  constexpr int BN = 32 * WN;
-  __shared__ __align__(16) _Float16 Bs[BN * kBStride];
-  __shared__ int64_t orow_s[4][32];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 31, kh = lane >> 5;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave * 32;
-  const int n0 = blockIdx.y * BN;
-  const int64_t t = t0 + r;
-  const bool tvalid = t < T;
-  floatx16 acc[WN];
-#pragma unroll
-  for (int wn = 0; wn < WN; ++wn)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[wn][i] = 0.f;
+#define SPIRA_RING_STAGES(C)                          \
+  __shared__ __align__(1024) char st0[C::STAGE];      \
+  __shared__ __align__(1024) char st1[C::STAGE];      \
+  __shared__ __align__(1024) char st2[C::STAGE]
 
-  for (int j = 0; j < Kc; ++j) {
-    const int32_t idx = tvalid ? map[t * Kc + j] : -1;
-    const bool any = ballot(idx >= 0) != 0;
-    const _Float16 *xrow = X + static_cast<int64_t>(idx < 0 ? 0 : idx) * Cin;
-    for (int kc = 0; kc < Cin; kc += kChunk) {
-      __syncthreads();
-      stage_weights<BN>(Bs, WT, j, n0, Cout, kc, Cin);
-      __syncthreads();
-      if (any) mma_chunk<WN>(acc, Bs, xrow, idx >= 0, kc, Cin, r, kh);
+// Output-stationary implicit GEMM.  A block owns BM = 128*MT logical rows
+// (wave w: rows [w*32*MT, (w+1)*32*MT) as MT tiles of 32) and BN = 32*WN
+// output channels; grid = (row blocks, column blocks, offset splits), split z
+// covering offsets [z*jper, min(Kc, (z+1)*jper)).  With `order`, logical row
+// i is target order[i] and `map` holds the rows in logical order; `rowmask`
+// (logical order, bit j = column j valid, bit 63 = some column >= 63 valid)
+// lets the block skip offsets none of its rows uses.
+template <int WN, int MT, int MODE, bool ALIGNED>
+__global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ map,
+                                                    const int32_t *__restrict__ order,
+                                                    const uint64_t *__restrict__ rowmask, int64_t T, int Kc, int jper,
+                                                    const _Float16 *__restrict__ X, int Cin, int CinP,
+                                                    const _Float16 *__restrict__ WT, int Cout, int CoutP, void *Y,
+                                                    Epilogue epi) {
+  using C = ring::Cfg<WN, MT>;
+  SPIRA_RING_STAGES(C);
+  __shared__ int32_t act[65];
+  __shared__ unsigned flag[2];
+  __shared__ int32_t orow_s[4][32 * MT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, kh = lane >> 5;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * C::BM;
+  const int n0 = blockIdx.y * C::BN;
+  const int j0 = blockIdx.z * jper;
+  const int j1 = (j0 + jper) < Kc ? (j0 + jper) : Kc;
+  const int jn = j1 - j0;
+  // offsets used by some row of the block
+  if (tid < 2) flag[tid] = 0;
+  __syncthreads();
+  if (rowmask && Kc <= 63) {
+    uint64_t used = 0;
+    for (int rr = tid; rr < C::BM; rr += 256) {
+      const int64_t lr = row0 + rr;
+      if (lr < T) used |= rowmask[lr];
+    }
+    used = (used >> j0) & (jn >= 64 ? ~uint64_t(0) : ((uint64_t(1) << jn) - 1));
+    if (used) {
+      atomicOr(&flag[0], static_cast<unsigned>(used));
+      atomicOr(&flag[1], static_cast<unsigned>(used >> 32));
+    }
+  } else if (tid == 0) {
+    const uint64_t all = jn >= 64 ? ~uint64_t(0) : ((uint64_t(1) << jn) - 1);
+    flag[0] = static_cast<unsigned>(all);
+    flag[1] = static_cast<unsigned>(all >> 32);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t used = static_cast<uint64_t>(flag[0]) | (static_cast<uint64_t>(flag[1]) << 32);
+    int n = 0;
+    while (used) {
+      act[n++] = j0 + __builtin_ctzll(used);
+      used &= used - 1;
+    }
+    act[64] = n;
+  }
+  __syncthreads();
+  const int nact = act[64];
+  const int nch = (CinP + ring::KC - 1) / ring::KC;
+
+  floatx16 acc[MT][WN];
+  zero_acc<WN, MT>(acc);
+  bool mvalid[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) mvalid[m] = row0 + wave * 32 * MT + m * 32 + r < T;
+  // Map entries of step u: lane L of a wave fetches row L (MT = 2) or row
+  // L % 32 (MT = 1) of the wave's rows into the stage's index slot; rows past
+  // T fetch row 0 and are masked when resolved.  Every address stays inside
+  // map: the row is < T (or 0) and the column < Kc.
+  const int nsteps = nact * nch;
+  const int frow = MT == 2 ? lane : r;
+  const int64_t flr = row0 + wave * 32 * MT + frow;
+  const int32_t *fptr = map + (flr < T ? flr * Kc : 0);
+  auto fetch = [&](int u, char *st) {
+    // act[] holds nact entries (possibly none): steps past the end read column 0
+    const int j = u < nsteps ? act[u / nch] : 0;
+    __builtin_amdgcn_global_load_lds((gbl_void_t *)(const_cast<int32_t *>(fptr + j)),
+                                     (lds_void_t *)(st + C::IDX_OFF + wave * 256), 4, 0, 0);
+  };
+  auto resolve = [&](int u, const char *st, int32_t (&idx)[MT], int64_t &wrow, int &kb) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) idx[m] = ring::lds_read4(st + C::IDX_OFF + wave * 256 + (m * 32 + r) * 4);
+    ring::lds_wait();
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      ring::pin(idx[m]);
+      if (!mvalid[m]) idx[m] = -1;
+    }
+    wrow = act[u / nch];
+    kb = (u % nch) * ring::KC;
+  };
+  ring::run<WN, MT, ALIGNED, 1>(acc, nsteps, fetch, resolve, X, Cin, CinP, WT, n0, CoutP, st0, st1, st2);
+  if (kh == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int64_t lr = row0 + wave * 32 * MT + m * 32 + r;
+      orow_s[wave][m * 32 + r] = lr < T ? (order ? order[lr] : static_cast<int32_t>(lr)) : -1;
     }
   }
-  if (kh == 0) orow_s[wave][r] = tvalid ? t : -1;
   __syncthreads();
-  store_tile<WN, MODE>(acc, orow_s[wave], n0, Cout, r, kh, Y);
+#pragma unroll
+  for (int m = 0; m < MT; ++m) store_tile<WN, MODE>(acc[m], orow_s[wave] + m * 32, n0, Cout, r, kh, Y, epi);
 }
 
-// Fused weight-stationary tile over 128 consecutive pairs of one offset row.
-// Tiles [0, nfwd) use (in -> out) with W[woffset + r]; with `mirror`, tiles
-// [nfwd, 2 nfwd) use (out -> in) with W[woffset + Kw-1-r], skipping a
-// self-mirrored centre row.  Results are atomically added to an fp32 buffer.
-template <int WN>
-__global__ __launch_bounds__(256) void ws_fused_f16_kernel(const int32_t *__restrict__ in_idx,
-                                                           const int32_t *__restrict__ out_idx,
-                                                           const int32_t *__restrict__ naddrs,
-                                                           const int32_t *__restrict__ qnaddrs, int R, int64_t nfwd,
-                                                           int Kw, int woffset, const _Float16 *__restrict__ X,
-                                                           int Cin, const _Float16 *__restrict__ WT, int Cout,
-                                                           float *__restrict__ Yacc) {
-  constexpr int BN = 32 * WN;
-  __shared__ __align__(16) _Float16 Bs[BN * kBStride];
-  __shared__ int64_t orow_s[4][32];
+// Fused weight-stationary pass.  Rows of the pair list are tiled per
+// compacted offset row in blocks of BM pairs (the tile table is rebuilt in
+// LDS from naddrs); tiles [0, nfwd) apply (in -> out) with W[woffset + r],
+// with Kw > 0 tiles [nfwd, 2 nfwd) apply the mirrored pass (out -> in) with
+// W[woffset + Kw-1-r] except for a self-mirrored centre row.  Results are
+// atomically added to an fp32 buffer.
+template <int WN, int MT, bool ALIGNED>
+__global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ in_idx,
+                                                    const int32_t *__restrict__ out_idx,
+                                                    const int32_t *__restrict__ naddrs, int R, int64_t nfwd, int Kw,
+                                                    int woffset, const _Float16 *__restrict__ X, int Cin, int CinP,
+                                                    const _Float16 *__restrict__ WT, int Cout, int CoutP,
+                                                    float *__restrict__ Yacc) {
+  using C = ring::Cfg<WN, MT>;
+  SPIRA_RING_STAGES(C);
+  __shared__ int32_t tstart[kMaxGroups + 1];
+  __shared__ int32_t orow_s[4][32 * MT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, kh = lane >> 5;
+  // tile starts per compacted row: exclusive scan of ceil(rows / BM), R <= 128
+  {
+    int cnt = 0;
+    if (tid < R) cnt = (naddrs[tid + 1] - naddrs[tid] + C::BM - 1) / C::BM;
+    if (tid < kMaxGroups + 1) tstart[tid] = cnt;
+    __syncthreads();
+    for (int off = 1; off < kMaxGroups + 1; off <<= 1) {
+      const int v = (tid < kMaxGroups + 1 && tid >= off) ? tstart[tid - off] : 0;
+      __syncthreads();
+      if (tid < kMaxGroups + 1) tstart[tid] += v;
+      __syncthreads();
+    }
+    const int incl = tid < kMaxGroups + 1 ? tstart[tid] : 0;
+    __syncthreads();
+    if (tid < kMaxGroups + 1) tstart[tid] = incl - (tid < R ? cnt : 0);
+    __syncthreads();
+  }
   int64_t tile = blockIdx.x;
   const bool mir = tile >= nfwd;
   if (mir) tile -= nfwd;
-  const int64_t pos = tile * kRowsPerBlock;
-  // row r: last r with qnaddrs[r] <= pos
-  int lo = 0, hi = R;
+  int lo = 0, hi = R;  // last row with tstart[row] <= tile
   while (hi - lo > 1) {
-    int m = (lo + hi) >> 1;
-    if (qnaddrs[m] <= pos) lo = m;
-    else hi = m;
+    const int md = (lo + hi) >> 1;
+    if (tstart[md] <= tile) lo = md;
+    else hi = md;
   }
   const int row = lo;
-  if (mir && 2 * row + 1 == Kw) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 31, kh = lane >> 5;
-  const int64_t local = pos - qnaddrs[row] + wave * 32 + r;
+  if (tile >= tstart[R] || (mir && 2 * row + 1 == Kw)) return;  // block-uniform
   const int64_t nrow = naddrs[row + 1] - naddrs[row];
-  const bool valid = local < nrow;
-  const int64_t p = naddrs[row] + local;
-  const int32_t src = valid ? (mir ? out_idx[p] : in_idx[p]) : -1;
-  const int32_t dst = valid ? (mir ? in_idx[p] : out_idx[p]) : -1;
-  const int64_t wrow = woffset + (mir ? Kw - 1 - row : row);
-  const int n0 = blockIdx.y * BN;
-  floatx16 acc[WN];
+  int32_t src[MT], dst[MT];
 #pragma unroll
-  for (int wn = 0; wn < WN; ++wn)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[wn][i] = 0.f;
-  const bool any = ballot(src >= 0) != 0;
-  const _Float16 *xrow = X + static_cast<int64_t>(src < 0 ? 0 : src) * Cin;
-  for (int kc = 0; kc < Cin; kc += kChunk) {
-    __syncthreads();
-    stage_weights<BN>(Bs, WT, wrow, n0, Cout, kc, Cin);
-    __syncthreads();
-    if (any) mma_chunk<WN>(acc, Bs, xrow, src >= 0, kc, Cin, r, kh);
+  for (int m = 0; m < MT; ++m) {
+    const int64_t local = (tile - tstart[row]) * C::BM + wave * 32 * MT + m * 32 + r;
+    const bool valid = local < nrow;
+    const int64_t p = naddrs[row] + local;
+    src[m] = valid ? (mir ? out_idx[p] : in_idx[p]) : -1;
+    dst[m] = valid ? (mir ? in_idx[p] : out_idx[p]) : -1;
   }
-  if (kh == 0) orow_s[wave][r] = dst;
+  const int64_t wrow0 = woffset + (mir ? Kw - 1 - row : row);
+  const int n0 = blockIdx.y * C::BN;
+  floatx16 acc[MT][WN];
+  zero_acc<WN, MT>(acc);
+  auto fetch = [](int, char *) {};
+  auto resolve = [&](int u, const char *, int32_t (&idx)[MT], int64_t &wrow, int &kb) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) idx[m] = src[m];
+    wrow = wrow0;
+    kb = u * ring::KC;
+  };
+  const int nch = (CinP + ring::KC - 1) / ring::KC;
+  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, X, Cin, CinP, WT, n0, CoutP, st0, st1, st2);
+  if (kh == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = dst[m];
+  }
   __syncthreads();
-  store_tile<WN, kAtomicF32>(acc, orow_s[wave], n0, Cout, r, kh, Yacc);
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    store_tile<WN, kAtomicF32>(acc[m], orow_s[wave] + m * 32, n0, Cout, r, kh, Yacc, Epilogue{});
 }
 
 struct GroupTable {
-  int n;                          // groups
-  int64_t tile_start[kMaxGroups + 1];  // prefix of 128-row tiles
-  int64_t row_off[kMaxGroups];    // first buffer row of the group
-  int32_t rows[kMaxGroups];       // valid rows of the group
+  int n;                               // groups
+  int64_t tile_start[kMaxGroups + 1];  // prefix of row tiles
+  int64_t row_off[kMaxGroups];         // first buffer row of the group
+  int32_t rows[kMaxGroups];            // valid rows of the group
 };
 
-// Grouped GEMM over the padded gather buffer: Ybuf[g rows] = Xbuf[g rows] @ W[g].
-template <int WN>
-__global__ __launch_bounds__(256) void group_gemm_f16_kernel(const GroupTable gt, const _Float16 *__restrict__ Xb,
-                                                             int Cin, const _Float16 *__restrict__ WT, int Cout,
-                                                             float *__restrict__ Yb) {
-  constexpr int BN = 32 * WN;
-  __shared__ __align__(16) _Float16 Bs[BN * kBStride];
-  __shared__ int64_t orow_s[4][32];
+// Grouped GEMM over the padded gather buffer: Ybuf[rows of g] = Xbuf[rows of g] @ W[g].
+template <int WN, int MT, bool ALIGNED>
+__global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, const _Float16 *__restrict__ Xb, int Cin,
+                                                    int CinP, const _Float16 *__restrict__ WT, int Cout, int CoutP,
+                                                    float *__restrict__ Yb) {
+  using C = ring::Cfg<WN, MT>;
+  SPIRA_RING_STAGES(C);
+  __shared__ int32_t orow_s[4][32 * MT];
   const int64_t tile = blockIdx.x;
-  int g = 0;
-  while (g + 1 < gt.n && gt.tile_start[g + 1] <= tile) ++g;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 31, kh = lane >> 5;
-  const int64_t local = (tile - gt.tile_start[g]) * kRowsPerBlock + wave * 32 + r;
-  const bool valid = local < gt.rows[g];
-  const int64_t brow = gt.row_off[g] + local;
-  const int n0 = blockIdx.y * BN;
-  floatx16 acc[WN];
-#pragma unroll
-  for (int wn = 0; wn < WN; ++wn)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[wn][i] = 0.f;
-  const bool any = ballot(valid) != 0;
-  const _Float16 *xrow = Xb + (valid ? brow : 0) * Cin;
-  for (int kc = 0; kc < Cin; kc += kChunk) {
-    __syncthreads();
-    stage_weights<BN>(Bs, WT, g, n0, Cout, kc, Cin);
-    __syncthreads();
-    if (any) mma_chunk<WN>(acc, Bs, xrow, valid, kc, Cin, r, kh);
+  int g = 0, ghi = gt.n;  // last group with tile_start[g] <= tile
+  while (ghi - g > 1) {
+    const int md = (g + ghi) >> 1;
+    if (gt.tile_start[md] <= tile) g = md;
+    else ghi = md;
   }
-  if (kh == 0) orow_s[wave][r] = valid ? brow : -1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, kh = lane >> 5;
+  int32_t src[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int64_t local = (tile - gt.tile_start[g]) * C::BM + wave * 32 * MT + m * 32 + r;
+    src[m] = local < gt.rows[g] ? static_cast<int32_t>(gt.row_off[g] + local) : -1;
+  }
+  const int n0 = blockIdx.y * C::BN;
+  floatx16 acc[MT][WN];
+  zero_acc<WN, MT>(acc);
+  auto fetch = [](int, char *) {};
+  auto resolve = [&](int u, const char *, int32_t (&idx)[MT], int64_t &wrow, int &kb) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) idx[m] = src[m];
+    wrow = g;
+    kb = u * ring::KC;
+  };
+  const int nch = (CinP + ring::KC - 1) / ring::KC;
+  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, Xb, Cin, CinP, WT, n0, CoutP, st0, st1, st2);
+  if (kh == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = src[m];
+  }
   __syncthreads();
-  store_tile<WN, kStoreF32>(acc, orow_s[wave], n0, Cout, r, kh, Yb);
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    store_tile<WN, kStoreF32>(acc[m], orow_s[wave] + m * 32, n0, Cout, r, kh, Yb, Epilogue{});
 }
 
 // ---------------------------------------------------------------------------
-// generic (any channel count, fp32 or fp16 storage) kernels, fp32 accumulate
-// ---------------------------------------------------------------------------
+// // element-wise helpers
 template <typename FT> __device__ __forceinline__ float ld(const FT *p) { return static_cast<float>(*p); }
 
+// [K, Cin, Cout] -> zero-padded [K, CoutP, CinP]
+__global__ void prepare_w_kernel(const _Float16 *__restrict__ W, int K, int Cin, int Cout, int CinP, int CoutP,
+                                 _Float16 *__restrict__ WT) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t n = static_cast<int64_t>(K) * CoutP * CinP;
+  if (i >= n) return;
+  const int64_t k = i / (static_cast<int64_t>(CoutP) * CinP);
+  const int64_t rem = i % (static_cast<int64_t>(CoutP) * CinP);
+  const int co = static_cast<int>(rem / CinP), ci = static_cast<int>(rem % CinP);
+  WT[i] = (co < Cout && ci < Cin) ? W[(k * Cin + ci) * Cout + co] : static_cast<_Float16>(0.f);
+}
+
+// fp32 partial sums -> storage dtype, with the optional epilogue
+template <typename FT>
+__global__ void finalize_kernel(const float *__restrict__ acc, int64_t T, int Cout, FT *__restrict__ Y,
+                                Epilogue epi) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= T * Cout) return;
+  const int c = static_cast<int>(i % Cout);
+  float v = acc[i];
+  if (epi.scale) v *= epi.scale[c];
+  if (epi.shift) v += epi.shift[c];
+  if (epi.residual) v += ld(static_cast<const FT *>(epi.residual) + i);
+  if (epi.relu) v = v > 0.f ? v : 0.f;
+  Y[i] = static_cast<FT>(v);
+}
+
+__global__ void fill_f32_kernel(float *__restrict__ p, int64_t n, float v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// generic (fp32 storage) kernels, fp32 accumulate
 template <typename FT, int MODE>
 __device__ __forceinline__ void put(void *Y, int64_t i, float v) {
   if constexpr (MODE == kStoreNative) static_cast<FT *>(Y)[i] = static_cast<FT>(v);
@@ -252,18 +586,28 @@ __device__ __forceinline__ void put(void *Y, int64_t i, float v) {
 template <typename FT, int MODE>
 __global__ __launch_bounds__(256) void os_generic_kernel(const int32_t *__restrict__ map, int64_t T, int Kc,
                                                          const FT *__restrict__ X, int Cin,
-                                                         const FT *__restrict__ W, int Cout, void *Y) {
+                                                         const FT *__restrict__ W, int Cout, void *Y, Epilogue epi) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= T * Cout) return;
   const int64_t t = i / Cout;
   const int c = static_cast<int>(i % Cout);
+  // two-level sum (per offset, then across offsets) keeps the fp32 rounding
+  // error at O((Cin + K) eps) instead of O(Cin K eps)
   float acc = 0.f;
   for (int j = 0; j < Kc; ++j) {
     const int32_t s = map[t * Kc + j];
     if (s < 0) continue;
     const FT *x = X + static_cast<int64_t>(s) * Cin;
     const FT *w = W + (static_cast<int64_t>(j) * Cin) * Cout + c;
-    for (int ci = 0; ci < Cin; ++ci) acc += ld(x + ci) * ld(w + static_cast<int64_t>(ci) * Cout);
+    float part = 0.f;
+    for (int ci = 0; ci < Cin; ++ci) part = fmaf(ld(x + ci), ld(w + static_cast<int64_t>(ci) * Cout), part);
+    acc += part;
+  }
+  if constexpr (MODE == kStoreNative) {
+    if (epi.scale) acc *= epi.scale[c];
+    if (epi.shift) acc += epi.shift[c];
+    if (epi.residual) acc += ld(static_cast<const FT *>(epi.residual) + i);
+    if (epi.relu) acc = acc > 0.f ? acc : 0.f;
   }
   put<FT, MODE>(Y, i, acc);
 }
@@ -272,12 +616,11 @@ template <typename FT>
 __global__ __launch_bounds__(256) void ws_fused_generic_kernel(const int32_t *__restrict__ in_idx,
                                                                const int32_t *__restrict__ out_idx,
                                                                const int32_t *__restrict__ naddrs, int R, int Kw,
-                                                               int woffset, int mirror, int64_t P,
-                                                               const FT *__restrict__ X, int Cin,
-                                                               const FT *__restrict__ W, int Cout,
+                                                               int woffset, int64_t P, const FT *__restrict__ X,
+                                                               int Cin, const FT *__restrict__ W, int Cout,
                                                                float *__restrict__ Yacc) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t passes = mirror ? 2 : 1;
+  const int64_t passes = Kw > 0 ? 2 : 1;
   if (i >= passes * P * Cout) return;
   int64_t p = i / Cout;
   const int c = static_cast<int>(i % Cout);
@@ -285,7 +628,7 @@ __global__ __launch_bounds__(256) void ws_fused_generic_kernel(const int32_t *__
   if (mir) p -= P;
   int lo = 0, hi = R;
   while (hi - lo > 1) {
-    int m = (lo + hi) >> 1;
+    const int m = (lo + hi) >> 1;
     if (naddrs[m] <= p) lo = m;
     else hi = m;
   }
@@ -297,7 +640,7 @@ __global__ __launch_bounds__(256) void ws_fused_generic_kernel(const int32_t *__
   const FT *x = X + static_cast<int64_t>(s) * Cin;
   const FT *w = W + wrow * Cin * Cout + c;
   float acc = 0.f;
-  for (int ci = 0; ci < Cin; ++ci) acc += ld(x + ci) * ld(w + static_cast<int64_t>(ci) * Cout);
+  for (int ci = 0; ci < Cin; ++ci) acc = fmaf(ld(x + ci), ld(w + static_cast<int64_t>(ci) * Cout), acc);
   atomicAdd(Yacc + static_cast<int64_t>(d) * Cout + c, acc);
 }
 
@@ -316,7 +659,7 @@ __global__ __launch_bounds__(256) void group_gemm_generic_kernel(const GroupTabl
   const FT *x = Xb + brow * Cin;
   const FT *w = W + static_cast<int64_t>(g) * Cin * Cout + c;
   float acc = 0.f;
-  for (int ci = 0; ci < Cin; ++ci) acc += ld(x + ci) * ld(w + static_cast<int64_t>(ci) * Cout);
+  for (int ci = 0; ci < Cin; ++ci) acc = fmaf(ld(x + ci), ld(w + static_cast<int64_t>(ci) * Cout), acc);
   Yb[i] = acc;
 }
 
@@ -357,7 +700,7 @@ __global__ __launch_bounds__(256) void gather_h8_kernel(const OffsetTable ot, in
   }
 }
 
-// scatter: Y[t] (+)= sum_k buf[off[k] + mask[k, t]]
+// scatter: Y[t] = base[t] + sum_k buf[off[k] + mask[k, t]]
 template <typename FT>
 __global__ __launch_bounds__(256) void scatter_kernel(const OffsetTable ot, int64_t T, int Cout,
                                                       const int32_t *__restrict__ tmask,
@@ -375,70 +718,149 @@ __global__ __launch_bounds__(256) void scatter_kernel(const OffsetTable ot, int6
   Y[i] = static_cast<FT>(acc);
 }
 
-template <typename FT>
-__global__ void cast_f32_kernel(const float *__restrict__ src, int64_t n, FT *__restrict__ dst) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) dst[i] = static_cast<FT>(src[i]);
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static inline bool mfma_path(int dtype) { return dtype == SPIRA_F16; }
+static inline int pad_in(int c) { return static_cast<int>(round_up(c, 16)); }
+static inline int pad_out(int c) { return static_cast<int>(round_up(c, 32)); }
+
+static inline int wn_for(int Cout) {
+  if (Cout <= 32) return 1;
+  if (Cout <= 64) return 2;
+  if (Cout <= 96) return 3;
+  if (Cout <= 128) return 4;
+  return 8;
+}
+// 32-row tiles per wave: accumulators stay <= 128 VGPRs
+template <int WN> struct MtOf { static constexpr int value = WN >= 8 ? 1 : 2; };
+static inline int mt_for(int wn) { return wn >= 8 ? 1 : 2; }
+
+// offsets per split: small layers split their offsets so that the grid
+// covers the chip; a split never exceeds 64 offsets (the active-offset list)
+static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
+  int jper = Kc;
+  const int64_t want = static_cast<int64_t>(cus);
+  if (blocks_xy < want && Kc > 1) {
+    const int64_t splits = std::min<int64_t>(Kc, div_up(want, blocks_xy));
+    jper = static_cast<int>(div_up(Kc, splits));
+  }
+  return std::min(jper, 64);
 }
 
-// [K, Cin, Cout] -> [K, Cout, Cin]
-__global__ void transpose_w_kernel(const _Float16 *__restrict__ W, int K, int Cin, int Cout,
-                                   _Float16 *__restrict__ WT) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t n = static_cast<int64_t>(K) * Cin * Cout;
-  if (i >= n) return;
-  const int64_t k = i / (static_cast<int64_t>(Cin) * Cout);
-  const int64_t rem = i % (static_cast<int64_t>(Cin) * Cout);
-  const int ci = static_cast<int>(rem / Cout), co = static_cast<int>(rem % Cout);
-  WT[(k * Cout + co) * Cin + ci] = W[i];
+template <int WN, int MODE, bool AL>
+static void launch_os_wn(dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order, const uint64_t *rowmask,
+                         int64_t T, int Kc, int jper, const void *X, int Cin, int CinP, const void *WT, int Cout,
+                         int CoutP, void *Y, const Epilogue &epi) {
+  hipLaunchKernelGGL((os_kernel<WN, MtOf<WN>::value, MODE, AL>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc,
+                     jper, static_cast<const _Float16 *>(X), Cin, CinP, static_cast<const _Float16 *>(WT), Cout, CoutP,
+                     Y, epi);
 }
 
-// ---------------------------------------------------------------------------
-// host helpers
-// ---------------------------------------------------------------------------
-static inline bool mfma_ok(int dtype, int Cin) { return dtype == SPIRA_F16 && Cin % 8 == 0; }
-
-static inline int wn_for(int Cout) { return Cout <= 32 ? 1 : (Cout <= 64 ? 2 : 4); }
-
-static size_t wt_bytes(int K, int Cin, int Cout) { return static_cast<size_t>(K) * Cin * Cout * sizeof(_Float16); }
-
-static int transpose_weights(const void *W, int K, int Cin, int Cout, void *WT, hipStream_t s) {
-  const int64_t n = static_cast<int64_t>(K) * Cin * Cout;
-  if (n == 0) return kOk;
-  hipLaunchKernelGGL(transpose_w_kernel, dim3(div_up(n, 256)), dim3(256), 0, s, static_cast<const _Float16 *>(W), K,
-                     Cin, Cout, static_cast<_Float16 *>(WT));
-  SPIRA_HIP_LAUNCH_CHECK();
-  return kOk;
+template <int MODE, bool AL>
+static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
+                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const void *X, int Cin, int CinP,
+                      const void *WT, int Cout, int CoutP, void *Y, const Epilogue &epi) {
+#define SPIRA_OS_CASE(W)                                                                                         \
+  case W:                                                                                                        \
+    launch_os_wn<W, MODE, AL>(grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi); \
+    break;
+  switch (wn) {
+    SPIRA_OS_CASE(1)
+    SPIRA_OS_CASE(2)
+    SPIRA_OS_CASE(3)
+    SPIRA_OS_CASE(4)
+    default:
+      launch_os_wn<8, MODE, AL>(grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi);
+  }
+#undef SPIRA_OS_CASE
 }
 
 template <int MODE>
-static void launch_os_f16(int wn, dim3 grid, hipStream_t s, const int32_t *map, int64_t T, int Kc, const void *X,
-                          int Cin, const void *WT, int Cout, void *Y) {
-  auto x = static_cast<const _Float16 *>(X);
-  auto wt = static_cast<const _Float16 *>(WT);
-  if (wn == 1) hipLaunchKernelGGL((os_f16_kernel<1, MODE>), grid, dim3(256), 0, s, map, T, Kc, x, Cin, wt, Cout, Y);
-  else if (wn == 2) hipLaunchKernelGGL((os_f16_kernel<2, MODE>), grid, dim3(256), 0, s, map, T, Kc, x, Cin, wt, Cout, Y);
-  else hipLaunchKernelGGL((os_f16_kernel<4, MODE>), grid, dim3(256), 0, s, map, T, Kc, x, Cin, wt, Cout, Y);
+static void launch_os_any(bool aligned, int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
+                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const void *X, int Cin, int CinP,
+                          const void *WT, int Cout, int CoutP, void *Y, const Epilogue &epi) {
+  if (aligned)
+    launch_os<MODE, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi);
+  else
+    launch_os<MODE, false>(wn, grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi);
+}
+
+template <int WN, bool AL>
+static void launch_ws_wn(dim3 grid, hipStream_t s, const int32_t *in_idx, const int32_t *out_idx,
+                         const int32_t *naddrs, int R, int64_t nfwd, int Kw, int woffset, const void *X, int Cin,
+                         int CinP, const void *WT, int Cout, int CoutP, float *Yacc) {
+  hipLaunchKernelGGL((ws_kernel<WN, MtOf<WN>::value, AL>), grid, dim3(256), 0, s, in_idx, out_idx, naddrs, R, nfwd,
+                     Kw, woffset, static_cast<const _Float16 *>(X), Cin, CinP, static_cast<const _Float16 *>(WT), Cout,
+                     CoutP, Yacc);
+}
+
+template <bool AL>
+static void launch_ws(int wn, dim3 grid, hipStream_t s, const int32_t *in_idx, const int32_t *out_idx,
+                      const int32_t *naddrs, int R, int64_t nfwd, int Kw, int woffset, const void *X, int Cin,
+                      int CinP, const void *WT, int Cout, int CoutP, float *Yacc) {
+  switch (wn) {
+    case 1: launch_ws_wn<1, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
+    case 2: launch_ws_wn<2, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
+    case 3: launch_ws_wn<3, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
+    case 4: launch_ws_wn<4, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
+    default: launch_ws_wn<8, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
+  }
+}
+
+template <int WN, bool AL>
+static void launch_gg_wn(dim3 grid, hipStream_t s, const GroupTable &gt, const void *X, int Cin, int CinP,
+                         const void *WT, int Cout, int CoutP, float *Yb) {
+  hipLaunchKernelGGL((gg_kernel<WN, MtOf<WN>::value, AL>), grid, dim3(256), 0, s, gt, static_cast<const _Float16 *>(X),
+                     Cin, CinP, static_cast<const _Float16 *>(WT), Cout, CoutP, Yb);
+}
+
+template <bool AL>
+static void launch_gg(int wn, dim3 grid, hipStream_t s, const GroupTable &gt, const void *X, int Cin, int CinP,
+                      const void *WT, int Cout, int CoutP, float *Yb) {
+  switch (wn) {
+    case 1: launch_gg_wn<1, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
+    case 2: launch_gg_wn<2, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
+    case 3: launch_gg_wn<3, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
+    case 4: launch_gg_wn<4, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
+    default: launch_gg_wn<8, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
+  }
 }
 
 template <typename FT, int MODE>
 static void launch_os_generic(hipStream_t s, const int32_t *map, int64_t T, int Kc, const void *X, int Cin,
-                              const void *W, int Cout, void *Y) {
+                              const void *W, int Cout, void *Y, const Epilogue &epi) {
   const int64_t n = T * Cout;
   hipLaunchKernelGGL((os_generic_kernel<FT, MODE>), dim3(div_up(n, 256)), dim3(256), 0, s, map, T, Kc,
-                     static_cast<const FT *>(X), Cin, static_cast<const FT *>(W), Cout, Y);
+                     static_cast<const FT *>(X), Cin, static_cast<const FT *>(W), Cout, Y, epi);
 }
 
-static int fill_groups(GroupTable &gt, int K, const int32_t *rows, const int64_t *row_off) {
+static int fill_groups(GroupTable &gt, int K, const int32_t *rows, const int64_t *row_off, int bm) {
   SPIRA_HIP_REQUIRE(K <= kMaxGroups, "at most 128 kernel offsets are supported");
   gt.n = K;
   gt.tile_start[0] = 0;
   for (int k = 0; k < K; ++k) {
     gt.rows[k] = rows[k];
     gt.row_off[k] = row_off[k];
-    gt.tile_start[k + 1] = gt.tile_start[k] + div_up(rows[k], kRowsPerBlock);
+    gt.tile_start[k + 1] = gt.tile_start[k] + div_up(rows[k], bm);
   }
   return kOk;
+}
+
+static int fill_f32(float *p, int64_t n, float v, hipStream_t s) {
+  if (n <= 0) return kOk;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(div_up(n, 256)), dim3(256), 0, s, p, n, v);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+static Epilogue make_epi(const float *scale, const float *shift, const void *residual, int relu) {
+  Epilogue e;
+  e.scale = scale;
+  e.shift = shift;
+  e.residual = residual;
+  e.relu = relu;
+  return e;
 }
 
 }  // namespace spira_hip
@@ -447,53 +869,100 @@ using namespace spira_hip;
 
 extern "C" {
 
-int spira_hip_conv_workspace(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes) {
-  *bytes = mfma_ok(dtype, c_in) ? wt_bytes(num_offsets, c_in, c_out) : 0;
+int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes) {
+  *bytes = mfma_path(dtype) ? static_cast<size_t>(num_offsets) * pad_in(c_in) * pad_out(c_out) * sizeof(_Float16) : 0;
   return kOk;
 }
 
-int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const void *sources,
-                      int64_t num_sources, int c_in, const void *weights, int c_out, int dtype, void *targets,
-                      int out_mode, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, int c_out, int dtype, void *prepared,
+                              hipStream_t stream) {
+  if (!mfma_path(dtype)) return kOk;
+  const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
+  const int64_t n = static_cast<int64_t>(num_offsets) * CinP * CoutP;
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(prepare_w_kernel, dim3(div_up(n, 256)), dim3(256), 0, stream,
+                     static_cast<const _Float16 *>(weights), num_offsets, c_in, c_out, CinP, CoutP,
+                     static_cast<_Float16 *>(prepared));
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
+                                size_t *bytes) {
+  (void)c_in;
+  *bytes = 0;
+  if (!mfma_path(dtype) || out_mode != SPIRA_OUT_STORE || num_targets <= 0) return kOk;
+  const int wn = wn_for(c_out);
+  const int bm = 128 * mt_for(wn);
+  const int64_t blocks = div_up(num_targets, bm) * div_up(pad_out(c_out), 32 * wn);
+  if (choose_jper(blocks, num_offsets, device_cu_count()) < num_offsets)
+    *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
+  return kOk;
+}
+
+int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
+                      const uint64_t *row_masks, const void *sources,
+                      int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
+                      void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
+                      int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
   (void)num_sources;
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_os: dtype must be fp16 or fp32");
   SPIRA_HIP_REQUIRE(out_mode >= SPIRA_OUT_STORE && out_mode <= SPIRA_OUT_ADD_F32, "conv_os: bad out_mode");
   SPIRA_HIP_REQUIRE(c_in > 0 && c_out > 0 && num_offsets > 0, "conv_os: empty channel / offset dimension");
+  SPIRA_HIP_REQUIRE(out_mode == SPIRA_OUT_STORE || (!scale && !shift && !residual && !relu),
+                    "conv_os: the epilogue applies to the storage-dtype output only");
   if (num_targets <= 0) return kOk;
-  // out_mode: 0 = store in dtype, 1 = store fp32, 2 = add into fp32
-  if (mfma_ok(dtype, c_in)) {
-    SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= wt_bytes(num_offsets, c_in, c_out),
-                      "conv_os: workspace too small");
-    int rc = transpose_weights(weights, num_offsets, c_in, c_out, workspace, stream);
-    if (rc) return rc;
+  const Epilogue epi = make_epi(scale, shift, residual, relu);
+  if (mfma_path(dtype)) {
+    SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
+    const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
     const int wn = wn_for(c_out);
-    dim3 grid(static_cast<unsigned>(div_up(num_targets, kRowsPerBlock)), static_cast<unsigned>(div_up(c_out, 32 * wn)));
-    if (out_mode == SPIRA_OUT_STORE)
-      launch_os_f16<kStoreNative>(wn, grid, stream, out_in_map, num_targets, num_offsets, sources, c_in, workspace,
-                                c_out, targets);
-    else if (out_mode == SPIRA_OUT_STORE_F32)
-      launch_os_f16<kStoreF32>(wn, grid, stream, out_in_map, num_targets, num_offsets, sources, c_in, workspace,
-                               c_out, targets);
-    else
-      launch_os_f16<kAddF32>(wn, grid, stream, out_in_map, num_targets, num_offsets, sources, c_in, workspace,
-                             c_out, targets);
-  } else if (dtype == SPIRA_F16) {
-    if (out_mode == SPIRA_OUT_STORE)
-      launch_os_generic<_Float16, kStoreNative>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights,
-                                              c_out, targets);
-    else if (out_mode == SPIRA_OUT_STORE_F32)
-      launch_os_generic<_Float16, kStoreF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights,
-                                             c_out, targets);
-    else
-      launch_os_generic<_Float16, kAddF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights,
-                                           c_out, targets);
+    const int bm = 128 * mt_for(wn);
+    const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
+    const int jper = choose_jper(bx * by, num_offsets, device_cu_count());
+    const int splits = static_cast<int>(div_up(num_offsets, jper));
+    dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(by), static_cast<unsigned>(splits));
+    const bool al = c_in % 8 == 0;
+    if (splits == 1) {
+      if (out_mode == SPIRA_OUT_STORE)
+        launch_os_any<kStoreNative>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in,
+                                    CinP, prepared, c_out, CoutP, targets, epi);
+      else if (out_mode == SPIRA_OUT_STORE_F32)
+        launch_os_any<kStoreF32>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in,
+                                 CinP, prepared, c_out, CoutP, targets, epi);
+      else
+        launch_os_any<kAddF32>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in, CinP,
+                               prepared, c_out, CoutP, targets, epi);
+    } else {
+      float *acc = nullptr;
+      if (out_mode == SPIRA_OUT_STORE) {
+        SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= static_cast<size_t>(num_targets) * c_out * sizeof(float),
+                          "conv_os: workspace too small (spira_hip_conv_os_workspace)");
+        acc = static_cast<float *>(workspace);
+      } else {
+        acc = static_cast<float *>(targets);
+      }
+      if (out_mode != SPIRA_OUT_ADD_F32) {
+        int rc = fill_f32(acc, num_targets * c_out, 0.f, stream);
+        if (rc) return rc;
+      }
+      launch_os_any<kAtomicF32>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in, CinP,
+                                prepared, c_out, CoutP, acc, epi);
+      SPIRA_HIP_LAUNCH_CHECK();
+      if (out_mode == SPIRA_OUT_STORE)
+        hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(num_targets * c_out, 256)), dim3(256), 0, stream,
+                           acc, num_targets, c_out, static_cast<_Float16 *>(targets), epi);
+    }
   } else {
-    if (out_mode == SPIRA_OUT_ADD_F32)
-      launch_os_generic<float, kAddF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out,
-                                        targets);
-    else
+    if (out_mode == SPIRA_OUT_STORE)
       launch_os_generic<float, kStoreNative>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights,
-                                           c_out, targets);
+                                             c_out, targets, epi);
+    else if (out_mode == SPIRA_OUT_STORE_F32)
+      launch_os_generic<float, kStoreF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out,
+                                          targets, epi);
+    else
+      launch_os_generic<float, kAddF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out,
+                                        targets, epi);
   }
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
@@ -502,48 +971,37 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
 int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int32_t *in_idx, const int32_t *out_idx,
                             int rows, const int32_t *naddrs, const int32_t *qnaddrs, int64_t num_pairs,
                             int64_t quantized_pairs, int weight_offset, int mirror_rows, const void *sources,
-                            int c_in, const void *weights, int num_weights, int c_out, int dtype, float *target_acc,
-                            void *workspace,
-                            size_t workspace_bytes, hipStream_t stream) {
+                            int c_in, const void *weights, const void *prepared, int num_weights, int c_out,
+                            int dtype, float *target_acc, hipStream_t stream) {
   (void)num_sources;
   (void)num_targets;
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_ws_fused: dtype must be fp16 or fp32");
   SPIRA_HIP_REQUIRE(rows >= 1 || num_pairs == 0, "conv_ws_fused: rows must be positive");
+  SPIRA_HIP_REQUIRE(weight_offset + std::max(mirror_rows, rows) <= num_weights,
+                    "conv_ws_fused: weight rows out of range");
   if (num_pairs <= 0) return kOk;
-  // mirror_rows = Kw > 0 enables the mirrored pass over Kw offsets; 0 disables it
   const int Kw = mirror_rows;
-  if (mfma_ok(dtype, c_in)) {
-    const int K = num_weights;
-    SPIRA_HIP_REQUIRE(weight_offset + std::max(Kw, rows) <= K, "conv_ws_fused: weight rows out of range");
-    SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= wt_bytes(K, c_in, c_out), "conv_ws_fused: workspace too small");
-    int rc = transpose_weights(weights, K, c_in, c_out, workspace, stream);
-    if (rc) return rc;
+  if (mfma_path(dtype)) {
+    SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_ws_fused: fp16 needs prepared weights");
+    SPIRA_HIP_REQUIRE(rows <= kMaxGroups, "conv_ws_fused: at most 128 offset rows");
+    const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
     const int wn = wn_for(c_out);
-    const int64_t nfwd = quantized_pairs / kRowsPerBlock;
-    dim3 grid(static_cast<unsigned>(Kw > 0 ? 2 * nfwd : nfwd), static_cast<unsigned>(div_up(c_out, 32 * wn)));
-    auto x = static_cast<const _Float16 *>(sources);
-    auto wt = static_cast<const _Float16 *>(workspace);
-    if (wn == 1)
-      hipLaunchKernelGGL((ws_fused_f16_kernel<1>), grid, dim3(256), 0, stream, in_idx, out_idx, naddrs, qnaddrs, rows,
-                         nfwd, Kw, weight_offset, x, c_in, wt, c_out, target_acc);
-    else if (wn == 2)
-      hipLaunchKernelGGL((ws_fused_f16_kernel<2>), grid, dim3(256), 0, stream, in_idx, out_idx, naddrs, qnaddrs, rows,
-                         nfwd, Kw, weight_offset, x, c_in, wt, c_out, target_acc);
+    const int bm = 128 * mt_for(wn);
+    // tiles: sum over rows of ceil(rows_r / bm) <= num_pairs / bm + rows
+    const int64_t nfwd = div_up(num_pairs, bm) + rows;
+    (void)quantized_pairs;
+    dim3 grid(static_cast<unsigned>(Kw > 0 ? 2 * nfwd : nfwd), static_cast<unsigned>(div_up(CoutP, 32 * wn)));
+    if (c_in % 8 == 0)
+      launch_ws<true>(wn, grid, stream, in_idx, out_idx, naddrs, rows, nfwd, Kw, weight_offset, sources, c_in, CinP,
+                      prepared, c_out, CoutP, target_acc);
     else
-      hipLaunchKernelGGL((ws_fused_f16_kernel<4>), grid, dim3(256), 0, stream, in_idx, out_idx, naddrs, qnaddrs, rows,
-                         nfwd, Kw, weight_offset, x, c_in, wt, c_out, target_acc);
+      launch_ws<false>(wn, grid, stream, in_idx, out_idx, naddrs, rows, nfwd, Kw, weight_offset, sources, c_in, CinP,
+                       prepared, c_out, CoutP, target_acc);
   } else {
     const int64_t n = (Kw > 0 ? 2 : 1) * num_pairs * c_out;
-    if (dtype == SPIRA_F16)
-      hipLaunchKernelGGL(ws_fused_generic_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream, in_idx,
-                         out_idx, naddrs, rows, Kw, weight_offset, Kw > 0 ? 1 : 0, num_pairs,
-                         static_cast<const _Float16 *>(sources), c_in, static_cast<const _Float16 *>(weights), c_out,
-                         target_acc);
-    else
-      hipLaunchKernelGGL(ws_fused_generic_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, in_idx, out_idx,
-                         naddrs, rows, Kw, weight_offset, Kw > 0 ? 1 : 0, num_pairs,
-                         static_cast<const float *>(sources), c_in, static_cast<const float *>(weights), c_out,
-                         target_acc);
+    hipLaunchKernelGGL(ws_fused_generic_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, in_idx, out_idx,
+                       naddrs, rows, Kw, weight_offset, num_pairs, static_cast<const float *>(sources), c_in,
+                       static_cast<const float *>(weights), c_out, target_acc);
   }
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
@@ -574,42 +1032,30 @@ int spira_hip_ws_gather(int64_t num_sources, int c_in, int num_offsets, int dtyp
 }
 
 int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padded_offsets, int c_in, int c_out,
-                      int dtype, const void *buffer_in, const void *weights, float *buffer_out, void *workspace,
-                      size_t workspace_bytes, hipStream_t stream) {
+                      int dtype, const void *buffer_in, const void *weights, const void *prepared, float *buffer_out,
+                      hipStream_t stream) {
   GroupTable gt{};
-  int rc = fill_groups(gt, num_offsets, rows, padded_offsets);
+  const int bm = 128 * mt_for(wn_for(c_out));
+  int rc = fill_groups(gt, num_offsets, rows, padded_offsets, bm);
   if (rc) return rc;
   if (num_offsets <= 0) return kOk;
-  if (mfma_ok(dtype, c_in)) {
-    SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= wt_bytes(num_offsets, c_in, c_out),
-                      "ws_gemm: workspace too small");
-    rc = transpose_weights(weights, num_offsets, c_in, c_out, workspace, stream);
-    if (rc) return rc;
+  if (mfma_path(dtype)) {
+    SPIRA_HIP_REQUIRE(prepared != nullptr, "ws_gemm: fp16 needs prepared weights");
     const int64_t tiles = gt.tile_start[num_offsets];
     if (tiles == 0) return kOk;
+    const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
     const int wn = wn_for(c_out);
-    dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(div_up(c_out, 32 * wn)));
-    auto x = static_cast<const _Float16 *>(buffer_in);
-    auto wt = static_cast<const _Float16 *>(workspace);
-    if (wn == 1)
-      hipLaunchKernelGGL((group_gemm_f16_kernel<1>), grid, dim3(256), 0, stream, gt, x, c_in, wt, c_out, buffer_out);
-    else if (wn == 2)
-      hipLaunchKernelGGL((group_gemm_f16_kernel<2>), grid, dim3(256), 0, stream, gt, x, c_in, wt, c_out, buffer_out);
-    else
-      hipLaunchKernelGGL((group_gemm_f16_kernel<4>), grid, dim3(256), 0, stream, gt, x, c_in, wt, c_out, buffer_out);
+    dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(div_up(CoutP, 32 * wn)));
+    if (c_in % 8 == 0) launch_gg<true>(wn, grid, stream, gt, buffer_in, c_in, CinP, prepared, c_out, CoutP, buffer_out);
+    else launch_gg<false>(wn, grid, stream, gt, buffer_in, c_in, CinP, prepared, c_out, CoutP, buffer_out);
   } else {
     int64_t total = 0;
     for (int k = 0; k < num_offsets; ++k) total = std::max<int64_t>(total, padded_offsets[k] + rows[k]);
     const int64_t n = total * c_out;
     if (n == 0) return kOk;
-    if (dtype == SPIRA_F16)
-      hipLaunchKernelGGL(group_gemm_generic_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream, gt, total,
-                         static_cast<const _Float16 *>(buffer_in), c_in, static_cast<const _Float16 *>(weights),
-                         c_out, buffer_out);
-    else
-      hipLaunchKernelGGL(group_gemm_generic_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, gt, total,
-                         static_cast<const float *>(buffer_in), c_in, static_cast<const float *>(weights), c_out,
-                         buffer_out);
+    hipLaunchKernelGGL(group_gemm_generic_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, gt, total,
+                       static_cast<const float *>(buffer_in), c_in, static_cast<const float *>(weights), c_out,
+                       buffer_out);
   }
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
@@ -634,14 +1080,17 @@ int spira_hip_ws_scatter(int64_t num_targets, int c_out, int num_offsets, int dt
   return kOk;
 }
 
-int spira_hip_cast_f32(const float *src, int64_t n, int dtype, void *dst, hipStream_t stream) {
+int spira_hip_finalize(const float *acc, int64_t num_targets, int c_out, int dtype, const float *scale,
+                       const float *shift, const void *residual, int relu, void *targets, hipStream_t stream) {
+  const int64_t n = num_targets * c_out;
   if (n <= 0) return kOk;
+  const Epilogue epi = make_epi(scale, shift, residual, relu);
   if (dtype == SPIRA_F16)
-    hipLaunchKernelGGL(cast_f32_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream, src, n,
-                       static_cast<_Float16 *>(dst));
+    hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream, acc, num_targets, c_out,
+                       static_cast<_Float16 *>(targets), epi);
   else
-    hipLaunchKernelGGL(cast_f32_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, src, n,
-                       static_cast<float *>(dst));
+    hipLaunchKernelGGL(finalize_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, acc, num_targets, c_out,
+                       static_cast<float *>(targets), epi);
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }

@@ -425,6 +425,40 @@ __global__ void convert_transposed_kernel(const int32_t *__restrict__ map, int64
   out[static_cast<int64_t>(s) * K + i % K] = static_cast<int32_t>(i / K);
 }
 
+// Row-order key of an output-stationary map row: the bitmask of its valid
+// columns (the first 63 columns, with bit 63 flagging any valid column past
+// them), so that sorting groups rows with identical neighbour patterns.
+__global__ void row_mask_kernel(const int32_t *__restrict__ map, int64_t T, int K, uint64_t *__restrict__ keys,
+                                int32_t *__restrict__ iota) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const int32_t *row = map + t * K;
+  uint64_t m = 0;
+  for (int j = 0; j < K; ++j)
+    if (row[j] >= 0) m |= (j < 63) ? (uint64_t(1) << j) : (uint64_t(1) << 63);
+  keys[t] = m;
+  iota[t] = static_cast<int32_t>(t);
+}
+
+// ordered[i, :] = map[order[i], :]
+__global__ void gather_rows_kernel(const int32_t *__restrict__ map, const int32_t *__restrict__ order, int64_t T,
+                                   int K, int32_t *__restrict__ ordered) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= T * K) return;
+  const int64_t row = i / K;
+  ordered[i] = map[static_cast<int64_t>(order[row]) * K + (i - row * K)];
+}
+
+static size_t row_order_parts(int64_t T, size_t *sort_bytes) {
+  size_t b = 0;
+  (void)rocprim::radix_sort_pairs(nullptr, b, static_cast<const uint64_t *>(nullptr),
+                                  static_cast<uint64_t *>(nullptr), static_cast<const int32_t *>(nullptr),
+                                  static_cast<int32_t *>(nullptr), static_cast<size_t>(T), 0, 64);
+  *sort_bytes = b;
+  auto a = [](size_t x) { return (x + 255) / 256 * 256; };
+  return 2 * a(T * sizeof(uint64_t)) + a(T * sizeof(int32_t)) + a(b);
+}
+
 static size_t scan_temp_bytes(int64_t n) {
   size_t b = 0;
   (void)rocprim::exclusive_scan(nullptr, b, static_cast<const int32_t *>(nullptr), static_cast<int32_t *>(nullptr), 0,
@@ -527,6 +561,44 @@ int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_t
 
 int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t stream) {
   return fill_i32(ptr, n, value, stream);
+}
+
+int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes) {
+  size_t sb = 0;
+  *bytes = num_targets <= 0 ? 0 : row_order_parts(num_targets, &sb);
+  return kOk;
+}
+
+int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int num_offsets, int32_t *order,
+                             uint64_t *row_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(num_targets >= 0 && num_targets < (int64_t(1) << 31), "kmap_row_order: size out of range");
+  SPIRA_HIP_REQUIRE(num_offsets >= 1, "kmap_row_order: no offsets");
+  if (num_targets == 0) return kOk;
+  size_t sb = 0;
+  const size_t need = row_order_parts(num_targets, &sb);
+  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= need, "kmap_row_order: workspace too small");
+  auto a = [](size_t x) { return (x + 255) / 256 * 256; };
+  char *p = static_cast<char *>(workspace);
+  uint64_t *keys = reinterpret_cast<uint64_t *>(p);
+  p += a(num_targets * sizeof(uint64_t));
+  uint64_t *keys_out = reinterpret_cast<uint64_t *>(p);
+  p += a(num_targets * sizeof(uint64_t));
+  int32_t *iota = reinterpret_cast<int32_t *>(p);
+  p += a(num_targets * sizeof(int32_t));
+  hipLaunchKernelGGL(row_mask_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, num_targets,
+                     num_offsets, keys, iota);
+  SPIRA_HIP_LAUNCH_CHECK();
+  const int bits = num_offsets >= 63 ? 64 : num_offsets;
+  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, sb, keys, row_masks ? row_masks : keys_out, iota, order,
+                                          static_cast<size_t>(num_targets), 0, bits, stream));
+  if (ordered_map) {
+    const int64_t n = num_targets * num_offsets;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(div_up(n, 256)), dim3(256), 0, stream, out_in_map, order,
+                       num_targets, num_offsets, ordered_map);
+    SPIRA_HIP_LAUNCH_CHECK();
+  }
+  return kOk;
 }
 
 }  // extern "C"

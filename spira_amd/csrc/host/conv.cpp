@@ -9,6 +9,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <unordered_map>
 
 namespace spira_host {
 
@@ -18,9 +20,119 @@ static int dtype_of(const torch::Tensor &t) {
   fail("Cannot find implementation for feature dtype ", t.scalar_type());
 }
 
-static torch::Tensor conv_workspace(int K, int cin, int cout, int dtype, const torch::Device &dev, size_t *bytes) {
-  check_rc(spira_hip_conv_workspace(K, cin, cout, dtype, bytes), "conv");
-  return workspace(*bytes, dev);
+// Prepared (MFMA-ready) weights, cached per weight tensor.  An entry is valid
+// while the same TensorImpl is alive with the same storage pointer and
+// version counter, so an optimizer step or `param.data = ...` invalidates it;
+// the weak reference keeps a freed tensor's address from being reused by a
+// different tensor while its entry exists.
+struct PreparedEntry {
+  explicit PreparedEntry(const torch::Tensor &w) : impl(w.getIntrusivePtr()) {}
+  c10::weak_intrusive_ptr<c10::TensorImpl> impl;
+  const void *data = nullptr;
+  uint32_t version = 0;
+  torch::Tensor prepared;
+};
+
+static std::unordered_map<const c10::TensorImpl *, PreparedEntry> &prepared_cache() {
+  static std::unordered_map<const c10::TensorImpl *, PreparedEntry> cache;
+  return cache;
+}
+
+// Returns the prepared copy of W (or an undefined tensor when the dtype needs none).
+static torch::Tensor prepared_weights(const torch::Tensor &W) {
+  const int dtype = dtype_of(W);
+  size_t bytes = 0;
+  check_rc(spira_hip_prepared_weights_bytes(W.size(0), W.size(1), W.size(2), dtype, &bytes), "prepare_weights");
+  if (bytes == 0) return torch::Tensor();
+  auto &cache = prepared_cache();
+  const c10::TensorImpl *key = W.unsafeGetTensorImpl();
+  auto it = cache.find(key);
+  if (it != cache.end()) {
+    auto &e = it->second;
+    if (!e.impl.expired() && e.data == W.data_ptr() && e.version == W._version() &&
+        e.prepared.device() == W.device())
+      return e.prepared;
+    cache.erase(it);
+  }
+  if (cache.size() > 4096) {  // drop entries of freed tensors
+    for (auto i = cache.begin(); i != cache.end();) i = i->second.impl.expired() ? cache.erase(i) : std::next(i);
+  }
+  PreparedEntry e(W);
+  e.data = W.data_ptr();
+  e.version = W._version();
+  e.prepared = workspace(bytes, W.device());
+  check_rc(spira_hip_prepare_weights(W.data_ptr(), W.size(0), W.size(1), W.size(2), dtype, e.prepared.data_ptr(),
+                                     current_stream()),
+           "prepare_weights");
+  auto out = e.prepared;
+  cache.emplace(key, std::move(e));
+  return out;
+}
+
+// pointer to weight row `k` of W, and of its prepared copy
+static const void *wrow_ptr(const torch::Tensor &W, int k) {
+  return static_cast<const char *>(W.data_ptr()) + static_cast<int64_t>(k) * W.size(1) * W.size(2) * W.element_size();
+}
+static const void *prow_ptr(const torch::Tensor &P, const torch::Tensor &W, int k) {
+  if (!P.defined()) return nullptr;
+  const int64_t cinp = (W.size(1) + 15) / 16 * 16, coutp = (W.size(2) + 31) / 32 * 32;
+  return static_cast<const char *>(P.data_ptr()) + static_cast<int64_t>(k) * cinp * coutp * 2;
+}
+
+// Row orders of output-stationary maps, cached per map tensor like the
+// prepared weights (valid while the same map tensor is alive and unchanged).
+struct OrderEntry {
+  explicit OrderEntry(const torch::Tensor &m) : impl(m.getIntrusivePtr()) {}
+  c10::weak_intrusive_ptr<c10::TensorImpl> impl;
+  const void *data = nullptr;
+  uint32_t version = 0;
+  int64_t T = 0;
+  torch::Tensor order, masks, ordered_map;
+};
+
+static std::unordered_map<const c10::TensorImpl *, OrderEntry> &order_cache() {
+  static std::unordered_map<const c10::TensorImpl *, OrderEntry> cache;
+  return cache;
+}
+
+static bool &row_order_flag() {
+  static bool on = [] {
+    const char *e = std::getenv("SPIRA_OS_ROW_ORDER");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+static bool row_order_enabled() { return row_order_flag(); }
+void set_row_order(bool on) { row_order_flag() = on; }
+
+static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
+  auto &cache = order_cache();
+  const c10::TensorImpl *key = map.unsafeGetTensorImpl();
+  auto it = cache.find(key);
+  if (it != cache.end()) {
+    auto &e = it->second;
+    if (!e.impl.expired() && e.data == map.data_ptr() && e.version == map._version() && e.T == T) return e;
+    cache.erase(it);
+  }
+  if (cache.size() > 1024) {
+    for (auto i = cache.begin(); i != cache.end();) i = i->second.impl.expired() ? cache.erase(i) : std::next(i);
+  }
+  OrderEntry e(map);
+  e.data = map.data_ptr();
+  e.version = map._version();
+  e.T = T;
+  const int64_t K = map.size(1);
+  e.order = empty_i32({std::max<int64_t>(T, 1)}, map.device());
+  e.masks = torch::empty({std::max<int64_t>(T, 1)}, torch::TensorOptions(map.device()).dtype(torch::kInt64));
+  e.ordered_map = empty_i32({std::max<int64_t>(T, 1), K}, map.device());
+  size_t wsb = 0;
+  check_rc(spira_hip_kmap_row_order_workspace(T, &wsb), "row_order");
+  auto ws = workspace(wsb, map.device());
+  check_rc(spira_hip_kmap_row_order(map.data_ptr<int32_t>(), T, static_cast<int>(K), e.order.data_ptr<int32_t>(),
+                                    reinterpret_cast<uint64_t *>(e.masks.data_ptr<int64_t>()),
+                                    e.ordered_map.data_ptr<int32_t>(), ws.data_ptr(), wsb, current_stream()),
+           "row_order");
+  return cache.emplace(key, std::move(e)).first->second;
 }
 
 static void check_features(const torch::Tensor &X, const torch::Tensor &W) {
@@ -33,11 +145,17 @@ static void check_features(const torch::Tensor &X, const torch::Tensor &W) {
   dtype_of(X);
 }
 
-// Output-stationary pass over weights W[0:K] into `out` (mode: SPIRA_OUT_*).
-// A missing map is the identity map (a submanifold layer whose only dense
-// offset is the centre: sparse_convolution.cu:1368-1380).
+// Output-stationary pass over weight rows W[w0 : w0+K] into `out` (mode:
+// SPIRA_OUT_*).  A missing map is the identity map (a submanifold layer whose
+// only dense offset is the centre: sparse_convolution.cu:1368-1380).
+struct Epi {
+  const float *scale = nullptr, *shift = nullptr;
+  const void *residual = nullptr;
+  int relu = 0;
+};
+
 static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
-                   int K, void *out, int mode) {
+                   int w0, int K, void *out, int mode, const Epi &epi = Epi()) {
   const auto dev = X.device();
   const int dtype = dtype_of(X);
   torch::Tensor ident;
@@ -53,10 +171,21 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
     ident = torch::arange(T, torch::TensorOptions(dev).dtype(torch::kInt32)).view({T, 1});
     mp = ident.data_ptr<int32_t>();
   }
+  auto P = prepared_weights(W);
   size_t wsb = 0;
-  auto ws = conv_workspace(K, W.size(1), W.size(2), dtype, dev, &wsb);
-  check_rc(spira_hip_conv_os(T, K, mp, X.data_ptr(), S, W.size(1), W.data_ptr(), W.size(2), dtype, out, mode,
-                             ws.data_ptr(), wsb, current_stream()),
+  check_rc(spira_hip_conv_os_workspace(T, K, W.size(1), W.size(2), dtype, mode, &wsb), "conv_os");
+  auto ws = workspace(wsb, dev);
+  const int32_t *order = nullptr;
+  const uint64_t *masks = nullptr;
+  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0) {
+    const OrderEntry &oe = row_order_of(*map, T);
+    order = oe.order.data_ptr<int32_t>();
+    masks = reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>());
+    mp = oe.ordered_map.data_ptr<int32_t>();
+  }
+  check_rc(spira_hip_conv_os(T, K, mp, order, masks, X.data_ptr(), S, W.size(1), wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
+                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, ws.data_ptr(), wsb,
+                             current_stream()),
            "sparse_convolution_forward_os");
 }
 
@@ -68,7 +197,7 @@ torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, 
   SPIRA_CHECK_ARG(W.size(0) == out_in_map.size(1), "weights have ", W.size(0), " offsets, map has ",
                   out_in_map.size(1));
   auto Y = torch::empty({T, W.size(2)}, X.options());
-  run_os(&out_in_map, S, T, X, W, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE);
+  run_os(&out_in_map, S, T, X, W, 0, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE);
   return Y;
 }
 
@@ -157,13 +286,9 @@ static void gs_gather(GsPlan &p, const torch::Tensor &X, hipStream_t s) {
 
 static void gs_gemm(GsPlan &p, const torch::Tensor &W, int woff, hipStream_t s) {
   const int dtype = dtype_of(W);
-  const int cin = W.size(1), cout = W.size(2);
-  size_t wsb = 0;
-  auto ws = conv_workspace(p.Km, cin, cout, dtype, W.device(), &wsb);
-  const int64_t wstep = static_cast<int64_t>(cin) * cout * W.element_size();
-  const char *wbase = static_cast<const char *>(W.data_ptr()) + woff * wstep;
-  check_rc(spira_hip_ws_gemm(p.Km, p.sizes.data(), p.off.data(), cin, cout, dtype, p.bin.data_ptr(), wbase,
-                             p.bout.data_ptr<float>(), ws.data_ptr(), wsb, s),
+  auto P = prepared_weights(W);
+  check_rc(spira_hip_ws_gemm(p.Km, p.sizes.data(), p.off.data(), W.size(1), W.size(2), dtype, p.bin.data_ptr(),
+                             wrow_ptr(W, woff), prow_ptr(P, W, woff), p.bout.data_ptr<float>(), s),
            "gemm");
 }
 
@@ -209,19 +334,20 @@ static void ws_fused_into(int64_t S, int64_t T, const torch::Tensor &X, const to
   const int32_t *imap = transpose ? base + mapsize : base;
   const int32_t *omap = transpose ? base : base + mapsize;
   const int dtype = dtype_of(X);
-  size_t wsb = 0;
-  auto ws = conv_workspace(W.size(0), W.size(1), W.size(2), dtype, X.device(), &wsb);
+  auto P = prepared_weights(W);
   check_rc(spira_hip_conv_ws_fused(S, T, imap, omap, rows, naddrs.data_ptr<int32_t>(), qnaddrs.data_ptr<int32_t>(),
                                    mapsize, qmapsize, woff, mirror_rows, X.data_ptr(), W.size(1), W.data_ptr(),
-                                   W.size(0), W.size(2), dtype, acc, ws.data_ptr(), wsb, current_stream()),
+                                   P.defined() ? P.data_ptr() : nullptr, W.size(0), W.size(2), dtype, acc,
+                                   current_stream()),
            "sparse_convolution_forward_ws_merged");
 }
 
 static torch::Tensor finish_acc(const torch::Tensor &acc, const torch::Tensor &X) {
   if (X.scalar_type() == torch::kFloat) return acc;
   auto Y = torch::empty(acc.sizes(), X.options());
-  check_rc(spira_hip_cast_f32(acc.data_ptr<float>(), acc.numel(), dtype_of(X), Y.data_ptr(), current_stream()),
-           "cast");
+  check_rc(spira_hip_finalize(acc.data_ptr<float>(), acc.size(0), acc.size(1), dtype_of(X), nullptr, nullptr,
+                              nullptr, 0, Y.data_ptr(), current_stream()),
+           "finalize");
   return Y;
 }
 
@@ -252,8 +378,8 @@ torch::Tensor forward_hs(int64_t S, int64_t T, int64_t gather_tile, int64_t scat
   const int Kos = out_in_map.has_value() ? static_cast<int>(out_in_map->size(1)) : 1;
   SPIRA_CHECK_ARG(W.size(0) == Kws + Kos, "weights have ", W.size(0), " offsets, expected ", Kws + Kos);
   auto acc = torch::empty({T, W.size(2)}, X.options().dtype(torch::kFloat));
-  run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W.narrow(0, 0, Kos).contiguous(), Kos,
-         acc.data_ptr<float>(), SPIRA_OUT_STORE_F32);
+  run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W, 0, Kos, acc.data_ptr<float>(),
+         SPIRA_OUT_STORE_F32);
   auto p = plan_gs(S, T, source_masks, target_masks, nbsizes, true, threshold, W.size(1), W.size(2), X.options());
   auto Y = torch::empty({T, W.size(2)}, X.options());
   auto s = current_stream();
@@ -273,8 +399,8 @@ torch::Tensor forward_hs_merged(int64_t S, int64_t T, const torch::Tensor &X, co
   const int Kos = out_in_map.has_value() ? static_cast<int>(out_in_map->size(1)) : 1;
   SPIRA_CHECK_ARG(W.size(0) == Kws + Kos, "weights have ", W.size(0), " offsets, expected ", Kws + Kos);
   auto acc = torch::empty({T, W.size(2)}, X.options().dtype(torch::kFloat));
-  run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W.narrow(0, 0, Kos).contiguous(), Kos,
-         acc.data_ptr<float>(), SPIRA_OUT_STORE_F32);
+  run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W, 0, Kos, acc.data_ptr<float>(),
+         SPIRA_OUT_STORE_F32);
   ws_fused_into(S, T, X, W, naddrs, qnaddrs, nbmaps, mapsize, qmapsize, transpose, Kos, Kws, acc.data_ptr<float>());
   return finish_acc(acc, X);
 }
@@ -347,6 +473,7 @@ void register_conv(pybind11::module_ &m) {
   m.def("cuda_time_scatter", &time_scatter);
   m.def("cuda_free_buffers", &free_buffers);
   m.def("cuda_reset_error", &reset_error);
+  m.def("set_os_row_order", &set_row_order);
 }
 
 }  // namespace spira_host
