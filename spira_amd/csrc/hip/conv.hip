@@ -35,6 +35,7 @@
 #include "../../../include/spira_hip.h"
 
 #include <algorithm>
+#include <utility>
 #include <vector>
 
 namespace spira_hip {
@@ -55,28 +56,62 @@ struct Epilogue {
   int relu;
 };
 
-// 16 zero bytes: the source of every masked lane of an LDS-DMA load
-__device__ __align__(64) _Float16 g_zero16[32];
+// Gathered operands of the MMA core.  Both are addressed through buffer
+// resources with 32-bit byte offsets: a lane whose row is missing (or whose
+// channels lie in the padding) uses an offset past the end, and the buffer
+// unit then returns zeros instead of reading memory.
+struct Operands {
+  const _Float16 *X;  // [rows, Cin] gathered rows
+  uint32_t xbytes;
+  int Cin, CinP;
+  const _Float16 *WT;  // prepared weights [K, CoutP, CinP]
+  uint32_t wbytes;
+  int Cout, CoutP;
+};
+constexpr uint32_t kOutOfRange = 0x80000000u;  // > every buffer size (sizes are < 2^31)
+constexpr int kRsrcWord3 = 0x00020000;         // raw (untyped) buffer, 32-bit data format
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), kRsrcWord3);
+}
 
 namespace ring {
 
 constexpr int KC = 32;  // input channels per step
 constexpr int NS = 3;   // LDS ring depth
 
+// Ring layout: stage s at byte s * STAGE holds the step's weight chunk
+// (B_BYTES: BN rows x 64 B, XOR-swizzled) followed by its gathered rows
+// (A_BYTES: per wave MT tiles x 2 k-halves x 64 lanes x 16 B, lane-linear).
 template <int WN, int MT> struct Cfg {
   static constexpr int BN = 32 * WN;
   static constexpr int BM = 128 * MT;
-  static constexpr int A_BYTES = MT * 8192;          // 4 waves x MT x 2 k-halves x 64 lanes x 16 B
   static constexpr int BVEC = (BN * 4 + 255) / 256;  // 16-byte weight vectors per thread and step
   static constexpr int B_BYTES = BVEC * 4096;
-  static constexpr int IDX_OFF = A_BYTES + B_BYTES;  // 4 waves x 64 row indices of a later step
-  static constexpr int STAGE = IDX_OFF + 1024;
-  static constexpr int LPS = MT * 2 + BVEC;          // LDS-DMA loads per wave and step
+  static constexpr int A_BYTES = MT * 8192;
+  static constexpr int STAGE = B_BYTES + A_BYTES;
+  static constexpr int RING = NS * STAGE;
+  static constexpr int LPS = MT * 2 + BVEC;  // LDS-DMA loads per wave and step
+  // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
+  static_assert((NS - 1) * STAGE + (WN - 1) * 2048 < 65536, "weight read offset exceeds 16 bits");
+  static_assert((NS - 1) * STAGE + (2 * MT - 1) * 1024 < 65536, "row read offset exceeds 16 bits");
 };
 
-__device__ __forceinline__ void dma16(const void *g, void *lds_wave_base) {
-  // address-space casts (generic -> global / LDS) need C-style casts
-  __builtin_amdgcn_global_load_lds((gbl_void_t *)(const_cast<void *>(g)), (lds_void_t *)(lds_wave_base), 16, 0, 0);
+// compile-time loop: f(std::integral_constant<int, I>) for I in [0, N)
+template <class F, int... I>
+__device__ __forceinline__ void unroll_seq(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F> __device__ __forceinline__ void unroll(F &&f) {
+  unroll_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// 16 (or 4) bytes per lane from buffer `r` at byte offset `off` into
+// lds_wave_base + lane * 16 (or * 4); the LDS base must be wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, void *lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_wave_base), 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t off, void *lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_wave_base), 4, off, 0, 0, 0);
 }
 
 // wait until at most N vector-memory operations of this wave are in flight
@@ -85,113 +120,127 @@ template <int N> __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-__device__ __forceinline__ const _Float16 *zero16() { return g_zero16; }
+// LDS reads of the ring are inline assembly with immediate offsets from a
+// few per-lane base registers.  The compiler then inserts no waits of its own
+// for them (its LDS-DMA tracking loses precision at the loop header and
+// would drain the whole ring there) and cannot hoist one address register per
+// read and stage out of the loop; the ring's explicit vmcnt wait + barrier
+// orders them after the DMA writes, lds_wait() after their own completion.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t *)(const_cast<void *>(p))));
+}
+template <int OFF> __device__ __forceinline__ half8 rd16(uint32_t base) {
+  half8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(base), "i"(OFF) : "memory");
+  return v;
+}
+template <int OFF> __device__ __forceinline__ int32_t rd4(uint32_t base) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(base), "i"(OFF) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// ties a value read by rd16 / rd4 to a point after lds_wait()
+template <class V> __device__ __forceinline__ void pin(V &v) { asm volatile("" : "+v"(v)); }
 
-// B slot of (row n, 16-byte chunk c) inside a stage's weight region: four
-// chunks per row, the chunk index XOR-ed with (n / 4) % 4
-__device__ __forceinline__ int bslot(int n, int c) { return n * 4 + (c ^ ((n >> 2) & 3)); }
-
-// Issue the loads of one step into `stage`: A rows idx[m] (or -1) at channels
-// kb..kb+31, weight row `wrow` (ignored when !live: every wave then issues
-// the same number of loads from the zero block, which keeps vmcnt uniform).
-template <int WN, int MT, bool ALIGNED>
-__device__ __forceinline__ void issue(char *stage, bool live, const int32_t (&idx)[MT], int64_t wrow, int kb,
-                                      const _Float16 *X, int Cin, int CinP,
-                                      const _Float16 *WT, int n0, int CoutP) {
+// per-lane LDS read bases of the ring
+struct ReadBase {
+  uint32_t a;       // rows: + s * STAGE + (m * 2 + ks) * 1024
+  uint32_t b0, b1;  // weights, k-half 0 / 1: + s * STAGE + wn * 2048
+};
+template <int WN, int MT> __device__ __forceinline__ ReadBase read_base(const char *ring, int wave) {
   using C = Cfg<WN, MT>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
+  const uint32_t base = lds_addr(ring);
+  const int q = (r >> 2) & 3;  // B swizzle: chunk c of row n sits at n * 4 + (c ^ ((n / 4) % 4))
+  ReadBase rb;
+  rb.a = base + C::B_BYTES + wave * MT * 2048 + lane * 16;
+  rb.b0 = base + (r * 4 + (kh ^ q)) * 16;
+  rb.b1 = base + (r * 4 + ((2 | kh) ^ q)) * 16;
+  return rb;
+}
+
+// Issue the loads of one step into stage S: A rows idx[m] (or -1) at
+// channels kb..kb+31, weight row `wrow`.  When !live every load is out of
+// range, so each wave issues the same number of loads in every step.
+template <int WN, int MT, bool ALIGNED, int S>
+__device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[MT], int wrow, int kb,
+                                      const Operands &op, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr,
+                                      int n0) {
+  using C = Cfg<WN, MT>;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int kh = lane >> 5;
+  char *stage = ring + S * C::STAGE;
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int k = kb + ks * 16 + kh * 8;
-      const _Float16 *g = zero16();
-      if (live && idx[m] >= 0 && k < Cin) g = X + static_cast<int64_t>(idx[m]) * Cin + k;
+      char *dst = stage + C::B_BYTES + ((wave * MT + m) * 2 + ks) * 1024;
       if constexpr (!ALIGNED) {
         // rows that are not 16-byte aligned are staged through registers
         half8 v;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          v[e] = (live && idx[m] >= 0 && k + e < Cin) ? X[static_cast<int64_t>(idx[m]) * Cin + k + e]
-                                                     : static_cast<_Float16>(0.f);
-        *reinterpret_cast<half8 *>(stage + ((wave * MT + m) * 2 + ks) * 1024 + lane * 16) = v;
+          v[e] = (live && idx[m] >= 0 && k + e < op.Cin) ? op.X[static_cast<int64_t>(idx[m]) * op.Cin + k + e]
+                                                        : static_cast<_Float16>(0.f);
+        *reinterpret_cast<half8 *>(dst + lane * 16) = v;
         __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
       } else {
-        dma16(g, stage + ((wave * MT + m) * 2 + ks) * 1024);
+        const uint32_t off = (live && idx[m] >= 0 && k < op.Cin)
+                                 ? (static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>(op.Cin) + k) * 2u
+                                 : kOutOfRange;
+        dma16(xr, off, dst);
       }
     }
   }
-  char *bst = stage + C::A_BYTES;
 #pragma unroll
   for (int i = 0; i < C::BVEC; ++i) {
     const int v = i * 256 + tid;
     const int n = v >> 2, cp = v & 3;
     const int c = cp ^ ((n >> 2) & 3);
-    const _Float16 *g = zero16();
-    if (live && n < C::BN && n0 + n < CoutP && kb + c * 8 < CinP)
-      g = WT + (wrow * CoutP + n0 + n) * CinP + kb + c * 8;
-    dma16(g, bst + (i * 256 + wave * 64) * 16);
+    const uint32_t off = (live && n < C::BN && n0 + n < op.CoutP && kb + c * 8 < op.CinP)
+                             ? ((static_cast<uint32_t>(wrow) * op.CoutP + n0 + n) * op.CinP + kb + c * 8) * 2u
+                             : kOutOfRange;
+    dma16(wr, off, stage + (i * 256 + wave * 64) * 16);
   }
 }
 
-// LDS reads of the ring are inline assembly: the compiler then inserts no
-// waits of its own for them (its LDS-DMA tracking loses precision at the loop
-// header and would drain the whole ring there); the ring's explicit
-// vmcnt wait + barrier orders them after the DMA writes, lds_fence() after
-// their own completion.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t *)(const_cast<void *>(p))));
-}
-__device__ __forceinline__ half8 lds_read16(const void *p) {
-  half8 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
-  return v;
-}
-__device__ __forceinline__ int32_t lds_read4(const void *p) {
-  int32_t v;
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
-  return v;
-}
-__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-// ties a value read by lds_read* to a point after lds_wait()
-template <class V> __device__ __forceinline__ void pin(V &v) { asm volatile("" : "+v"(v)); }
-
-// MFMAs of one staged step
-template <int WN, int MT>
-__device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const char *stage, unsigned anymask) {
+// MFMAs of stage S (rows without a neighbour hold zeros)
+template <int WN, int MT, int S>
+__device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const ReadBase &rb) {
   using C = Cfg<WN, MT>;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 31, kh = lane >> 5;
-  const char *bst = stage + C::A_BYTES;
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  unroll<2>([&](auto KS) {
+    constexpr int ks = decltype(KS)::value;
     half8 b[WN], a[MT];
-#pragma unroll
-    for (int wn = 0; wn < WN; ++wn) b[wn] = lds_read16(bst + bslot(wn * 32 + r, ks * 2 + kh) * 16);
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-      if ((anymask >> m) & 1) a[m] = lds_read16(stage + ((wave * MT + m) * 2 + ks) * 1024 + lane * 16);
+    unroll<WN>([&](auto W) {
+      constexpr int wn = decltype(W)::value;
+      b[wn] = rd16<S * C::STAGE + wn * 2048>(ks ? rb.b1 : rb.b0);
+    });
+    unroll<MT>([&](auto M) {
+      constexpr int m = decltype(M)::value;
+      a[m] = rd16<S * C::STAGE + (m * 2 + ks) * 1024>(rb.a);
+    });
     lds_wait();
 #pragma unroll
     for (int wn = 0; wn < WN; ++wn) pin(b[wn]);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (!((anymask >> m) & 1)) continue;
-      pin(a[m]);
+    for (int m = 0; m < MT; ++m) pin(a[m]);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int wn = 0; wn < WN; ++wn)
         acc[m][wn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m], b[wn], acc[m][wn], 0, 0, 0);
-    }
-  }
+  });
 }
 
 // The pipelined step loop over nsteps steps; stage u % 3 of the ring holds
-// step u.  Two callbacks describe the steps:
-//  * fetch(u, st) issues exactly PL LDS-DMA loads per wave that bring step
-//    u's row indices into st + IDX_OFF (also for u >= nsteps, so that the
-//    vmcnt arithmetic is the same in every wave);
-//  * resolve(u, st, idx, wrow, kb) turns them into the gathered rows idx[m]
+// step u.  Two callbacks describe the steps (S = the stage, a
+// std::integral_constant):
+//  * fetch(u, S) issues exactly PL LDS-DMA loads per wave that bring step
+//    u's row indices into the caller's index slot S (also for u >= nsteps,
+//    so that the vmcnt arithmetic is the same in every wave);
+//  * resolve(u, S, idx, wrow, kb) turns them into the gathered rows idx[m]
 //    (or -1), the weight row and the first input channel of step u.
 // Order of vector-memory operations: F0 F1 F2 D0 F3 D1 F4 | D2 F5 | D3 F6 ...
 // (F = fetch, D = the LPS LDS-DMA loads of a step).  Before step s computes,
@@ -201,52 +250,54 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const char *sta
 // slot that step u's issue has just read (each wave reads only its own).
 template <int WN, int MT, bool ALIGNED, int PL, class Fetch, class Resolve>
 __device__ __forceinline__ void run(floatx16 (&acc)[MT][WN], int nsteps, Fetch fetch, Resolve resolve,
-                                    const _Float16 *X, int Cin, int CinP, const _Float16 *WT, int n0, int CoutP,
-                                    char *s0, char *s1, char *s2) {
+                                    const Operands &op, int n0, char *ring) {
   using C = Cfg<WN, MT>;
-  unsigned any0 = 0, any1 = 0, any2 = 0;  // per-stage "m-tile has a row" bits
-  auto put = [&](int u, char *st, unsigned &anyb) {
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
+  const ReadBase rb = read_base<WN, MT>(ring, wave);
+  auto put = [&](int u, auto St) {
     int32_t idx[MT];
-    int64_t wrow = 0;
+    int wrow = 0;
     int kb = 0;
     const bool live = u < nsteps;
-    if (live) resolve(u, st, idx, wrow, kb);
+    if (live) resolve(u, St, idx, wrow, kb);
     else {
 #pragma unroll
       for (int m = 0; m < MT; ++m) idx[m] = -1;
     }
-    anyb = 0;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) anyb |= (ballot(idx[m] >= 0) != 0 ? 1u : 0u) << m;
-    issue<WN, MT, ALIGNED>(st, live, idx, wrow, kb, X, Cin, CinP, WT, n0, CoutP);
+    issue<WN, MT, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, wr, n0);
   };
-  fetch(0, s0);
-  fetch(1, s1);
-  fetch(2, s2);
+  fetch(0, S0{});
+  fetch(1, S1{});
+  fetch(2, S2{});
   if constexpr (PL > 0) wait_vm<2 * PL>();  // F0 is older than F1 F2
-  put(0, s0, any0);
-  fetch(3, s0);
+  put(0, S0{});
+  fetch(3, S0{});
   if constexpr (PL > 0) wait_vm<C::LPS + 2 * PL>();  // F1 is older than F2 D0 F3
-  put(1, s1, any1);
-  fetch(4, s1);
+  put(1, S1{});
+  fetch(4, S1{});
   for (int s = 0; s < nsteps; s += 3) {
     wait_vm<C::LPS + 2 * PL>();
     __builtin_amdgcn_s_barrier();
-    put(s + 2, s2, any2);
-    fetch(s + 5, s2);
-    compute<WN, MT>(acc, s0, any0);
-    if (s + 1 >= nsteps) break;
+    put(s + 2, S2{});
+    fetch(s + 5, S2{});
+    compute<WN, MT, 0>(acc, rb);
+    // Steps past nsteps (at most two) compute on all-zero stages: the trip
+    // is uniform, with a single loop exit that keeps the accumulators in place.
     wait_vm<C::LPS + 2 * PL>();
     __builtin_amdgcn_s_barrier();
-    put(s + 3, s0, any0);
-    fetch(s + 6, s0);
-    compute<WN, MT>(acc, s1, any1);
-    if (s + 2 >= nsteps) break;
+    put(s + 3, S0{});
+    fetch(s + 6, S0{});
+    compute<WN, MT, 1>(acc, rb);
     wait_vm<C::LPS + 2 * PL>();
     __builtin_amdgcn_s_barrier();
-    put(s + 4, s1, any1);
-    fetch(s + 7, s1);
-    compute<WN, MT>(acc, s2, any2);
+    put(s + 4, S1{});
+    fetch(s + 7, S1{});
+    compute<WN, MT, 2>(acc, rb);
   }
   wait_vm<0>();
 }
@@ -298,10 +349,7 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[WN], const int3
   }
 }
 
-#define SPIRA_RING_STAGES(C)                          \
-  __shared__ __align__(1024) char st0[C::STAGE];      \
-  __shared__ __align__(1024) char st1[C::STAGE];      \
-  __shared__ __align__(1024) char st2[C::STAGE]
+#define SPIRA_RING_STAGES(C) __shared__ __align__(1024) char ring_lds[C::RING]
 
 // Output-stationary implicit GEMM.  A block owns BM = 128*MT logical rows
 // (wave w: rows [w*32*MT, (w+1)*32*MT) as MT tiles of 32) and BN = 32*WN
@@ -314,11 +362,10 @@ template <int WN, int MT, int MODE, bool ALIGNED>
 __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ rowmask, int64_t T, int Kc, int jper,
-                                                    const _Float16 *__restrict__ X, int Cin, int CinP,
-                                                    const _Float16 *__restrict__ WT, int Cout, int CoutP, void *Y,
-                                                    Epilogue epi) {
+                                                    Operands op, void *Y, Epilogue epi) {
   using C = ring::Cfg<WN, MT>;
   SPIRA_RING_STAGES(C);
+  __shared__ __align__(16) int32_t idx_lds[ring::NS][256];  // map entries of a later step, per stage
   __shared__ int32_t act[65];
   __shared__ unsigned flag[2];
   __shared__ int32_t orow_s[4][32 * MT];
@@ -360,7 +407,7 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   }
   __syncthreads();
   const int nact = act[64];
-  const int nch = (CinP + ring::KC - 1) / ring::KC;
+  const int nch = (op.CinP + ring::KC - 1) / ring::KC;
 
   floatx16 acc[MT][WN];
   zero_acc<WN, MT>(acc);
@@ -374,16 +421,19 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   const int nsteps = nact * nch;
   const int frow = MT == 2 ? lane : r;
   const int64_t flr = row0 + wave * 32 * MT + frow;
-  const int32_t *fptr = map + (flr < T ? flr * Kc : 0);
-  auto fetch = [&](int u, char *st) {
+  const uint32_t fbase = flr < T ? static_cast<uint32_t>(flr * Kc) * 4u : kOutOfRange;
+  const __amdgpu_buffer_rsrc_t mr = make_rsrc(map, static_cast<uint32_t>(T * Kc * 4));
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + r) * 4;
+  auto fetch = [&](int u, auto St) {
     // act[] holds nact entries (possibly none): steps past the end read column 0
     const int j = u < nsteps ? act[u / nch] : 0;
-    __builtin_amdgcn_global_load_lds((gbl_void_t *)(const_cast<int32_t *>(fptr + j)),
-                                     (lds_void_t *)(st + C::IDX_OFF + wave * 256), 4, 0, 0);
+    ring::dma4(mr, fbase == kOutOfRange ? kOutOfRange : fbase + j * 4u, &idx_lds[decltype(St)::value][uwave * 64]);
   };
-  auto resolve = [&](int u, const char *st, int32_t (&idx)[MT], int64_t &wrow, int &kb) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) idx[m] = ring::lds_read4(st + C::IDX_OFF + wave * 256 + (m * 32 + r) * 4);
+  auto resolve = [&](int u, auto St, int32_t (&idx)[MT], int &wrow, int &kb) {
+    ring::unroll<MT>([&](auto M) {
+      idx[decltype(M)::value] = ring::rd4<decltype(St)::value * 1024 + decltype(M)::value * 128>(ibase);
+    });
     ring::lds_wait();
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -393,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
     wrow = act[u / nch];
     kb = (u % nch) * ring::KC;
   };
-  ring::run<WN, MT, ALIGNED, 1>(acc, nsteps, fetch, resolve, X, Cin, CinP, WT, n0, CoutP, st0, st1, st2);
+  ring::run<WN, MT, ALIGNED, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -403,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   }
   __syncthreads();
 #pragma unroll
-  for (int m = 0; m < MT; ++m) store_tile<WN, MODE>(acc[m], orow_s[wave] + m * 32, n0, Cout, r, kh, Y, epi);
+  for (int m = 0; m < MT; ++m) store_tile<WN, MODE>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Y, epi);
 }
 
 // Fused weight-stationary pass.  Rows of the pair list are tiled per
@@ -416,9 +466,7 @@ template <int WN, int MT, bool ALIGNED>
 __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ in_idx,
                                                     const int32_t *__restrict__ out_idx,
                                                     const int32_t *__restrict__ naddrs, int R, int64_t nfwd, int Kw,
-                                                    int woffset, const _Float16 *__restrict__ X, int Cin, int CinP,
-                                                    const _Float16 *__restrict__ WT, int Cout, int CoutP,
-                                                    float *__restrict__ Yacc) {
+                                                    int woffset, Operands op, float *__restrict__ Yacc) {
   using C = ring::Cfg<WN, MT>;
   SPIRA_RING_STAGES(C);
   __shared__ int32_t tstart[kMaxGroups + 1];
@@ -463,19 +511,19 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
     src[m] = valid ? (mir ? out_idx[p] : in_idx[p]) : -1;
     dst[m] = valid ? (mir ? in_idx[p] : out_idx[p]) : -1;
   }
-  const int64_t wrow0 = woffset + (mir ? Kw - 1 - row : row);
+  const int wrow0 = woffset + (mir ? Kw - 1 - row : row);
   const int n0 = blockIdx.y * C::BN;
   floatx16 acc[MT][WN];
   zero_acc<WN, MT>(acc);
-  auto fetch = [](int, char *) {};
-  auto resolve = [&](int u, const char *, int32_t (&idx)[MT], int64_t &wrow, int &kb) {
+  auto fetch = [](int, auto) {};
+  auto resolve = [&](int u, auto, int32_t (&idx)[MT], int &wrow, int &kb) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) idx[m] = src[m];
     wrow = wrow0;
     kb = u * ring::KC;
   };
-  const int nch = (CinP + ring::KC - 1) / ring::KC;
-  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, X, Cin, CinP, WT, n0, CoutP, st0, st1, st2);
+  const int nch = (op.CinP + ring::KC - 1) / ring::KC;
+  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = dst[m];
@@ -483,7 +531,7 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
   __syncthreads();
 #pragma unroll
   for (int m = 0; m < MT; ++m)
-    store_tile<WN, kAtomicF32>(acc[m], orow_s[wave] + m * 32, n0, Cout, r, kh, Yacc, Epilogue{});
+    store_tile<WN, kAtomicF32>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Yacc, Epilogue{});
 }
 
 struct GroupTable {
@@ -495,9 +543,7 @@ struct GroupTable {
 
 // Grouped GEMM over the padded gather buffer: Ybuf[rows of g] = Xbuf[rows of g] @ W[g].
 template <int WN, int MT, bool ALIGNED>
-__global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, const _Float16 *__restrict__ Xb, int Cin,
-                                                    int CinP, const _Float16 *__restrict__ WT, int Cout, int CoutP,
-                                                    float *__restrict__ Yb) {
+__global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operands op, float *__restrict__ Yb) {
   using C = ring::Cfg<WN, MT>;
   SPIRA_RING_STAGES(C);
   __shared__ int32_t orow_s[4][32 * MT];
@@ -519,15 +565,15 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, const _
   const int n0 = blockIdx.y * C::BN;
   floatx16 acc[MT][WN];
   zero_acc<WN, MT>(acc);
-  auto fetch = [](int, char *) {};
-  auto resolve = [&](int u, const char *, int32_t (&idx)[MT], int64_t &wrow, int &kb) {
+  auto fetch = [](int, auto) {};
+  auto resolve = [&](int u, auto, int32_t (&idx)[MT], int &wrow, int &kb) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) idx[m] = src[m];
     wrow = g;
     kb = u * ring::KC;
   };
-  const int nch = (CinP + ring::KC - 1) / ring::KC;
-  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, Xb, Cin, CinP, WT, n0, CoutP, st0, st1, st2);
+  const int nch = (op.CinP + ring::KC - 1) / ring::KC;
+  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = src[m];
@@ -535,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, const _
   __syncthreads();
 #pragma unroll
   for (int m = 0; m < MT; ++m)
-    store_tile<WN, kStoreF32>(acc[m], orow_s[wave] + m * 32, n0, Cout, r, kh, Yb, Epilogue{});
+    store_tile<WN, kStoreF32>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Yb, Epilogue{});
 }
 
 // ---------------------------------------------------------------------------
@@ -748,83 +794,68 @@ static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
   return std::min(jper, 64);
 }
 
-template <int WN, int MODE, bool AL>
-static void launch_os_wn(dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order, const uint64_t *rowmask,
-                         int64_t T, int Kc, int jper, const void *X, int Cin, int CinP, const void *WT, int Cout,
-                         int CoutP, void *Y, const Epilogue &epi) {
-  hipLaunchKernelGGL((os_kernel<WN, MtOf<WN>::value, MODE, AL>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc,
-                     jper, static_cast<const _Float16 *>(X), Cin, CinP, static_cast<const _Float16 *>(WT), Cout, CoutP,
-                     Y, epi);
+// Operands of the MMA core; byte sizes must fit the 31-bit buffer offsets
+static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, const void *WT, int K, int Cout) {
+  op.Cin = Cin;
+  op.CinP = pad_in(Cin);
+  op.Cout = Cout;
+  op.CoutP = pad_out(Cout);
+  const int64_t xb = xrows * Cin * 2, wb = static_cast<int64_t>(K) * op.CoutP * op.CinP * 2;
+  SPIRA_HIP_REQUIRE(xb < (int64_t(1) << 31) && wb < (int64_t(1) << 31),
+                    "fp16 features / weights of one layer must stay below 2 GiB");
+  op.X = static_cast<const _Float16 *>(X);
+  op.xbytes = static_cast<uint32_t>(xb);
+  op.WT = static_cast<const _Float16 *>(WT);
+  op.wbytes = static_cast<uint32_t>(wb);
+  return kOk;
 }
+
+// launch `K<WN, MtOf<WN>, ...>` for the column-tile width chosen at run time
+#define SPIRA_WN_SWITCH(wn, CALL) \
+  switch (wn) {                   \
+    case 1: CALL(1); break;       \
+    case 2: CALL(2); break;       \
+    case 3: CALL(3); break;       \
+    case 4: CALL(4); break;       \
+    default: CALL(8); break;      \
+  }
 
 template <int MODE, bool AL>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const void *X, int Cin, int CinP,
-                      const void *WT, int Cout, int CoutP, void *Y, const Epilogue &epi) {
-#define SPIRA_OS_CASE(W)                                                                                         \
-  case W:                                                                                                        \
-    launch_os_wn<W, MODE, AL>(grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi); \
-    break;
-  switch (wn) {
-    SPIRA_OS_CASE(1)
-    SPIRA_OS_CASE(2)
-    SPIRA_OS_CASE(3)
-    SPIRA_OS_CASE(4)
-    default:
-      launch_os_wn<8, MODE, AL>(grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi);
-  }
-#undef SPIRA_OS_CASE
+                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op, void *Y,
+                      const Epilogue &epi) {
+#define SPIRA_OS_CALL(W)                                                                                         \
+  hipLaunchKernelGGL((os_kernel<W, MtOf<W>::value, MODE, AL>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
+                     jper, op, Y, epi)
+  SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
+#undef SPIRA_OS_CALL
 }
 
 template <int MODE>
-static void launch_os_any(bool aligned, int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const void *X, int Cin, int CinP,
-                          const void *WT, int Cout, int CoutP, void *Y, const Epilogue &epi) {
-  if (aligned)
-    launch_os<MODE, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi);
-  else
-    launch_os<MODE, false>(wn, grid, s, map, order, rowmask, T, Kc, jper, X, Cin, CinP, WT, Cout, CoutP, Y, epi);
-}
-
-template <int WN, bool AL>
-static void launch_ws_wn(dim3 grid, hipStream_t s, const int32_t *in_idx, const int32_t *out_idx,
-                         const int32_t *naddrs, int R, int64_t nfwd, int Kw, int woffset, const void *X, int Cin,
-                         int CinP, const void *WT, int Cout, int CoutP, float *Yacc) {
-  hipLaunchKernelGGL((ws_kernel<WN, MtOf<WN>::value, AL>), grid, dim3(256), 0, s, in_idx, out_idx, naddrs, R, nfwd,
-                     Kw, woffset, static_cast<const _Float16 *>(X), Cin, CinP, static_cast<const _Float16 *>(WT), Cout,
-                     CoutP, Yacc);
+static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
+                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op, void *Y,
+                          const Epilogue &epi) {
+  if (op.Cin % 8 == 0) launch_os<MODE, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  else launch_os<MODE, false>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
 }
 
 template <bool AL>
 static void launch_ws(int wn, dim3 grid, hipStream_t s, const int32_t *in_idx, const int32_t *out_idx,
-                      const int32_t *naddrs, int R, int64_t nfwd, int Kw, int woffset, const void *X, int Cin,
-                      int CinP, const void *WT, int Cout, int CoutP, float *Yacc) {
-  switch (wn) {
-    case 1: launch_ws_wn<1, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
-    case 2: launch_ws_wn<2, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
-    case 3: launch_ws_wn<3, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
-    case 4: launch_ws_wn<4, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
-    default: launch_ws_wn<8, AL>(grid, s, in_idx, out_idx, naddrs, R, nfwd, Kw, woffset, X, Cin, CinP, WT, Cout, CoutP, Yacc); break;
-  }
-}
-
-template <int WN, bool AL>
-static void launch_gg_wn(dim3 grid, hipStream_t s, const GroupTable &gt, const void *X, int Cin, int CinP,
-                         const void *WT, int Cout, int CoutP, float *Yb) {
-  hipLaunchKernelGGL((gg_kernel<WN, MtOf<WN>::value, AL>), grid, dim3(256), 0, s, gt, static_cast<const _Float16 *>(X),
-                     Cin, CinP, static_cast<const _Float16 *>(WT), Cout, CoutP, Yb);
+                      const int32_t *naddrs, int R, int64_t nfwd, int Kw, int woffset, const Operands &op,
+                      float *Yacc) {
+#define SPIRA_WS_CALL(W)                                                                                       \
+  hipLaunchKernelGGL((ws_kernel<W, MtOf<W>::value, AL>), grid, dim3(256), 0, s, in_idx, out_idx, naddrs, R, nfwd, \
+                     Kw, woffset, op, Yacc)
+  SPIRA_WN_SWITCH(wn, SPIRA_WS_CALL)
+#undef SPIRA_WS_CALL
 }
 
 template <bool AL>
-static void launch_gg(int wn, dim3 grid, hipStream_t s, const GroupTable &gt, const void *X, int Cin, int CinP,
-                      const void *WT, int Cout, int CoutP, float *Yb) {
-  switch (wn) {
-    case 1: launch_gg_wn<1, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
-    case 2: launch_gg_wn<2, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
-    case 3: launch_gg_wn<3, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
-    case 4: launch_gg_wn<4, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
-    default: launch_gg_wn<8, AL>(grid, s, gt, X, Cin, CinP, WT, Cout, CoutP, Yb); break;
-  }
+static void launch_gg(int wn, dim3 grid, hipStream_t s, const GroupTable &gt, const Operands &op, float *Yb) {
+#define SPIRA_GG_CALL(W) \
+  hipLaunchKernelGGL((gg_kernel<W, MtOf<W>::value, AL>), grid, dim3(256), 0, s, gt, op, Yb)
+  SPIRA_WN_SWITCH(wn, SPIRA_GG_CALL)
+#undef SPIRA_GG_CALL
 }
 
 template <typename FT, int MODE>
@@ -905,7 +936,6 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
                       int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
                       void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
                       int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
-  (void)num_sources;
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_os: dtype must be fp16 or fp32");
   SPIRA_HIP_REQUIRE(out_mode >= SPIRA_OUT_STORE && out_mode <= SPIRA_OUT_ADD_F32, "conv_os: bad out_mode");
   SPIRA_HIP_REQUIRE(c_in > 0 && c_out > 0 && num_offsets > 0, "conv_os: empty channel / offset dimension");
@@ -922,17 +952,17 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     const int jper = choose_jper(bx * by, num_offsets, device_cu_count());
     const int splits = static_cast<int>(div_up(num_offsets, jper));
     dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(by), static_cast<unsigned>(splits));
-    const bool al = c_in % 8 == 0;
+    SPIRA_HIP_REQUIRE(num_targets * num_offsets * 4 < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
+    Operands op;
+    int rc0 = make_operands(op, sources, num_sources, c_in, prepared, num_offsets, c_out);
+    if (rc0) return rc0;
     if (splits == 1) {
       if (out_mode == SPIRA_OUT_STORE)
-        launch_os_any<kStoreNative>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in,
-                                    CinP, prepared, c_out, CoutP, targets, epi);
+        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, targets, epi);
       else if (out_mode == SPIRA_OUT_STORE_F32)
-        launch_os_any<kStoreF32>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in,
-                                 CinP, prepared, c_out, CoutP, targets, epi);
+        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, targets, epi);
       else
-        launch_os_any<kAddF32>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in, CinP,
-                               prepared, c_out, CoutP, targets, epi);
+        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, targets, epi);
     } else {
       float *acc = nullptr;
       if (out_mode == SPIRA_OUT_STORE) {
@@ -946,8 +976,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
         int rc = fill_f32(acc, num_targets * c_out, 0.f, stream);
         if (rc) return rc;
       }
-      launch_os_any<kAtomicF32>(al, wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, sources, c_in, CinP,
-                                prepared, c_out, CoutP, acc, epi);
+      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, acc, epi);
       SPIRA_HIP_LAUNCH_CHECK();
       if (out_mode == SPIRA_OUT_STORE)
         hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(num_targets * c_out, 256)), dim3(256), 0, stream,
@@ -973,8 +1002,6 @@ int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int3
                             int64_t quantized_pairs, int weight_offset, int mirror_rows, const void *sources,
                             int c_in, const void *weights, const void *prepared, int num_weights, int c_out,
                             int dtype, float *target_acc, hipStream_t stream) {
-  (void)num_sources;
-  (void)num_targets;
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_ws_fused: dtype must be fp16 or fp32");
   SPIRA_HIP_REQUIRE(rows >= 1 || num_pairs == 0, "conv_ws_fused: rows must be positive");
   SPIRA_HIP_REQUIRE(weight_offset + std::max(mirror_rows, rows) <= num_weights,
@@ -991,12 +1018,15 @@ int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int3
     const int64_t nfwd = div_up(num_pairs, bm) + rows;
     (void)quantized_pairs;
     dim3 grid(static_cast<unsigned>(Kw > 0 ? 2 * nfwd : nfwd), static_cast<unsigned>(div_up(CoutP, 32 * wn)));
+    Operands op;
+    // the mirrored pass gathers target rows, so the feature rows cover both
+    int rc0 = make_operands(op, sources, std::max(num_sources, Kw > 0 ? num_targets : int64_t(0)), c_in, prepared,
+                            num_weights, c_out);
+    if (rc0) return rc0;
     if (c_in % 8 == 0)
-      launch_ws<true>(wn, grid, stream, in_idx, out_idx, naddrs, rows, nfwd, Kw, weight_offset, sources, c_in, CinP,
-                      prepared, c_out, CoutP, target_acc);
+      launch_ws<true>(wn, grid, stream, in_idx, out_idx, naddrs, rows, nfwd, Kw, weight_offset, op, target_acc);
     else
-      launch_ws<false>(wn, grid, stream, in_idx, out_idx, naddrs, rows, nfwd, Kw, weight_offset, sources, c_in, CinP,
-                       prepared, c_out, CoutP, target_acc);
+      launch_ws<false>(wn, grid, stream, in_idx, out_idx, naddrs, rows, nfwd, Kw, weight_offset, op, target_acc);
   } else {
     const int64_t n = (Kw > 0 ? 2 : 1) * num_pairs * c_out;
     hipLaunchKernelGGL(ws_fused_generic_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, in_idx, out_idx,
@@ -1046,8 +1076,13 @@ int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padde
     const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
     const int wn = wn_for(c_out);
     dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(div_up(CoutP, 32 * wn)));
-    if (c_in % 8 == 0) launch_gg<true>(wn, grid, stream, gt, buffer_in, c_in, CinP, prepared, c_out, CoutP, buffer_out);
-    else launch_gg<false>(wn, grid, stream, gt, buffer_in, c_in, CinP, prepared, c_out, CoutP, buffer_out);
+    int64_t total = 0;
+    for (int k = 0; k < num_offsets; ++k) total = std::max<int64_t>(total, padded_offsets[k] + rows[k]);
+    Operands op;
+    int rc0 = make_operands(op, buffer_in, total, c_in, prepared, num_offsets, c_out);
+    if (rc0) return rc0;
+    if (c_in % 8 == 0) launch_gg<true>(wn, grid, stream, gt, op, buffer_out);
+    else launch_gg<false>(wn, grid, stream, gt, op, buffer_out);
   } else {
     int64_t total = 0;
     for (int k = 0; k < num_offsets; ++k) total = std::max<int64_t>(total, padded_offsets[k] + rows[k]);
