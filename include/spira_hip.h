@@ -120,14 +120,17 @@ int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_t
 int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes);
 
 /* order = the targets of an output-stationary map [>= num_targets, K] sorted
- * (stably) by the bitmask of their valid columns, so that rows with the same
- * neighbour pattern are processed together; row_masks (nullable) receives
- * the sorted bitmasks (bit j: column j valid for j < 63, bit 63: any column
- * >= 63 valid) and ordered_map (nullable, [num_targets, K]) the map rows in
- * that order.  (No reference counterpart: the reference's output-stationary
- * kernels walk targets in index order, cuda/kernels/output_stat.cuh:20-1031.) */
+ * (stably) by neighbour count, most neighbours first, then by the bitmask of
+ * their valid columns, so that rows with the same neighbour pattern are
+ * processed together and the longest blocks start first; group_masks
+ * (nullable, needs K <= 128, [ceil(num_targets / 128), 2]) receives for each
+ * group of 128 consecutive ordered rows the 128-bit union of their valid
+ * columns (word 0: columns 0..63, word 1: 64..127), and ordered_map
+ * (nullable, [num_targets, K]) the map rows in that order.  (No reference
+ * counterpart: the reference's output-stationary kernels walk targets in
+ * index order, cuda/kernels/output_stat.cuh:20-1031.) */
 int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int num_offsets, int32_t *order,
-                             uint64_t *row_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
+                             uint64_t *group_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
 /* ptr[0..n) = value (reference: the cudaMemsetAsync(-1) mask initialisation,
@@ -169,10 +172,10 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
  * dtype; each nullable).  row_order (nullable, [num_targets]) is a
  * permutation of the targets (spira_hip_kmap_row_order) that the fp16 path
  * walks instead of 0..T-1, in which case out_in_map must hold the rows in
- * that order (row i = target row_order[i]); row_masks (nullable, [num_targets]
- * in the same order) are the rows' valid-column bitmasks, which let a block
- * skip offsets none of its rows uses.  Both change the schedule, not the
- * result.
+ * that order (row i = target row_order[i]); group_masks (nullable, needs
+ * num_offsets <= 128) are the 128-row valid-column unions of
+ * spira_hip_kmap_row_order for the rows in that order, which let a block skip
+ * offsets none of its rows uses.  Both change the schedule, not the result.
  * (reference: cuda_sparse_convolution_forward_os,
  * torch/cuda_sparse_convolution_forward.cu:448-496; SparseConvolutionForward_OS
  * cuda/functions/sparse_convolution.cu:1354-1393; kernels
@@ -180,7 +183,7 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
  * the epilogue replaces the separate bias / batch-norm / ReLU / residual ops of
  * source/spira/nn/conv.py:415-416 and scripts/models/spira/modules/blocks.py:12-84). */
 int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
-                      const uint64_t *row_masks, const void *sources,
+                      const uint64_t *group_masks, const void *sources,
                       int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
                       void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
                       int relu, void *workspace, size_t workspace_bytes, hipStream_t stream);

@@ -77,12 +77,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
 namespace ring {
 
 constexpr int KC = 32;  // input channels per step
-constexpr int NS = 3;   // LDS ring depth
 
 // Ring layout: stage s at byte s * STAGE holds the step's weight chunk
 // (B_BYTES: BN rows x 64 B, XOR-swizzled) followed by its gathered rows
 // (A_BYTES: per wave MT tiles x 2 k-halves x 64 lanes x 16 B, lane-linear).
-template <int WN, int MT> struct Cfg {
+template <int WN, int MT, int NS_> struct Cfg {
+  static constexpr int NS = NS_;  // ring depth: NS - 1 steps load while one computes
   static constexpr int BN = 32 * WN;
   static constexpr int BM = 128 * MT;
   static constexpr int BVEC = (BN * 4 + 255) / 256;  // 16-byte weight vectors per thread and step
@@ -94,6 +94,14 @@ template <int WN, int MT> struct Cfg {
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
   static_assert((NS - 1) * STAGE + (WN - 1) * 2048 < 65536, "weight read offset exceeds 16 bits");
   static_assert((NS - 1) * STAGE + (2 * MT - 1) * 1024 < 65536, "row read offset exceeds 16 bits");
+};
+
+// Tile shape per column-tile width: MT 32-row tiles per wave and the ring
+// depth, sized so that two blocks (eight waves) fit a CU's 160 KiB of LDS.
+template <int WN> struct TileOf {
+  static constexpr int MT = WN >= 8 ? 1 : (WN >= 3 ? 2 : 1);
+  static constexpr int NS = WN >= 3 ? 3 : 4;
+  using C = Cfg<WN, MT, NS>;
 };
 
 // compile-time loop: f(std::integral_constant<int, I>) for I in [0, N)
@@ -148,13 +156,12 @@ struct ReadBase {
   uint32_t a;       // rows: + s * STAGE + (m * 2 + ks) * 1024
   uint32_t b0, b1;  // weights, k-half 0 / 1: + s * STAGE + wn * 2048
 };
-template <int WN, int MT> __device__ __forceinline__ ReadBase read_base(const char *ring, int wave) {
-  using C = Cfg<WN, MT>;
+template <class C> __device__ __forceinline__ ReadBase read_base(const char *ring, int wave) {
   const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
   const uint32_t base = lds_addr(ring);
   const int q = (r >> 2) & 3;  // B swizzle: chunk c of row n sits at n * 4 + (c ^ ((n / 4) % 4))
   ReadBase rb;
-  rb.a = base + C::B_BYTES + wave * MT * 2048 + lane * 16;
+  rb.a = base + C::B_BYTES + wave * C::BM / 4 * 64 + lane * 16;
   rb.b0 = base + (r * 4 + (kh ^ q)) * 16;
   rb.b1 = base + (r * 4 + ((2 | kh) ^ q)) * 16;
   return rb;
@@ -163,11 +170,11 @@ template <int WN, int MT> __device__ __forceinline__ ReadBase read_base(const ch
 // Issue the loads of one step into stage S: A rows idx[m] (or -1) at
 // channels kb..kb+31, weight row `wrow`.  When !live every load is out of
 // range, so each wave issues the same number of loads in every step.
-template <int WN, int MT, bool ALIGNED, int S>
-__device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[MT], int wrow, int kb,
-                                      const Operands &op, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr,
-                                      int n0) {
-  using C = Cfg<WN, MT>;
+template <class C, bool ALIGNED, int S>
+__device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
+                                      int kb, const Operands &op, __amdgpu_buffer_rsrc_t xr,
+                                      __amdgpu_buffer_rsrc_t wr, int n0) {
+  constexpr int MT = C::BM / 128;
   const int tid = threadIdx.x, lane = tid & 63;
   const int kh = lane >> 5;
   char *stage = ring + S * C::STAGE;
@@ -207,9 +214,9 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
 }
 
 // MFMAs of stage S (rows without a neighbour hold zeros)
-template <int WN, int MT, int S>
-__device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const ReadBase &rb) {
-  using C = Cfg<WN, MT>;
+template <class C, int S>
+__device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase &rb) {
+  constexpr int MT = C::BM / 128, WN = C::BN / 32;
   unroll<2>([&](auto KS) {
     constexpr int ks = decltype(KS)::value;
     half8 b[WN], a[MT];
@@ -234,7 +241,7 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const ReadBase 
   });
 }
 
-// The pipelined step loop over nsteps steps; stage u % 3 of the ring holds
+// The pipelined step loop over nsteps steps; stage u % NS of the ring holds
 // step u.  Two callbacks describe the steps (S = the stage, a
 // std::integral_constant):
 //  * fetch(u, S) issues exactly PL LDS-DMA loads per wave that bring step
@@ -242,23 +249,24 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[MT][WN], const ReadBase 
 //    so that the vmcnt arithmetic is the same in every wave);
 //  * resolve(u, S, idx, wrow, kb) turns them into the gathered rows idx[m]
 //    (or -1), the weight row and the first input channel of step u.
-// Order of vector-memory operations: F0 F1 F2 D0 F3 D1 F4 | D2 F5 | D3 F6 ...
-// (F = fetch, D = the LPS LDS-DMA loads of a step).  Before step s computes,
-// D(s) must be complete while F(s+3) D(s+1) F(s+4) may still be in flight,
-// hence vmcnt(LPS + 2 PL); F(s+2), which step s+2's issue reads, is older
-// than D(s) and is covered by the same wait.  F(u+3) overwrites the index
-// slot that step u's issue has just read (each wave reads only its own).
-template <int WN, int MT, bool ALIGNED, int PL, class Fetch, class Resolve>
-__device__ __forceinline__ void run(floatx16 (&acc)[MT][WN], int nsteps, Fetch fetch, Resolve resolve,
-                                    const Operands &op, int n0, char *ring) {
-  using C = Cfg<WN, MT>;
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
+// Both are called with u = 0, 1, 2, ... in order (fetch NS steps ahead of
+// resolve).  Issue order: F(0..NS-1), then per step u: D(u) F(u+NS)
+// (D = the LPS LDS-DMA loads of a step, F = a fetch).  Before step s
+// computes, D(s) must be complete while F(s+NS) and D/F of the NS-2 younger
+// steps may still be in flight: vmcnt((NS-2) LPS + (NS-1) PL).  F(s+NS-1),
+// which step s+NS-1's issue reads, is older than D(s) and covered by the
+// same wait.  F(u+NS) overwrites the index slot that step u's issue has
+// just read (each wave reads only its own slot).  Steps past nsteps (at most
+// NS-1) compute on all-zero stages, so the trip is uniform and the
+// accumulators stay in place.
+template <class C, bool ALIGNED, int PL, class Fetch, class Resolve>
+__device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], int nsteps, Fetch fetch,
+                                    Resolve resolve, const Operands &op, int n0, char *ring) {
+  constexpr int MT = C::BM / 128, NS = C::NS;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
-  const ReadBase rb = read_base<WN, MT>(ring, wave);
+  const ReadBase rb = read_base<C>(ring, wave);
   auto put = [&](int u, auto St) {
     int32_t idx[MT];
     int wrow = 0;
@@ -269,38 +277,57 @@ __device__ __forceinline__ void run(floatx16 (&acc)[MT][WN], int nsteps, Fetch f
 #pragma unroll
       for (int m = 0; m < MT; ++m) idx[m] = -1;
     }
-    issue<WN, MT, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, wr, n0);
+    issue<C, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, wr, n0);
   };
-  fetch(0, S0{});
-  fetch(1, S1{});
-  fetch(2, S2{});
-  if constexpr (PL > 0) wait_vm<2 * PL>();  // F0 is older than F1 F2
-  put(0, S0{});
-  fetch(3, S0{});
-  if constexpr (PL > 0) wait_vm<C::LPS + 2 * PL>();  // F1 is older than F2 D0 F3
-  put(1, S1{});
-  fetch(4, S1{});
-  for (int s = 0; s < nsteps; s += 3) {
-    wait_vm<C::LPS + 2 * PL>();
-    __builtin_amdgcn_s_barrier();
-    put(s + 2, S2{});
-    fetch(s + 5, S2{});
-    compute<WN, MT, 0>(acc, rb);
-    // Steps past nsteps (at most two) compute on all-zero stages: the trip
-    // is uniform, with a single loop exit that keeps the accumulators in place.
-    wait_vm<C::LPS + 2 * PL>();
-    __builtin_amdgcn_s_barrier();
-    put(s + 3, S0{});
-    fetch(s + 6, S0{});
-    compute<WN, MT, 1>(acc, rb);
-    wait_vm<C::LPS + 2 * PL>();
-    __builtin_amdgcn_s_barrier();
-    put(s + 4, S1{});
-    fetch(s + 7, S1{});
-    compute<WN, MT, 2>(acc, rb);
+  unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
+  unroll<NS - 1>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    if constexpr (PL > 0) wait_vm<(NS - 1) * PL + i * C::LPS>();  // F(i) is older than these
+    put(i, I);
+    fetch(i + NS, I);
+  });
+  for (int s = 0; s < nsteps; s += NS) {
+    unroll<NS>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      constexpr int slot = (i + NS - 1) % NS;
+      wait_vm<(NS - 2) * C::LPS + (NS - 1) * PL>();
+      __builtin_amdgcn_s_barrier();
+      put(s + i + NS - 1, std::integral_constant<int, slot>{});
+      fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
+      compute<C, i>(acc, rb);
+    });
   }
   wait_vm<0>();
 }
+
+// Scalar iterator over the set bits of a 128-bit offset set, nch channel
+// chunks per offset: step() moves to the next (offset, chunk).
+struct StepIter {
+  uint64_t lo, hi;  // offsets not yet started (relative to j0)
+  int j;            // current offset (relative)
+  int chunk;
+  __device__ __forceinline__ static int first(uint64_t lo, uint64_t hi) {
+    return lo ? __builtin_ctzll(lo) : (hi ? 64 + __builtin_ctzll(hi) : 0);
+  }
+  __device__ __forceinline__ void init(uint64_t l, uint64_t h) {
+    lo = l;
+    hi = h;
+    j = first(lo, hi);
+    drop();
+    chunk = 0;
+  }
+  __device__ __forceinline__ void drop() {
+    if (j < 64) lo &= ~(uint64_t(1) << j);
+    else hi &= ~(uint64_t(1) << (j - 64));
+  }
+  __device__ __forceinline__ void step(int nch) {
+    if (++chunk == nch) {
+      chunk = 0;
+      j = first(lo, hi);
+      drop();
+    }
+  }
+};
 
 }  // namespace ring
 
@@ -349,65 +376,62 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[WN], const int3
   }
 }
 
-#define SPIRA_RING_STAGES(C) __shared__ __align__(1024) char ring_lds[C::RING]
+#ifdef SPIRA_BLOCK_TIMING
+// experiment builds only: per-block wall-clock stamps of the OS kernel
+__device__ int64_t g_block_times[1 << 20];
+#define SPIRA_STAMP(slot) \
+  if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + (slot)] = wall_clock64()
+#else
+#define SPIRA_STAMP(slot)
+#endif
 
 // Output-stationary implicit GEMM.  A block owns BM = 128*MT logical rows
 // (wave w: rows [w*32*MT, (w+1)*32*MT) as MT tiles of 32) and BN = 32*WN
 // output channels; grid = (row blocks, column blocks, offset splits), split z
-// covering offsets [z*jper, min(Kc, (z+1)*jper)).  With `order`, logical row
-// i is target order[i] and `map` holds the rows in logical order; `rowmask`
-// (logical order, bit j = column j valid, bit 63 = some column >= 63 valid)
+// covering offsets [z*jper, min(Kc, (z+1)*jper)), jper <= 128.  With `order`,
+// logical row i is target order[i] and `map` holds the rows in logical order;
+// `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
-template <int WN, int MT, int MODE, bool ALIGNED>
+template <int WN, int MODE, bool ALIGNED>
 __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
-                                                    const uint64_t *__restrict__ rowmask, int64_t T, int Kc, int jper,
+                                                    const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
                                                     Operands op, void *Y, Epilogue epi) {
-  using C = ring::Cfg<WN, MT>;
-  SPIRA_RING_STAGES(C);
-  __shared__ __align__(16) int32_t idx_lds[ring::NS][256];  // map entries of a later step, per stage
-  __shared__ int32_t act[65];
-  __shared__ unsigned flag[2];
+  using C = typename ring::TileOf<WN>::C;
+  constexpr int MT = C::BM / 128, NS = C::NS;
+  __shared__ __align__(1024) char ring_lds[C::RING];
+  __shared__ __align__(16) int32_t idx_lds[NS][256];  // map entries of a later step, per stage
   __shared__ int32_t orow_s[4][32 * MT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, kh = lane >> 5;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * C::BM;
   const int n0 = blockIdx.y * C::BN;
   const int j0 = blockIdx.z * jper;
-  const int j1 = (j0 + jper) < Kc ? (j0 + jper) : Kc;
-  const int jn = j1 - j0;
-  // offsets used by some row of the block
-  if (tid < 2) flag[tid] = 0;
-  __syncthreads();
-  if (rowmask && Kc <= 63) {
-    uint64_t used = 0;
-    for (int rr = tid; rr < C::BM; rr += 256) {
-      const int64_t lr = row0 + rr;
-      if (lr < T) used |= rowmask[lr];
+  const int jn = ((j0 + jper) < Kc ? (j0 + jper) : Kc) - j0;
+  SPIRA_STAMP(0);
+  // offsets [j0, j0 + jn) used by some row of the block, relative to j0
+  uint64_t ulo = jn >= 64 ? ~uint64_t(0) : (uint64_t(1) << jn) - 1;
+  uint64_t uhi = jn >= 128 ? ~uint64_t(0) : (jn > 64 ? (uint64_t(1) << (jn - 64)) - 1 : 0);
+  if (gmask) {
+    uint64_t glo = 0, ghi = 0;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int64_t g = row0 / 128 + m;
+      if (g * 128 < T) {
+        glo |= gmask[g * 2];
+        ghi |= gmask[g * 2 + 1];
+      }
     }
-    used = (used >> j0) & (jn >= 64 ? ~uint64_t(0) : ((uint64_t(1) << jn) - 1));
-    if (used) {
-      atomicOr(&flag[0], static_cast<unsigned>(used));
-      atomicOr(&flag[1], static_cast<unsigned>(used >> 32));
-    }
-  } else if (tid == 0) {
-    const uint64_t all = jn >= 64 ? ~uint64_t(0) : ((uint64_t(1) << jn) - 1);
-    flag[0] = static_cast<unsigned>(all);
-    flag[1] = static_cast<unsigned>(all >> 32);
+    // shift the 128-bit union right by j0 (0 <= j0 < 128)
+    const uint64_t slo = j0 == 0 ? glo : (j0 < 64 ? (glo >> j0) | (ghi << (64 - j0)) : ghi >> (j0 - 64));
+    const uint64_t shi = j0 == 0 ? ghi : (j0 < 64 ? ghi >> j0 : 0);
+    ulo &= slo;
+    uhi &= shi;
   }
-  __syncthreads();
-  if (tid == 0) {
-    uint64_t used = static_cast<uint64_t>(flag[0]) | (static_cast<uint64_t>(flag[1]) << 32);
-    int n = 0;
-    while (used) {
-      act[n++] = j0 + __builtin_ctzll(used);
-      used &= used - 1;
-    }
-    act[64] = n;
-  }
-  __syncthreads();
-  const int nact = act[64];
+  const int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
   const int nch = (op.CinP + ring::KC - 1) / ring::KC;
+  const int nsteps = nact * nch;
+  SPIRA_STAMP(1);
 
   floatx16 acc[MT][WN];
   zero_acc<WN, MT>(acc);
@@ -416,21 +440,26 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   for (int m = 0; m < MT; ++m) mvalid[m] = row0 + wave * 32 * MT + m * 32 + r < T;
   // Map entries of step u: lane L of a wave fetches row L (MT = 2) or row
   // L % 32 (MT = 1) of the wave's rows into the stage's index slot; rows past
-  // T fetch row 0 and are masked when resolved.  Every address stays inside
-  // map: the row is < T (or 0) and the column < Kc.
-  const int nsteps = nact * nch;
+  // T read nothing (out of range) and are masked when resolved.
   const int frow = MT == 2 ? lane : r;
   const int64_t flr = row0 + wave * 32 * MT + frow;
-  const uint32_t fbase = flr < T ? static_cast<uint32_t>(flr * Kc) * 4u : kOutOfRange;
+  const uint32_t fbase = flr < T ? static_cast<uint32_t>(flr * Kc + j0) * 4u : kOutOfRange;
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(map, static_cast<uint32_t>(T * Kc * 4));
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + r) * 4;
+  ring::StepIter fit, pit;  // fetch side (runs NS steps ahead) and issue side
+  fit.init(ulo, uhi);
+  pit = fit;
+  int fu = 0;
   auto fetch = [&](int u, auto St) {
-    // act[] holds nact entries (possibly none): steps past the end read column 0
-    const int j = u < nsteps ? act[u / nch] : 0;
-    ring::dma4(mr, fbase == kOutOfRange ? kOutOfRange : fbase + j * 4u, &idx_lds[decltype(St)::value][uwave * 64]);
+    (void)u;
+    const uint32_t off = (fbase == kOutOfRange || fu >= nsteps) ? kOutOfRange : fbase + fit.j * 4u;
+    ring::dma4(mr, off, &idx_lds[decltype(St)::value][uwave * 64]);
+    ++fu;
+    fit.step(nch);
   };
   auto resolve = [&](int u, auto St, int32_t (&idx)[MT], int &wrow, int &kb) {
+    (void)u;
     ring::unroll<MT>([&](auto M) {
       idx[decltype(M)::value] = ring::rd4<decltype(St)::value * 1024 + decltype(M)::value * 128>(ibase);
     });
@@ -440,10 +469,15 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
       ring::pin(idx[m]);
       if (!mvalid[m]) idx[m] = -1;
     }
-    wrow = act[u / nch];
-    kb = (u % nch) * ring::KC;
+    wrow = j0 + pit.j;
+    kb = pit.chunk * ring::KC;
+    pit.step(nch);
   };
-  ring::run<WN, MT, ALIGNED, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  SPIRA_STAMP(2);
+#ifdef SPIRA_BLOCK_TIMING
+  if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = nact;
+#endif
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -462,13 +496,14 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
 // with Kw > 0 tiles [nfwd, 2 nfwd) apply the mirrored pass (out -> in) with
 // W[woffset + Kw-1-r] except for a self-mirrored centre row.  Results are
 // atomically added to an fp32 buffer.
-template <int WN, int MT, bool ALIGNED>
+template <int WN, bool ALIGNED>
 __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ in_idx,
                                                     const int32_t *__restrict__ out_idx,
                                                     const int32_t *__restrict__ naddrs, int R, int64_t nfwd, int Kw,
                                                     int woffset, Operands op, float *__restrict__ Yacc) {
-  using C = ring::Cfg<WN, MT>;
-  SPIRA_RING_STAGES(C);
+  using C = typename ring::TileOf<WN>::C;
+  constexpr int MT = C::BM / 128;
+  __shared__ __align__(1024) char ring_lds[C::RING];
   __shared__ int32_t tstart[kMaxGroups + 1];
   __shared__ int32_t orow_s[4][32 * MT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -523,7 +558,7 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
     kb = u * ring::KC;
   };
   const int nch = (op.CinP + ring::KC - 1) / ring::KC;
-  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = dst[m];
@@ -542,10 +577,11 @@ struct GroupTable {
 };
 
 // Grouped GEMM over the padded gather buffer: Ybuf[rows of g] = Xbuf[rows of g] @ W[g].
-template <int WN, int MT, bool ALIGNED>
+template <int WN, bool ALIGNED>
 __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operands op, float *__restrict__ Yb) {
-  using C = ring::Cfg<WN, MT>;
-  SPIRA_RING_STAGES(C);
+  using C = typename ring::TileOf<WN>::C;
+  constexpr int MT = C::BM / 128;
+  __shared__ __align__(1024) char ring_lds[C::RING];
   __shared__ int32_t orow_s[4][32 * MT];
   const int64_t tile = blockIdx.x;
   int g = 0, ghi = gt.n;  // last group with tile_start[g] <= tile
@@ -573,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operand
     kb = u * ring::KC;
   };
   const int nch = (op.CinP + ring::KC - 1) / ring::KC;
-  ring::run<WN, MT, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = src[m];
@@ -778,12 +814,20 @@ static inline int wn_for(int Cout) {
   if (Cout <= 128) return 4;
   return 8;
 }
-// 32-row tiles per wave: accumulators stay <= 128 VGPRs
-template <int WN> struct MtOf { static constexpr int value = WN >= 8 ? 1 : 2; };
-static inline int mt_for(int wn) { return wn >= 8 ? 1 : 2; }
+// rows per block of the MMA kernels for a column-tile width
+static inline int bm_for(int wn) {
+  switch (wn) {
+    case 1: return ring::TileOf<1>::C::BM;
+    case 2: return ring::TileOf<2>::C::BM;
+    case 3: return ring::TileOf<3>::C::BM;
+    case 4: return ring::TileOf<4>::C::BM;
+    default: return ring::TileOf<8>::C::BM;
+  }
+}
 
 // offsets per split: small layers split their offsets so that the grid
-// covers the chip; a split never exceeds 64 offsets (the active-offset list)
+// covers the chip; a split never exceeds 128 offsets (the block's 128-bit
+// active-offset set)
 static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
   int jper = Kc;
   const int64_t want = static_cast<int64_t>(cus);
@@ -791,7 +835,7 @@ static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
     const int64_t splits = std::min<int64_t>(Kc, div_up(want, blocks_xy));
     jper = static_cast<int>(div_up(Kc, splits));
   }
-  return std::min(jper, 64);
+  return std::min(jper, 128);
 }
 
 // Operands of the MMA core; byte sizes must fit the 31-bit buffer offsets
@@ -810,7 +854,7 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
   return kOk;
 }
 
-// launch `K<WN, MtOf<WN>, ...>` for the column-tile width chosen at run time
+// launch `K<WN, ...>` for the column-tile width chosen at run time
 #define SPIRA_WN_SWITCH(wn, CALL) \
   switch (wn) {                   \
     case 1: CALL(1); break;       \
@@ -825,7 +869,7 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op, void *Y,
                       const Epilogue &epi) {
 #define SPIRA_OS_CALL(W)                                                                                         \
-  hipLaunchKernelGGL((os_kernel<W, MtOf<W>::value, MODE, AL>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
                      jper, op, Y, epi)
   SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
 #undef SPIRA_OS_CALL
@@ -844,7 +888,7 @@ static void launch_ws(int wn, dim3 grid, hipStream_t s, const int32_t *in_idx, c
                       const int32_t *naddrs, int R, int64_t nfwd, int Kw, int woffset, const Operands &op,
                       float *Yacc) {
 #define SPIRA_WS_CALL(W)                                                                                       \
-  hipLaunchKernelGGL((ws_kernel<W, MtOf<W>::value, AL>), grid, dim3(256), 0, s, in_idx, out_idx, naddrs, R, nfwd, \
+  hipLaunchKernelGGL((ws_kernel<W, AL>), grid, dim3(256), 0, s, in_idx, out_idx, naddrs, R, nfwd, \
                      Kw, woffset, op, Yacc)
   SPIRA_WN_SWITCH(wn, SPIRA_WS_CALL)
 #undef SPIRA_WS_CALL
@@ -853,7 +897,7 @@ static void launch_ws(int wn, dim3 grid, hipStream_t s, const int32_t *in_idx, c
 template <bool AL>
 static void launch_gg(int wn, dim3 grid, hipStream_t s, const GroupTable &gt, const Operands &op, float *Yb) {
 #define SPIRA_GG_CALL(W) \
-  hipLaunchKernelGGL((gg_kernel<W, MtOf<W>::value, AL>), grid, dim3(256), 0, s, gt, op, Yb)
+  hipLaunchKernelGGL((gg_kernel<W, AL>), grid, dim3(256), 0, s, gt, op, Yb)
   SPIRA_WN_SWITCH(wn, SPIRA_GG_CALL)
 #undef SPIRA_GG_CALL
 }
@@ -900,6 +944,12 @@ using namespace spira_hip;
 
 extern "C" {
 
+#ifdef SPIRA_BLOCK_TIMING
+int spira_hip_debug_block_times(int64_t *out, int n) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_block_times), sizeof(int64_t) * n) == hipSuccess ? 0 : 1;
+}
+#endif
+
 int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes) {
   *bytes = mfma_path(dtype) ? static_cast<size_t>(num_offsets) * pad_in(c_in) * pad_out(c_out) * sizeof(_Float16) : 0;
   return kOk;
@@ -924,7 +974,7 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
   *bytes = 0;
   if (!mfma_path(dtype) || out_mode != SPIRA_OUT_STORE || num_targets <= 0) return kOk;
   const int wn = wn_for(c_out);
-  const int bm = 128 * mt_for(wn);
+  const int bm = bm_for(wn);
   const int64_t blocks = div_up(num_targets, bm) * div_up(pad_out(c_out), 32 * wn);
   if (choose_jper(blocks, num_offsets, device_cu_count()) < num_offsets)
     *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
@@ -932,7 +982,7 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
 }
 
 int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
-                      const uint64_t *row_masks, const void *sources,
+                      const uint64_t *group_masks, const void *sources,
                       int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
                       void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
                       int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -941,13 +991,14 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
   SPIRA_HIP_REQUIRE(c_in > 0 && c_out > 0 && num_offsets > 0, "conv_os: empty channel / offset dimension");
   SPIRA_HIP_REQUIRE(out_mode == SPIRA_OUT_STORE || (!scale && !shift && !residual && !relu),
                     "conv_os: the epilogue applies to the storage-dtype output only");
+  SPIRA_HIP_REQUIRE(group_masks == nullptr || num_offsets <= 128, "conv_os: group masks need <= 128 offsets");
   if (num_targets <= 0) return kOk;
   const Epilogue epi = make_epi(scale, shift, residual, relu);
   if (mfma_path(dtype)) {
     SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
     const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
     const int wn = wn_for(c_out);
-    const int bm = 128 * mt_for(wn);
+    const int bm = bm_for(wn);
     const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
     const int jper = choose_jper(bx * by, num_offsets, device_cu_count());
     const int splits = static_cast<int>(div_up(num_offsets, jper));
@@ -958,11 +1009,11 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     if (rc0) return rc0;
     if (splits == 1) {
       if (out_mode == SPIRA_OUT_STORE)
-        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
       else if (out_mode == SPIRA_OUT_STORE_F32)
-        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
       else
-        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
     } else {
       float *acc = nullptr;
       if (out_mode == SPIRA_OUT_STORE) {
@@ -976,7 +1027,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
         int rc = fill_f32(acc, num_targets * c_out, 0.f, stream);
         if (rc) return rc;
       }
-      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, row_masks, num_targets, num_offsets, jper, op, acc, epi);
+      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, acc, epi);
       SPIRA_HIP_LAUNCH_CHECK();
       if (out_mode == SPIRA_OUT_STORE)
         hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(num_targets * c_out, 256)), dim3(256), 0, stream,
@@ -1013,7 +1064,7 @@ int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int3
     SPIRA_HIP_REQUIRE(rows <= kMaxGroups, "conv_ws_fused: at most 128 offset rows");
     const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
     const int wn = wn_for(c_out);
-    const int bm = 128 * mt_for(wn);
+    const int bm = bm_for(wn);
     // tiles: sum over rows of ceil(rows_r / bm) <= num_pairs / bm + rows
     const int64_t nfwd = div_up(num_pairs, bm) + rows;
     (void)quantized_pairs;
@@ -1065,7 +1116,7 @@ int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padde
                       int dtype, const void *buffer_in, const void *weights, const void *prepared, float *buffer_out,
                       hipStream_t stream) {
   GroupTable gt{};
-  const int bm = 128 * mt_for(wn_for(c_out));
+  const int bm = bm_for(wn_for(c_out));
   int rc = fill_groups(gt, num_offsets, rows, padded_offsets, bm);
   if (rc) return rc;
   if (num_offsets <= 0) return kOk;

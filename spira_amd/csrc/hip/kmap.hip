@@ -428,16 +428,54 @@ __global__ void convert_transposed_kernel(const int32_t *__restrict__ map, int64
 // Row-order key of an output-stationary map row: the bitmask of its valid
 // columns (the first 63 columns, with bit 63 flagging any valid column past
 // them), so that sorting groups rows with identical neighbour patterns.
+// Sort key of a map row: rows with more neighbours first (their blocks run
+// longest, so they are dispatched first), then rows with the same neighbour
+// pattern together.  With K <= 58 the key is exact: (K - popcount) in bits
+// 58..63 above the K-bit pattern; wider maps keep the first 57 offsets of the
+// pattern under a 7-bit (127 - popcount) field.
 __global__ void row_mask_kernel(const int32_t *__restrict__ map, int64_t T, int K, uint64_t *__restrict__ keys,
                                 int32_t *__restrict__ iota) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= T) return;
   const int32_t *row = map + t * K;
   uint64_t m = 0;
-  for (int j = 0; j < K; ++j)
-    if (row[j] >= 0) m |= (j < 63) ? (uint64_t(1) << j) : (uint64_t(1) << 63);
-  keys[t] = m;
+  int cnt = 0;
+  for (int j = 0; j < K; ++j) {
+    const bool v = row[j] >= 0;
+    cnt += v;
+    if (v && j < 58) m |= uint64_t(1) << j;
+  }
+  keys[t] = K <= 58 ? (static_cast<uint64_t>(K - cnt) << 58) | m
+                    : (static_cast<uint64_t>(127 - (cnt < 127 ? cnt : 127)) << 57) | (m & ((uint64_t(1) << 57) - 1));
   iota[t] = static_cast<int32_t>(t);
+}
+
+// 128-bit union of the valid columns of each group of 128 consecutive rows of
+// `map` (rows in the order of `order` when given): one wave per group.
+__global__ void group_mask_kernel(const int32_t *__restrict__ map, const int32_t *__restrict__ order, int64_t T,
+                                  int K, int64_t groups, uint64_t *__restrict__ out) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (g >= groups) return;
+  const int lane = threadIdx.x & 63;
+  uint64_t lo = 0, hi = 0;
+  for (int h = 0; h < 2; ++h) {
+    const int64_t i = g * 128 + h * 64 + lane;
+    if (i >= T) continue;
+    const int32_t *row = map + (order ? static_cast<int64_t>(order[i]) : i) * K;
+    for (int j = 0; j < K && j < 128; ++j)
+      if (row[j] >= 0) {
+        if (j < 64) lo |= uint64_t(1) << j;
+        else hi |= uint64_t(1) << (j - 64);
+      }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    lo |= static_cast<uint64_t>(__shfl_xor(lo, o, 64));
+    hi |= static_cast<uint64_t>(__shfl_xor(hi, o, 64));
+  }
+  if (lane == 0) {
+    out[g * 2] = lo;
+    out[g * 2 + 1] = hi;
+  }
 }
 
 // ordered[i, :] = map[order[i], :]
@@ -570,10 +608,11 @@ int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes) {
 }
 
 int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int num_offsets, int32_t *order,
-                             uint64_t *row_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
+                             uint64_t *group_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
                              hipStream_t stream) {
   SPIRA_HIP_REQUIRE(num_targets >= 0 && num_targets < (int64_t(1) << 31), "kmap_row_order: size out of range");
   SPIRA_HIP_REQUIRE(num_offsets >= 1, "kmap_row_order: no offsets");
+  SPIRA_HIP_REQUIRE(group_masks == nullptr || num_offsets <= 128, "kmap_row_order: group masks need <= 128 offsets");
   if (num_targets == 0) return kOk;
   size_t sb = 0;
   const size_t need = row_order_parts(num_targets, &sb);
@@ -589,13 +628,18 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
   hipLaunchKernelGGL(row_mask_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, num_targets,
                      num_offsets, keys, iota);
   SPIRA_HIP_LAUNCH_CHECK();
-  const int bits = num_offsets >= 63 ? 64 : num_offsets;
-  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, sb, keys, row_masks ? row_masks : keys_out, iota, order,
-                                          static_cast<size_t>(num_targets), 0, bits, stream));
+  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, sb, keys, keys_out, iota, order, static_cast<size_t>(num_targets), 0, 64,
+                                          stream));
   if (ordered_map) {
     const int64_t n = num_targets * num_offsets;
     hipLaunchKernelGGL(gather_rows_kernel, dim3(div_up(n, 256)), dim3(256), 0, stream, out_in_map, order,
                        num_targets, num_offsets, ordered_map);
+    SPIRA_HIP_LAUNCH_CHECK();
+  }
+  if (group_masks) {
+    const int64_t groups = div_up(num_targets, 128);
+    hipLaunchKernelGGL(group_mask_kernel, dim3(div_up(groups, 4)), dim3(256), 0, stream, out_in_map, order,
+                       num_targets, num_offsets, groups, group_masks);
     SPIRA_HIP_LAUNCH_CHECK();
   }
   return kOk;

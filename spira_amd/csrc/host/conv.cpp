@@ -123,13 +123,15 @@ static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
   e.T = T;
   const int64_t K = map.size(1);
   e.order = empty_i32({std::max<int64_t>(T, 1)}, map.device());
-  e.masks = torch::empty({std::max<int64_t>(T, 1)}, torch::TensorOptions(map.device()).dtype(torch::kInt64));
+  // 128-bit valid-column unions per 128 ordered rows (maps of <= 128 offsets)
+  if (K <= 128)
+    e.masks = torch::empty({(T + 127) / 128 * 2}, torch::TensorOptions(map.device()).dtype(torch::kInt64));
   e.ordered_map = empty_i32({std::max<int64_t>(T, 1), K}, map.device());
   size_t wsb = 0;
   check_rc(spira_hip_kmap_row_order_workspace(T, &wsb), "row_order");
   auto ws = workspace(wsb, map.device());
   check_rc(spira_hip_kmap_row_order(map.data_ptr<int32_t>(), T, static_cast<int>(K), e.order.data_ptr<int32_t>(),
-                                    reinterpret_cast<uint64_t *>(e.masks.data_ptr<int64_t>()),
+                                    e.masks.defined() ? reinterpret_cast<uint64_t *>(e.masks.data_ptr<int64_t>()) : nullptr,
                                     e.ordered_map.data_ptr<int32_t>(), ws.data_ptr(), wsb, current_stream()),
            "row_order");
   return cache.emplace(key, std::move(e)).first->second;
@@ -180,7 +182,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
-    masks = reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>());
+    masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
     mp = oe.ordered_map.data_ptr<int32_t>();
   }
   check_rc(spira_hip_conv_os(T, K, mp, order, masks, X.data_ptr(), S, W.size(1), wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
