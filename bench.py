@@ -40,6 +40,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--dataflow", type=int, default=0, help="map dataflow used by every layer")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-fuse", action="store_true", help="run batch norm / ReLU / residual adds unfused")
     p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer")
     return p.parse_args()
 
@@ -72,6 +73,8 @@ def e2e_leg(torch, args, coords_np):
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     model = SparseResUNet42(in_channels=3).to(dev).half().eval()
+    if not args.no_fuse:
+        spira_amd.nn.fuse_epilogues(model)
     cache = spira_amd.nn.KernelMapCache()
     spira_amd.set_kernel_map_cache(model, cache)
     for m in model.modules():

@@ -220,13 +220,13 @@ int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padde
                       int dtype, const void *buffer_in, const void *weights, const void *prepared, float *buffer_out,
                       hipStream_t stream);
 
-/* Scatter: targets[t] = base[t] + sum_k buffer[padded_offsets[k] + target_masks[k, t]]
- * (base: nullable fp32 [num_targets, c_out])
+/* Scatter: targets[t] = epilogue(base[t] + sum_k buffer[padded_offsets[k] + target_masks[k, t]])
+ * (base: nullable fp32 [num_targets, c_out]; the epilogue of spira_hip_conv_os)
  * (reference: Scatter / PaddedScatterWarpOptimized,
  * cuda/functions/sparse_convolution.cu:699-742, cuda/kernels/padded_scatter_warp_optimized.cuh:11-63). */
 int spira_hip_ws_scatter(int64_t num_targets, int c_out, int num_offsets, int dtype, const int32_t *target_masks,
-                         const int64_t *padded_offsets, const float *buffer, const float *base, void *targets,
-                         hipStream_t stream);
+                         const int64_t *padded_offsets, const float *buffer, const float *base, const float *scale,
+                         const float *shift, const void *residual, int relu, void *targets, hipStream_t stream);
 
 /* targets (storage dtype) = epilogue(acc) for an fp32 accumulation buffer
  * [num_targets, c_out], with the epilogue of spira_hip_conv_os (reference:

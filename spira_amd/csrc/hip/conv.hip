@@ -787,7 +787,7 @@ template <typename FT>
 __global__ __launch_bounds__(256) void scatter_kernel(const OffsetTable ot, int64_t T, int Cout,
                                                       const int32_t *__restrict__ tmask,
                                                       const float *__restrict__ buf, FT *__restrict__ Y,
-                                                      const float *__restrict__ base) {
+                                                      const float *__restrict__ base, Epilogue epi) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= T * Cout) return;
   const int64_t t = i / Cout;
@@ -797,6 +797,10 @@ __global__ __launch_bounds__(256) void scatter_kernel(const OffsetTable ot, int6
     const int32_t m = tmask[k * T + t];
     if (m >= 0) acc += buf[(ot.off[k] + m) * Cout + c];
   }
+  if (epi.scale) acc *= epi.scale[c];
+  if (epi.shift) acc += epi.shift[c];
+  if (epi.residual) acc += static_cast<float>(static_cast<const FT *>(epi.residual)[i]);
+  if (epi.relu) acc = acc > 0.f ? acc : 0.f;
   Y[i] = static_cast<FT>(acc);
 }
 
@@ -1148,8 +1152,9 @@ int spira_hip_ws_gemm(int num_offsets, const int32_t *rows, const int64_t *padde
 }
 
 int spira_hip_ws_scatter(int64_t num_targets, int c_out, int num_offsets, int dtype, const int32_t *target_masks,
-                         const int64_t *padded_offsets, const float *buffer, const float *base, void *targets,
-                         hipStream_t stream) {
+                         const int64_t *padded_offsets, const float *buffer, const float *base, const float *scale,
+                         const float *shift, const void *residual, int relu, void *targets, hipStream_t stream) {
+  const Epilogue epi = make_epi(scale, shift, residual, relu);
   SPIRA_HIP_REQUIRE(num_offsets <= kMaxGroups, "ws_scatter: at most 128 offsets");
   if (num_targets <= 0) return kOk;
   OffsetTable ot{};
@@ -1158,10 +1163,10 @@ int spira_hip_ws_scatter(int64_t num_targets, int c_out, int num_offsets, int dt
   const int64_t n = num_targets * c_out;
   if (dtype == SPIRA_F16)
     hipLaunchKernelGGL(scatter_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream, ot, num_targets, c_out,
-                       target_masks, buffer, static_cast<_Float16 *>(targets), base);
+                       target_masks, buffer, static_cast<_Float16 *>(targets), base, epi);
   else
     hipLaunchKernelGGL(scatter_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, ot, num_targets, c_out,
-                       target_masks, buffer, static_cast<float *>(targets), base);
+                       target_masks, buffer, static_cast<float *>(targets), base, epi);
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }

@@ -156,6 +156,34 @@ struct Epi {
   int relu = 0;
 };
 
+// Epilogue operands from the optional tensors of the torch API
+// (scale / shift fp32 [C], residual [T, C] in the feature dtype).
+static Epi epi_of(const std::optional<torch::Tensor> &scale, const std::optional<torch::Tensor> &shift,
+                  const std::optional<torch::Tensor> &residual, bool relu, int64_t T, int64_t C,
+                  const torch::Tensor &X) {
+  Epi e;
+  auto vec = [&](const std::optional<torch::Tensor> &v, const char *name) -> const float * {
+    if (!v.has_value() || !v->defined()) return nullptr;
+    SPIRA_CHECK_ARG(v->scalar_type() == torch::kFloat && v->numel() == C && v->is_contiguous(), name,
+                    " must be a contiguous fp32 vector of ", C, " channels");
+    require_device(*v, name);
+    return v->data_ptr<float>();
+  };
+  e.scale = vec(scale, "scale");
+  e.shift = vec(shift, "shift");
+  if (residual.has_value() && residual->defined()) {
+    SPIRA_CHECK_ARG(residual->scalar_type() == X.scalar_type() && residual->dim() == 2 && residual->size(0) == T &&
+                        residual->size(1) == C && residual->is_contiguous(),
+                    "residual must be a contiguous [", T, ", ", C, "] tensor of the feature dtype");
+    require_device(*residual, "residual");
+    e.residual = residual->data_ptr();
+  }
+  e.relu = relu ? 1 : 0;
+  return e;
+}
+
+static bool epi_empty(const Epi &e) { return !e.scale && !e.shift && !e.residual && !e.relu; }
+
 static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
                    int w0, int K, void *out, int mode, const Epi &epi = Epi()) {
   const auto dev = X.device();
@@ -193,13 +221,16 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
 
 // (reference: CUDASparseConvolutionForward_OS, :448-496)
 torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const torch::Tensor &X,
-                         const torch::Tensor &W) {
+                         const torch::Tensor &W, const std::optional<torch::Tensor> &scale,
+                         const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
+                         bool relu) {
   check_features(X, W);
   SPIRA_CHECK_ARG(out_in_map.dim() == 2, "out_in_map must be 2-D");
   SPIRA_CHECK_ARG(W.size(0) == out_in_map.size(1), "weights have ", W.size(0), " offsets, map has ",
                   out_in_map.size(1));
   auto Y = torch::empty({T, W.size(2)}, X.options());
-  run_os(&out_in_map, S, T, X, W, 0, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE);
+  run_os(&out_in_map, S, T, X, W, 0, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE,
+         epi_of(scale, shift, residual, relu, T, W.size(2), X));
   return Y;
 }
 
@@ -294,8 +325,10 @@ static void gs_gemm(GsPlan &p, const torch::Tensor &W, int woff, hipStream_t s) 
            "gemm");
 }
 
-static void gs_scatter(GsPlan &p, int cout, int dtype, const float *base, void *Y, hipStream_t s) {
-  check_rc(spira_hip_ws_scatter(p.T, cout, p.Km, dtype, p.tmask, p.off.data(), p.bout.data_ptr<float>(), base, Y, s),
+static void gs_scatter(GsPlan &p, int cout, int dtype, const float *base, void *Y, hipStream_t s,
+                       const Epi &e = Epi()) {
+  check_rc(spira_hip_ws_scatter(p.T, cout, p.Km, dtype, p.tmask, p.off.data(), p.bout.data_ptr<float>(), base,
+                                e.scale, e.shift, e.residual, e.relu, Y, s),
            "scatter");
 }
 
@@ -303,7 +336,9 @@ static void gs_scatter(GsPlan &p, int cout, int dtype, const float *base, void *
 torch::Tensor forward_ws(int64_t S, int64_t T, int64_t gather_tile, int64_t scatter_tile, int64_t parallel,
                          const std::optional<double> &threshold, const torch::Tensor &X, const torch::Tensor &W,
                          const torch::Tensor &source_masks, const torch::Tensor &target_masks,
-                         const torch::Tensor &nbsizes) {
+                         const torch::Tensor &nbsizes, const std::optional<torch::Tensor> &scale,
+                         const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
+                         bool relu) {
   (void)gather_tile;
   (void)scatter_tile;
   (void)parallel;
@@ -317,7 +352,7 @@ torch::Tensor forward_ws(int64_t S, int64_t T, int64_t gather_tile, int64_t scat
   auto s = current_stream();
   gs_gather(p, X, s);
   gs_gemm(p, W, 0, s);
-  gs_scatter(p, W.size(2), dtype_of(X), nullptr, Y.data_ptr(), s);
+  gs_scatter(p, W.size(2), dtype_of(X), nullptr, Y.data_ptr(), s, epi_of(scale, shift, residual, relu, T, W.size(2), X));
   return Y;
 }
 
@@ -344,11 +379,11 @@ static void ws_fused_into(int64_t S, int64_t T, const torch::Tensor &X, const to
            "sparse_convolution_forward_ws_merged");
 }
 
-static torch::Tensor finish_acc(const torch::Tensor &acc, const torch::Tensor &X) {
-  if (X.scalar_type() == torch::kFloat) return acc;
+static torch::Tensor finish_acc(const torch::Tensor &acc, const torch::Tensor &X, const Epi &e = Epi()) {
+  if (X.scalar_type() == torch::kFloat && epi_empty(e)) return acc;
   auto Y = torch::empty(acc.sizes(), X.options());
-  check_rc(spira_hip_finalize(acc.data_ptr<float>(), acc.size(0), acc.size(1), dtype_of(X), nullptr, nullptr,
-                              nullptr, 0, Y.data_ptr(), current_stream()),
+  check_rc(spira_hip_finalize(acc.data_ptr<float>(), acc.size(0), acc.size(1), dtype_of(X), e.scale, e.shift,
+                              e.residual, e.relu, Y.data_ptr(), current_stream()),
            "finalize");
   return Y;
 }
@@ -356,7 +391,9 @@ static torch::Tensor finish_acc(const torch::Tensor &acc, const torch::Tensor &X
 // (reference: CUDASparseConvolutionForward_WS_Merged, :186-250)
 torch::Tensor forward_ws_merged(int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
                                 const torch::Tensor &naddrs, const torch::Tensor &qnaddrs, const torch::Tensor &nbmaps,
-                                int64_t mapsize, int64_t qmapsize, bool transpose) {
+                                int64_t mapsize, int64_t qmapsize, bool transpose,
+                                const std::optional<torch::Tensor> &scale, const std::optional<torch::Tensor> &shift,
+                                const std::optional<torch::Tensor> &residual, bool relu) {
   check_features(X, W);
   const int K = static_cast<int>(W.size(0));
   // mirrored pass for submanifold maps with an odd kernel volume
@@ -364,14 +401,16 @@ torch::Tensor forward_ws_merged(int64_t S, int64_t T, const torch::Tensor &X, co
   const int mirror = (S == T && K % 2 == 1) ? K : 0;
   auto acc = torch::zeros({T, W.size(2)}, X.options().dtype(torch::kFloat));
   ws_fused_into(S, T, X, W, naddrs, qnaddrs, nbmaps, mapsize, qmapsize, transpose, 0, mirror, acc.data_ptr<float>());
-  return finish_acc(acc, X);
+  return finish_acc(acc, X, epi_of(scale, shift, residual, relu, T, W.size(2), X));
 }
 
 // (reference: CUDASparseConvolutionForward_HS, :254-342)
 torch::Tensor forward_hs(int64_t S, int64_t T, int64_t gather_tile, int64_t scatter_tile, int64_t parallel,
                          const std::optional<double> &threshold, const torch::Tensor &X, const torch::Tensor &W,
                          const torch::Tensor &source_masks, const torch::Tensor &target_masks,
-                         const torch::Tensor &nbsizes, const std::optional<torch::Tensor> &out_in_map) {
+                         const torch::Tensor &nbsizes, const std::optional<torch::Tensor> &out_in_map,
+                         const std::optional<torch::Tensor> &scale, const std::optional<torch::Tensor> &shift,
+                         const std::optional<torch::Tensor> &residual, bool relu) {
   (void)gather_tile;
   (void)scatter_tile;
   (void)parallel;
@@ -387,7 +426,8 @@ torch::Tensor forward_hs(int64_t S, int64_t T, int64_t gather_tile, int64_t scat
   auto s = current_stream();
   gs_gather(p, X, s);
   gs_gemm(p, W, Kos, s);
-  gs_scatter(p, W.size(2), dtype_of(X), acc.data_ptr<float>(), Y.data_ptr(), s);
+  gs_scatter(p, W.size(2), dtype_of(X), acc.data_ptr<float>(), Y.data_ptr(), s,
+             epi_of(scale, shift, residual, relu, T, W.size(2), X));
   return Y;
 }
 
@@ -395,7 +435,9 @@ torch::Tensor forward_hs(int64_t S, int64_t T, int64_t gather_tile, int64_t scat
 torch::Tensor forward_hs_merged(int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
                                 const torch::Tensor &naddrs, const torch::Tensor &qnaddrs, const torch::Tensor &nbmaps,
                                 const std::optional<torch::Tensor> &out_in_map, int64_t mapsize, int64_t qmapsize,
-                                bool transpose) {
+                                bool transpose, const std::optional<torch::Tensor> &scale,
+                                const std::optional<torch::Tensor> &shift,
+                                const std::optional<torch::Tensor> &residual, bool relu) {
   check_features(X, W);
   const int Kws = static_cast<int>((naddrs.size(0) - 1) * 2);
   const int Kos = out_in_map.has_value() ? static_cast<int>(out_in_map->size(1)) : 1;
@@ -404,7 +446,7 @@ torch::Tensor forward_hs_merged(int64_t S, int64_t T, const torch::Tensor &X, co
   run_os(out_in_map.has_value() ? &*out_in_map : nullptr, S, T, X, W, 0, Kos, acc.data_ptr<float>(),
          SPIRA_OUT_STORE_F32);
   ws_fused_into(S, T, X, W, naddrs, qnaddrs, nbmaps, mapsize, qmapsize, transpose, Kos, Kws, acc.data_ptr<float>());
-  return finish_acc(acc, X);
+  return finish_acc(acc, X, epi_of(scale, shift, residual, relu, T, W.size(2), X));
 }
 
 // ---- selector probes: time one phase of the gather-GEMM-scatter path ----

@@ -47,8 +47,14 @@ class SparseResBlock(nn.Module):
         else:
             self.shortcut = nn.Identity()
         self.relu = spnn.ReLU(True)
+        self._fused = False  # set by spira_amd.nn.fuse_epilogues
 
     def forward(self, x: SparseTensor) -> SparseTensor:
+        if self._fused and self.main[3]._fused_active():
+            # the shortcut's output is the residual of the second conv's epilogue
+            sc = self.shortcut(x)
+            h = self.main[2](self.main[1](self.main[0](x)))
+            return self.main[4](self.main[3](h, residual=sc))
         return self.relu(self.main(x) + self.shortcut(x))
 
 

@@ -136,6 +136,17 @@ class SparseConv(Module):
             "force_os": False,
         }
         self._tuning_data = None
+        # fused epilogue (spira_amd.nn.fusion): an absorbed eval-mode batch
+        # norm (plain attribute, not a submodule) and ReLU
+        object.__setattr__(self, "_epi_bn", None)
+        self._epi_relu = False
+
+    def _fused_active(self) -> bool:
+        """The fused epilogue applies: autograd off and, with a batch norm,
+        the norm in eval mode."""
+        if self._epi_bn is None and not self._epi_relu:
+            return False
+        return not torch.is_grad_enabled() and (self._epi_bn is None or not self._epi_bn.training)
 
     @property
     def tunable_config(self) -> Dict[str, Any]:
@@ -198,8 +209,20 @@ class SparseConv(Module):
         finally:
             self._tuning_data = None
 
-    def forward(self, inputs: SparseTensor) -> SparseTensor:
+    def forward(self, inputs: SparseTensor, residual: Optional[SparseTensor] = None) -> SparseTensor:
+        """residual (fused res blocks only): features added after the batch
+        norm and before the ReLU of the fused epilogue."""
         x = inputs._features
+        epilogue = None
+        if self._fused_active():
+            from .fusion import bn_affine
+            scale, shift = bn_affine(self._epi_bn) if self._epi_bn is not None else (None, None)
+            if self.bias is not None:
+                b = self.bias.float()
+                shift = b * scale + shift if scale is not None else b
+            epilogue = (scale, shift, None if residual is None else residual._features, self._epi_relu)
+        elif residual is not None:
+            raise ValueError("a residual is only taken by a conv with an active fused epilogue")
         if self.is_trivial:
             y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
             coords, stride = inputs._coordinates, inputs._stride
@@ -219,26 +242,39 @@ class SparseConv(Module):
             S, T = (m[1], m[0]) if self.transposed else (m[0], m[1])
             cfg = self._tunable_config
             if d == 0 or force_os:
-                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel)
+                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue)
             elif d == 1:
                 y = F.sparse_convolution_forward_ws_merged(S, T, x, self.kernel, m[5], m[6], m[3], m[7], m[8],
-                                                           self.transposed)
+                                                           self.transposed, epilogue=epilogue)
             elif d == 2:
                 sm, tm = (m[4], m[3]) if self.transposed else (m[3], m[4])
                 if self._tuning_data is not None:
                     self._tuning_data.append((sm, tm, m[5]))
                 y = F.sparse_convolution_forward_ws(S, T, x, self.kernel, sm, tm, m[5], cfg["gather_tile_size"],
-                                                    cfg["scatter_tile_size"], None, cfg["threshold"])
+                                                    cfg["scatter_tile_size"], None, cfg["threshold"],
+                                                    epilogue=epilogue)
             elif d % 2 == 1:
                 dense = None if d == 3 else m[2]
                 y = F.sparse_convolution_forward_hs_merged(S, T, x, self.kernel, m[5], m[6], m[3], dense, m[7],
-                                                           m[8], self.transposed)
+                                                           m[8], self.transposed, epilogue=epilogue)
             else:
                 sm, tm = (m[4], m[3]) if self.transposed else (m[3], m[4])
                 dense = None if d == 4 else m[2]
                 y = F.sparse_convolution_forward_hs(S, T, x, self.kernel, sm, tm, m[5], dense,
                                                     cfg["gather_tile_size"], cfg["scatter_tile_size"], None,
-                                                    cfg["threshold"])
-        if self.bias is not None:
+                                                    cfg["threshold"], epilogue=epilogue)
+        if self.is_trivial and epilogue is not None:
+            scale, shift, res, relu = epilogue
+            y = y.float()
+            if scale is not None:
+                y = y * scale
+            if shift is not None:
+                y = y + shift
+            if res is not None:
+                y = y + res.float()
+            if relu:
+                y = torch.relu(y)
+            y = y.to(x.dtype)
+        elif self.bias is not None and epilogue is None:
             y += self.bias
         return SparseTensor(features=y, coordinates=coords, stride=stride)

@@ -56,47 +56,63 @@ def _gpu(sources: torch.Tensor) -> None:
         raise NotImplementedError("spira_amd runs on the GPU only")
 
 
+def _epi(epilogue) -> tuple:
+    """(scale, shift, residual, relu) folded into the output write:
+    y = conv * scale[c] + shift[c] + residual[t, c], then max(y, 0) if relu.
+    scale / shift are fp32 [C_out], residual is [T, C_out] in the feature
+    dtype; None entries are skipped.  No reference counterpart: the
+    reference applies batch norm, ReLU and the residual add as separate ops
+    (scripts/models/spira/modules/blocks.py:12-84)."""
+    if epilogue is None:
+        return (None, None, None, False)
+    scale, shift, residual, relu = epilogue
+    return (_c(scale), _c(shift), _c(residual), bool(relu))
+
+
 def sparse_convolution_forward_ws(num_sources: int, num_targets: int, sources, weights, source_masks,
                                   target_masks, kernel_map_sizes, gather_tile_size: int, scatter_tile_size: int,
-                                  parallel: Optional[int] = None, threshold: Optional[float] = 0):
+                                  parallel: Optional[int] = None, threshold: Optional[float] = 0, *, epilogue=None):
     _gpu(sources)
     if parallel is None:
         parallel = GEMM_PARALLEL_LEVEL
     return _C.cuda_sparse_convolution_forward_ws(num_sources, num_targets, gather_tile_size, scatter_tile_size,
                                                  parallel, threshold, _c(sources), _c(weights), _c(source_masks),
-                                                 _c(target_masks), _c(kernel_map_sizes))
+                                                 _c(target_masks), _c(kernel_map_sizes), *_epi(epilogue))
 
 
 def sparse_convolution_forward_ws_merged(num_sources: int, num_targets: int, sources, weights, naddrs, qnaddrs,
-                                         nbmaps, mapsize: int, qmapsize: int, transpose: Optional[bool] = False):
+                                         nbmaps, mapsize: int, qmapsize: int, transpose: Optional[bool] = False, *,
+                                         epilogue=None):
     _gpu(sources)
     return _C.cuda_sparse_convolution_forward_ws_merged(num_sources, num_targets, _c(sources), _c(weights),
                                                         _c(naddrs), _c(qnaddrs), _c(nbmaps), mapsize, qmapsize,
-                                                        bool(transpose))
+                                                        bool(transpose), *_epi(epilogue))
 
 
 def sparse_convolution_forward_hs(num_sources: int, num_targets: int, sources, weights, source_masks,
                                   target_masks, kernel_map_sizes, out_in_map, gather_tile_size: int,
                                   scatter_tile_size: int, parallel: Optional[int] = None,
-                                  threshold: Optional[float] = 0):
+                                  threshold: Optional[float] = 0, *, epilogue=None):
     _gpu(sources)
     if parallel is None:
         parallel = GEMM_PARALLEL_LEVEL
     return _C.cuda_sparse_convolution_forward_hs(num_sources, num_targets, gather_tile_size, scatter_tile_size,
                                                  parallel, threshold, _c(sources), _c(weights), _c(source_masks),
-                                                 _c(target_masks), _c(kernel_map_sizes), _c(out_in_map))
+                                                 _c(target_masks), _c(kernel_map_sizes), _c(out_in_map),
+                                                 *_epi(epilogue))
 
 
 def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sources, weights, naddrs, qnaddrs,
                                          nbmaps, out_in_map, mapsize: int, qmapsize: int,
-                                         transpose: Optional[bool] = False):
+                                         transpose: Optional[bool] = False, *, epilogue=None):
     _gpu(sources)
     return _C.cuda_sparse_convolution_forward_hs_merged(num_sources, num_targets, _c(sources), _c(weights),
                                                         _c(naddrs), _c(qnaddrs), _c(nbmaps), _c(out_in_map),
-                                                        mapsize, qmapsize, bool(transpose))
+                                                        mapsize, qmapsize, bool(transpose), *_epi(epilogue))
 
 
-def sparse_convolution_forward_os(num_sources: int, num_targets: int, out_in_map, sources, weights):
+def sparse_convolution_forward_os(num_sources: int, num_targets: int, out_in_map, sources, weights, *,
+                                  epilogue=None):
     _gpu(sources)
     return _C.cuda_sparse_convolution_forward_os(num_sources, num_targets, _c(out_in_map), _c(sources),
-                                                 _c(weights))
+                                                 _c(weights), *_epi(epilogue))
