@@ -6,22 +6,26 @@
 // iz = 1..kz-1: idx += (src[idx] <= c); c += sz; entry(iz) = idx if
 // src[idx] == c.  Indices at or past the end of src give -1.
 //
-// MI355X design: one wave64 owns a tile of 64 consecutive (sorted) targets.
-//  1. For every dx-group of offsets the wave reduces the min / max query key
-//     (all queries of the group lie between them, so their lower bounds lie
-//     between the lower bounds of min and max, whatever modular wrap occurs).
-//  2. All 2*G bounds are found together by a wave-cooperative 64-ary search:
-//     each step every lane probes one evenly spaced key per bound and a
-//     ballot picks the sub-range, so a bound costs ~log64(S) dependent L2
-//     round trips instead of log2(S).
-//  3. The source window [lb(min), lb(max)+kz) is staged in LDS with
-//     coalesced loads; each lane then runs its lower-bound search and z-scan
-//     out of LDS.  Windows larger than the LDS cap fall back to a per-lane
-//     search in global memory restricted to the window (same results).
+// MI355X design: a block owns a tile of 64 consecutive (sorted) targets and
+// runs one wave64 per dx-group of offsets (kx waves), so that every tile's
+// searches proceed in parallel and a CU holds enough waves to overlap the
+// dependent L2/HBM round trips of the searches.  Per wave:
+//  1. the wave reduces the min / max query key of its group (all queries of
+//     the group lie between them, so their lower bounds lie between the lower
+//     bounds of min and max, whatever modular wrap occurs);
+//  2. both bounds are found by a wave-cooperative 64-ary search: each step
+//     every lane probes one evenly spaced key per bound and a ballot picks
+//     the sub-range, so a bound costs ~log64(S) dependent round trips instead
+//     of log2(S);
+//  3. the source window [lb(min), lb(max)+kz) is staged in the wave's LDS
+//     slot with coalesced loads; each lane then runs its lower-bound search
+//     and z-scan out of LDS.  Windows larger than the slot fall back to a
+//     per-lane search in global memory restricted to the window (same
+//     results);
 //  4. [K, Tp] layouts store rows with coalesced 256-byte wave stores and emit
 //     per-(row, tile) valid counts for compaction (ballot + popcount);
-//     [Tp, K] layouts stage the tile's 64 x K block in LDS and write it out
-//     contiguously.
+//     [Tp, K] layouts stage the tile's 64 x K block in LDS and the block
+//     writes it out contiguously.
 #include "common.hpp"
 #include "../../../include/spira_hip.h"
 
@@ -33,7 +37,7 @@ namespace spira_hip {
 
 constexpr int kGroupMax = 8;      // dx groups (kx <= 8)
 constexpr int kOffsetsMax = 128;  // offsets per map (K <= 128 for the no-z layout)
-constexpr int kWindowCap = 1024;  // LDS window entries per wave
+constexpr int kWindowCap = 512;   // LDS window entries per wave
 
 template <typename CT> struct SearchParams {
   const CT *src;
@@ -52,55 +56,17 @@ template <typename CT> struct SearchParams {
 
 template <typename CT> __device__ __forceinline__ CT max_key() { return static_cast<CT>(~static_cast<CT>(0)); }
 
-// Wave-cooperative lower bounds of up to 2*kGroupMax values (wave-uniform).
+// Range of lower_bound(src, v) from 64 wave-uniform samples: lane i holds
+// src[base + i * step] (positions < end) or max_key past the end.  On return
+// lb(v) lies in [blo, bhi].
 template <typename CT>
-__device__ __forceinline__ void wave_lower_bounds(const CT *__restrict__ src, int64_t S, const CT *vals, int ns,
-                                                  int64_t *out) {
-  const int lane = lane_id();
-  int64_t lo[2 * kGroupMax], hi[2 * kGroupMax];
-#pragma unroll
-  for (int s = 0; s < 2 * kGroupMax; ++s) {
-    lo[s] = 0;
-    hi[s] = S;
-  }
-  while (true) {
-    bool more = false;
-#pragma unroll
-    for (int s = 0; s < 2 * kGroupMax; ++s)
-      if (s < ns && hi[s] - lo[s] > 64) more = true;
-    if (!more) break;
-    CT sample[2 * kGroupMax];
-    int64_t step[2 * kGroupMax];
-#pragma unroll
-    for (int s = 0; s < 2 * kGroupMax; ++s) {
-      step[s] = (hi[s] - lo[s] + 63) >> 6;
-      int64_t p = lo[s] + lane * step[s];
-      sample[s] = (s < ns && hi[s] - lo[s] > 64 && p < hi[s]) ? src[p] : max_key<CT>();
-    }
-#pragma unroll
-    for (int s = 0; s < 2 * kGroupMax; ++s) {
-      if (s < ns && hi[s] - lo[s] > 64) {
-        int64_t p = lo[s] + lane * step[s];
-        bool ge = (p >= hi[s]) || (sample[s] >= vals[s]);
-        uint64_t m = ballot(ge);
-        int f = m ? __builtin_ctzll(m) : 64;
-        int64_t nlo = f == 0 ? lo[s] : lo[s] + (f - 1) * step[s] + 1;
-        int64_t nhi = f == 64 ? hi[s] : lo[s] + f * step[s];
-        if (nhi > hi[s]) nhi = hi[s];
-        lo[s] = nlo;
-        hi[s] = nhi;
-      }
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < 2 * kGroupMax; ++s) {
-    if (s < ns) {
-      int64_t p = lo[s] + lane;
-      bool ge = (p >= hi[s]) || (src[p] >= vals[s]);
-      uint64_t m = ballot(ge);
-      out[s] = m ? lo[s] + __builtin_ctzll(m) : hi[s];
-    }
-  }
+__device__ __forceinline__ void sample_bucket(CT sample, CT v, int64_t base, int64_t step, int64_t end,
+                                              int64_t &blo, int64_t &bhi) {
+  const uint64_t m = ballot(sample >= v);
+  const int j = m ? __builtin_ctzll(m) : 64;
+  blo = j == 0 ? base : base + (j - 1) * step + 1;
+  const int64_t p = base + j * step;
+  bhi = p < end ? p : end;
 }
 
 template <typename CT>
@@ -129,24 +95,29 @@ __device__ __forceinline__ int64_t global_lower_bound(const CT *__restrict__ src
 }
 
 template <typename CT, int KZ>
-__global__ __launch_bounds__(64) void kmap_search_kernel(const SearchParams<CT> p) {
+__global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const SearchParams<CT> p) {
   extern __shared__ __align__(16) char smem[];
-  CT *win = reinterpret_cast<CT *>(smem);
-  int32_t *stage = reinterpret_cast<int32_t *>(smem + kWindowCap * sizeof(CT));
+  const int g = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // dx-group of this wave
+  CT *win = reinterpret_cast<CT *>(smem) + g * kWindowCap;
+  int32_t *stage = reinterpret_cast<int32_t *>(smem + p.G * kWindowCap * sizeof(CT));
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int64_t tile = blockIdx.x;
   const int64_t t = tile * 64 + lane;
   const bool valid = t < p.T;
+  // level-1 samples of the sources (independent of the queries, so this load
+  // overlaps the target-key load): lane i holds src[i * s1]
+  const int64_t s1 = (p.S + 63) / 64;
+  const CT l1 = lane * s1 < p.S ? p.src[lane * s1] : max_key<CT>();
   const CT key = valid ? p.tgt[t] : CT(0);
   const CT sz = p.sz;
 
   if (ballot(valid) == 0) {
     // fully padded tile: every entry is -1
     if (p.os_layout) {
-      for (int i = lane; i < 64 * p.K; i += 64) p.map[tile * 64 * p.K + i] = -1;
+      for (int i = threadIdx.x; i < 64 * p.K; i += blockDim.x) p.map[tile * 64 * p.K + i] = -1;
     } else {
-      for (int r = 0; r < p.K; ++r) {
+      for (int r = g; r < p.K; r += p.G) {
         p.map[r * p.Tp + t] = -1;
         if (p.tile_counts && lane == 0) p.tile_counts[r * p.ntiles + tile] = 0;
       }
@@ -154,73 +125,89 @@ __global__ __launch_bounds__(64) void kmap_search_kernel(const SearchParams<CT> 
     return;
   }
 
-  // 1. query bounds per dx-group
-  CT vals[2 * kGroupMax];
-#pragma unroll
-  for (int g = 0; g < kGroupMax; ++g) {
-    if (g < p.G) {
-      CT mn = max_key<CT>(), mx = CT(0);
-      for (int j = 0; j < p.GS; ++j) {
-        CT q = key + p.off[g * p.GS + j];
-        if (valid) {
-          mn = q < mn ? q : mn;
-          mx = q > mx ? q : mx;
-        }
-      }
-      vals[2 * g] = wave_min(mn);
-      vals[2 * g + 1] = wave_max(mx);
-    }
-  }
-  // 2. all bounds at once
-  int64_t lb[2 * kGroupMax];
-  wave_lower_bounds<CT>(p.src, p.S, vals, 2 * p.G, lb);
-
-  // 3. per group: stage the window, search, z-scan, store
-  for (int g = 0; g < p.G; ++g) {
-    const int64_t lo = lb[2 * g];
-    int64_t hi = lb[2 * g + 1] + KZ;
-    if (hi > p.S) hi = p.S;
-    const int n = static_cast<int>(hi - lo);
-    const bool in_lds = (hi - lo) <= kWindowCap;
-    if (in_lds) {
-      for (int i = lane; i < n; i += 64) win[i] = p.src[lo + i];
-      __syncthreads();
-    }
+  // 1. query bounds of this wave's group
+  CT vals[2];
+  {
+    CT mn = max_key<CT>(), mx = CT(0);
     for (int j = 0; j < p.GS; ++j) {
-      const int o = g * p.GS + j;
-      // padded lanes query the group minimum so that every index stays inside the window
-      CT c = valid ? CT(key + p.off[o]) : vals[2 * g];
-      int64_t idx = in_lds ? lo + lds_lower_bound(win, n, c) : global_lower_bound(p.src, lo, hi, c);
-      int32_t res[KZ];
-      {
-        CT v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
-        res[0] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
-#pragma unroll
-        for (int iz = 1; iz < KZ; ++iz) {
-          if (idx < p.S && v <= c) ++idx;
-          c += sz;
-          v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
-          res[iz] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
-        }
+      CT q = key + p.off[g * p.GS + j];
+      if (valid) {
+        mn = q < mn ? q : mn;
+        mx = q > mx ? q : mx;
       }
+    }
+    vals[0] = wave_min(mn);
+    vals[1] = wave_max(mx);
+  }
+  // 2. lower-bound ranges of both: level 1 from the samples above, level 2
+  //    from 64 samples inside each level-1 bucket (one dependent round trip)
+  int64_t lb[2];
+  {
+    int64_t blo[2], bhi[2];
+    sample_bucket(l1, vals[0], 0, s1, p.S, blo[0], bhi[0]);
+    sample_bucket(l1, vals[1], 0, s1, p.S, blo[1], bhi[1]);
+    CT l2[2];
+    int64_t s2[2];
 #pragma unroll
-      for (int iz = 0; iz < KZ; ++iz) {
-        const int32_t r = valid ? res[iz] : -1;
-        const int k = o * KZ + iz;
-        if (p.os_layout) {
-          const int col = p.zmajor ? iz * p.O + o : k;
-          stage[lane * p.K + col] = r;
-        } else {
-          const int row = p.use_perm ? p.perm[k] : k;
-          p.map[row * p.Tp + t] = r;
-          if (p.tile_counts) {
-            uint64_t m = ballot(r >= 0);
-            if (lane == 0) p.tile_counts[row * p.ntiles + tile] = __builtin_popcountll(m);
-          }
+    for (int b = 0; b < 2; ++b) {
+      s2[b] = (bhi[b] - blo[b] + 63) / 64;
+      if (s2[b] < 1) s2[b] = 1;
+      const int64_t q = blo[b] + lane * s2[b];
+      l2[b] = q < bhi[b] ? p.src[q] : max_key<CT>();
+    }
+    int64_t lo2, hi2;
+    sample_bucket(l2[0], vals[0], blo[0], s2[0], bhi[0], lo2, hi2);
+    lb[0] = lo2;
+    sample_bucket(l2[1], vals[1], blo[1], s2[1], bhi[1], lo2, hi2);
+    lb[1] = hi2;  // upper end of lb(max)'s range
+  }
+
+  // 3. stage the window, search, z-scan, store
+  const int64_t lo = lb[0];
+  int64_t hi = lb[1] + KZ;
+  if (hi > p.S) hi = p.S;
+  const int n = static_cast<int>(hi - lo);
+  const bool in_lds = (hi - lo) <= kWindowCap;
+  if (in_lds) {
+    for (int i = lane; i < n; i += 64) win[i] = p.src[lo + i];
+    // the window is private to this wave: LDS keeps a wave's accesses in order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  for (int j = 0; j < p.GS; ++j) {
+    const int o = g * p.GS + j;
+    // padded lanes query the group minimum so that every index stays inside the window
+    CT c = valid ? CT(key + p.off[o]) : vals[0];
+    int64_t idx = in_lds ? lo + lds_lower_bound(win, n, c) : global_lower_bound(p.src, lo, hi, c);
+    int32_t res[KZ];
+    {
+      CT v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
+      res[0] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
+#pragma unroll
+      for (int iz = 1; iz < KZ; ++iz) {
+        if (idx < p.S && v <= c) ++idx;
+        c += sz;
+        v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
+        res[iz] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
+      }
+    }
+#pragma unroll
+    for (int iz = 0; iz < KZ; ++iz) {
+      const int32_t r = valid ? res[iz] : -1;
+      const int k = o * KZ + iz;
+      if (p.os_layout) {
+        const int col = p.zmajor ? iz * p.O + o : k;
+        stage[lane * p.K + col] = r;
+      } else {
+        const int row = p.use_perm ? p.perm[k] : k;
+        p.map[row * p.Tp + t] = r;
+        if (p.tile_counts) {
+          uint64_t m = ballot(r >= 0);
+          if (lane == 0) p.tile_counts[row * p.ntiles + tile] = __builtin_popcountll(m);
         }
       }
     }
-    if (in_lds) __syncthreads();
   }
 
   if (p.os_layout) {
@@ -229,7 +216,7 @@ __global__ __launch_bounds__(64) void kmap_search_kernel(const SearchParams<CT> 
     const int total = 64 * p.K;  // multiple of 4
     const int4 *s4 = reinterpret_cast<const int4 *>(stage);
     int4 *d4 = reinterpret_cast<int4 *>(dst);
-    for (int i = lane; i < total / 4; i += 64) d4[i] = s4[i];
+    for (int i = threadIdx.x; i < total / 4; i += blockDim.x) d4[i] = s4[i];
   }
 }
 
@@ -303,8 +290,8 @@ static int search_impl(const CT *src, int64_t S, const CT *tgt, int64_t T, int k
   }
   p.tile_counts = p.os_layout ? nullptr : tile_counts;
   if (p.Tp == 0) return kOk;
-  const size_t lds = kWindowCap * sizeof(CT) + (p.os_layout ? 64 * K * sizeof(int32_t) : 0);
-  dim3 grid(static_cast<unsigned>(p.ntiles)), block(64);
+  const size_t lds = p.G * kWindowCap * sizeof(CT) + (p.os_layout ? 64 * K * sizeof(int32_t) : 0);
+  dim3 grid(static_cast<unsigned>(p.ntiles)), block(64 * p.G);
   switch (KZ) {
     case 1: hipLaunchKernelGGL((kmap_search_kernel<CT, 1>), grid, block, lds, stream, p); break;
     case 2: hipLaunchKernelGGL((kmap_search_kernel<CT, 2>), grid, block, lds, stream, p); break;
