@@ -163,7 +163,9 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
                                 size_t *bytes);
 
 /* Output-stationary implicit GEMM: targets[t] = sum_j sources[map[t, j]] @
- * weights[j] for map entries >= 0; map is [>= num_targets, num_offsets],
+ * weights[j] for map entries >= 0; map is [>= num_targets, num_offsets]
+ * (null: the identity map, with one offset and num_sources == num_targets,
+ * i.e. a dense GEMM such as a 1x1x1 layer),
  * weights [num_offsets, c_in, c_out]; fp32 accumulation.  fp16 needs
  * `prepared` (spira_hip_prepare_weights); fp32 reads `weights`.  With
  * out_mode SPIRA_OUT_STORE an optional epilogue is applied per element:

@@ -441,9 +441,12 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   // Map entries of step u: lane L of a wave fetches row L (MT = 2) or row
   // L % 32 (MT = 1) of the wave's rows into the stage's index slot; rows past
   // T read nothing (out of range) and are masked when resolved.
+  // No map: the identity (logical row i reads source i); the fetches then
+  // load nothing (out of range) but keep the vmcnt arithmetic.
+  const bool ident = map == nullptr;
   const int frow = MT == 2 ? lane : r;
   const int64_t flr = row0 + wave * 32 * MT + frow;
-  const uint32_t fbase = flr < T ? static_cast<uint32_t>(flr * Kc + j0) * 4u : kOutOfRange;
+  const uint32_t fbase = (flr < T && !ident) ? static_cast<uint32_t>(flr * Kc + j0) * 4u : kOutOfRange;
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(map, static_cast<uint32_t>(T * Kc * 4));
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + r) * 4;
@@ -467,6 +470,7 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       ring::pin(idx[m]);
+      if (ident) idx[m] = static_cast<int32_t>(row0 + wave * 32 * MT + m * 32 + r);
       if (!mvalid[m]) idx[m] = -1;
     }
     wrow = j0 + pit.j;
@@ -677,7 +681,7 @@ __global__ __launch_bounds__(256) void os_generic_kernel(const int32_t *__restri
   // error at O((Cin + K) eps) instead of O(Cin K eps)
   float acc = 0.f;
   for (int j = 0; j < Kc; ++j) {
-    const int32_t s = map[t * Kc + j];
+    const int32_t s = map ? map[t * Kc + j] : static_cast<int32_t>(t);  // no map: identity
     if (s < 0) continue;
     const FT *x = X + static_cast<int64_t>(s) * Cin;
     const FT *w = W + (static_cast<int64_t>(j) * Cin) * Cout + c;
@@ -996,6 +1000,8 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
   SPIRA_HIP_REQUIRE(out_mode == SPIRA_OUT_STORE || (!scale && !shift && !residual && !relu),
                     "conv_os: the epilogue applies to the storage-dtype output only");
   SPIRA_HIP_REQUIRE(group_masks == nullptr || num_offsets <= 128, "conv_os: group masks need <= 128 offsets");
+  SPIRA_HIP_REQUIRE(out_in_map != nullptr || (num_offsets == 1 && num_sources == num_targets && !row_order),
+                    "conv_os: without a map (identity) there must be one offset and as many sources as targets");
   if (num_targets <= 0) return kOk;
   const Epilogue epi = make_epi(scale, shift, residual, relu);
   if (mfma_path(dtype)) {
@@ -1008,6 +1014,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     const int splits = static_cast<int>(div_up(num_offsets, jper));
     dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(by), static_cast<unsigned>(splits));
     SPIRA_HIP_REQUIRE(num_targets * num_offsets * 4 < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
+    // (out_in_map may be null: the identity map, handled in the kernel)
     Operands op;
     int rc0 = make_operands(op, sources, num_sources, c_in, prepared, num_offsets, c_out);
     if (rc0) return rc0;

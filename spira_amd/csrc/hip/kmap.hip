@@ -417,61 +417,77 @@ __global__ void convert_transposed_kernel(const int32_t *__restrict__ map, int64
 // them), so that sorting groups rows with identical neighbour patterns.
 // Sort key of a map row: rows with more neighbours first (their blocks run
 // longest, so they are dispatched first), then rows with the same neighbour
-// pattern together.  With K <= 58 the key is exact: (K - popcount) in bits
-// 58..63 above the K-bit pattern; wider maps keep the first 57 offsets of the
-// pattern under a 7-bit (127 - popcount) field.
-__global__ void row_mask_kernel(const int32_t *__restrict__ map, int64_t T, int K, uint64_t *__restrict__ keys,
-                                int32_t *__restrict__ iota) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  const int32_t *row = map + t * K;
+// pattern together.  Key = (K - popcount) << P | pattern, where the pattern
+// keeps the first P = min(K, 57) columns; row_key_bits(K) bits in all.
+__host__ __device__ __forceinline__ int row_pattern_bits(int K) { return K < 57 ? K : 57; }
+__host__ __device__ __forceinline__ int row_key_bits(int K) {
+  int c = 1;  // bits of the largest count field value K
+  while ((1 << c) <= K) ++c;
+  return row_pattern_bits(K) + c;
+}
+// One block stages RB consecutive map rows in LDS with coalesced loads (RB =
+// 256 rows for K <= 32, else 64), then thread t < RB builds row t's key.
+__global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict__ map, int64_t T, int K, int RB,
+                                                       uint64_t *__restrict__ keys, int32_t *__restrict__ iota) {
+  extern __shared__ int32_t rows_lds[];
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RB;
+  const int64_t nr = (T - row0) < RB ? (T - row0) : RB;
+  for (int64_t e = threadIdx.x; e < nr * K; e += 256) rows_lds[e] = map[row0 * K + e];
+  __syncthreads();
+  if (threadIdx.x >= nr) return;
+  const int32_t *row = rows_lds + threadIdx.x * K;
+  const int P = row_pattern_bits(K);
   uint64_t m = 0;
   int cnt = 0;
   for (int j = 0; j < K; ++j) {
     const bool v = row[j] >= 0;
     cnt += v;
-    if (v && j < 58) m |= uint64_t(1) << j;
+    if (v && j < P) m |= uint64_t(1) << j;
   }
-  keys[t] = K <= 58 ? (static_cast<uint64_t>(K - cnt) << 58) | m
-                    : (static_cast<uint64_t>(127 - (cnt < 127 ? cnt : 127)) << 57) | (m & ((uint64_t(1) << 57) - 1));
-  iota[t] = static_cast<int32_t>(t);
+  keys[row0 + threadIdx.x] = (static_cast<uint64_t>(K - cnt) << P) | m;
+  iota[row0 + threadIdx.x] = static_cast<int32_t>(row0 + threadIdx.x);
 }
 
-// 128-bit union of the valid columns of each group of 128 consecutive rows of
-// `map` (rows in the order of `order` when given): one wave per group.
-__global__ void group_mask_kernel(const int32_t *__restrict__ map, const int32_t *__restrict__ order, int64_t T,
-                                  int K, int64_t groups, uint64_t *__restrict__ out) {
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (g >= groups) return;
-  const int lane = threadIdx.x & 63;
-  uint64_t lo = 0, hi = 0;
-  for (int h = 0; h < 2; ++h) {
-    const int64_t i = g * 128 + h * 64 + lane;
-    if (i >= T) continue;
-    const int32_t *row = map + (order ? static_cast<int64_t>(order[i]) : i) * K;
-    for (int j = 0; j < K && j < 128; ++j)
-      if (row[j] >= 0) {
-        if (j < 64) lo |= uint64_t(1) << j;
-        else hi |= uint64_t(1) << (j - 64);
-      }
+// ordered[i, :] = map[order[i], :] and, per group of 128 ordered rows, the
+// 128-bit union of their valid columns (when gmask is given, K <= 128).  A
+// block covers 2 groups: its threads walk the 256 x K ordered elements
+// linearly (coalesced stores, row-contiguous loads) and OR-reduce the
+// column bits through LDS.
+__global__ __launch_bounds__(256) void order_rows_kernel(const int32_t *__restrict__ map,
+                                                         const int32_t *__restrict__ order, int64_t T, int K,
+                                                         int32_t *__restrict__ ordered, uint64_t *__restrict__ gmask) {
+  __shared__ uint64_t red[2][2][4];  // [group][word][wave]
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 256;
+  const int64_t rows = (T - row0) < 256 ? (T - row0) : 256;
+  const int64_t n = rows * K;
+  uint64_t m[2][2] = {{0, 0}, {0, 0}};
+  for (int64_t e = threadIdx.x; e < n; e += 256) {
+    const int64_t r = e / K;
+    const int c = static_cast<int>(e - r * K);
+    const int32_t v = map[static_cast<int64_t>(order[row0 + r]) * K + c];
+    if (ordered) ordered[row0 * K + e] = v;
+    if (v >= 0 && c < 128) {
+      const int gi = r >= 128 ? 1 : 0;
+      if (c < 64) m[gi][0] |= uint64_t(1) << c;
+      else m[gi][1] |= uint64_t(1) << (c - 64);
+    }
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    lo |= static_cast<uint64_t>(__shfl_xor(lo, o, 64));
-    hi |= static_cast<uint64_t>(__shfl_xor(hi, o, 64));
+  if (!gmask) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      uint64_t v = m[gi][w];
+      for (int o = 32; o > 0; o >>= 1) v |= static_cast<uint64_t>(__shfl_xor(v, o, 64));
+      if (lane == 0) red[gi][w][wave] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < 4) {
+    const int gi = threadIdx.x >> 1, w = threadIdx.x & 1;
+    const int64_t g = row0 / 128 + gi;
+    if (g * 128 < T) gmask[g * 2 + w] = red[gi][w][0] | red[gi][w][1] | red[gi][w][2] | red[gi][w][3];
   }
-  if (lane == 0) {
-    out[g * 2] = lo;
-    out[g * 2 + 1] = hi;
-  }
-}
-
-// ordered[i, :] = map[order[i], :]
-__global__ void gather_rows_kernel(const int32_t *__restrict__ map, const int32_t *__restrict__ order, int64_t T,
-                                   int K, int32_t *__restrict__ ordered) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= T * K) return;
-  const int64_t row = i / K;
-  ordered[i] = map[static_cast<int64_t>(order[row]) * K + (i - row * K)];
 }
 
 static size_t row_order_parts(int64_t T, size_t *sort_bytes) {
@@ -612,21 +628,17 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
   p += a(num_targets * sizeof(uint64_t));
   int32_t *iota = reinterpret_cast<int32_t *>(p);
   p += a(num_targets * sizeof(int32_t));
-  hipLaunchKernelGGL(row_mask_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, num_targets,
-                     num_offsets, keys, iota);
+  const int rb = num_offsets <= 32 ? 256 : 64;
+  SPIRA_HIP_REQUIRE(static_cast<size_t>(rb) * num_offsets * sizeof(int32_t) <= 64 * 1024,
+                    "kmap_row_order: at most 256 offsets");
+  hipLaunchKernelGGL(row_mask_kernel, dim3(div_up(num_targets, rb)), dim3(256), rb * num_offsets * sizeof(int32_t),
+                     stream, out_in_map, num_targets, num_offsets, rb, keys, iota);
   SPIRA_HIP_LAUNCH_CHECK();
-  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, sb, keys, keys_out, iota, order, static_cast<size_t>(num_targets), 0, 64,
-                                          stream));
-  if (ordered_map) {
-    const int64_t n = num_targets * num_offsets;
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(div_up(n, 256)), dim3(256), 0, stream, out_in_map, order,
-                       num_targets, num_offsets, ordered_map);
-    SPIRA_HIP_LAUNCH_CHECK();
-  }
-  if (group_masks) {
-    const int64_t groups = div_up(num_targets, 128);
-    hipLaunchKernelGGL(group_mask_kernel, dim3(div_up(groups, 4)), dim3(256), 0, stream, out_in_map, order,
-                       num_targets, num_offsets, groups, group_masks);
+  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, sb, keys, keys_out, iota, order, static_cast<size_t>(num_targets), 0,
+                                          row_key_bits(num_offsets), stream));
+  if (ordered_map || group_masks) {
+    hipLaunchKernelGGL(order_rows_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, order,
+                       num_targets, num_offsets, ordered_map, group_masks);
     SPIRA_HIP_LAUNCH_CHECK();
   }
   return kOk;

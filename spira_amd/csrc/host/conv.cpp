@@ -188,7 +188,6 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
                    int w0, int K, void *out, int mode, const Epi &epi = Epi()) {
   const auto dev = X.device();
   const int dtype = dtype_of(X);
-  torch::Tensor ident;
   const int32_t *mp = nullptr;
   if (map) {
     SPIRA_CHECK_ARG(map->dim() == 2 && map->scalar_type() == torch::kInt32, "out_in_map must be 2-D int32");
@@ -197,9 +196,8 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
     SPIRA_CHECK_ARG(map->size(1) == K, "out_in_map has ", map->size(1), " columns, expected ", K);
     mp = map->data_ptr<int32_t>();
   } else {
-    SPIRA_CHECK_ARG(S == T, "the identity dense part needs as many sources as targets");
-    ident = torch::arange(T, torch::TensorOptions(dev).dtype(torch::kInt32)).view({T, 1});
-    mp = ident.data_ptr<int32_t>();
+    // no map: the identity map (targets[t] reads sources[t], one offset)
+    SPIRA_CHECK_ARG(S == T && K == 1, "the identity map needs as many sources as targets and one offset");
   }
   auto P = prepared_weights(W);
   size_t wsb = 0;
@@ -207,7 +205,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto ws = workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0) {
+  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && K <= 128) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
@@ -231,6 +229,20 @@ torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, 
   auto Y = torch::empty({T, W.size(2)}, X.options());
   run_os(&out_in_map, S, T, X, W, 0, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE,
          epi_of(scale, shift, residual, relu, T, W.size(2), X));
+  return Y;
+}
+
+// 1x1x1 / stride-1 layers: targets = sources @ W[0] with the fused epilogue,
+// on the output-stationary kernel with the identity map (reference:
+// the torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313).
+torch::Tensor forward_dense(const torch::Tensor &X, const torch::Tensor &W, const std::optional<torch::Tensor> &scale,
+                            const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
+                            bool relu) {
+  check_features(X, W);
+  SPIRA_CHECK_ARG(W.size(0) == 1, "a dense layer has one weight offset, got ", W.size(0));
+  const int64_t T = X.size(0);
+  auto Y = torch::empty({T, W.size(2)}, X.options());
+  run_os(nullptr, T, T, X, W, 0, 1, Y.data_ptr(), SPIRA_OUT_STORE, epi_of(scale, shift, residual, relu, T, W.size(2), X));
   return Y;
 }
 
@@ -508,6 +520,7 @@ void reset_error() { (void)hipGetLastError(); }
 
 void register_conv(pybind11::module_ &m) {
   m.def("cuda_sparse_convolution_forward_os", &forward_os);
+  m.def("cuda_dense_forward", &forward_dense);
   m.def("cuda_sparse_convolution_forward_ws", &forward_ws);
   m.def("cuda_sparse_convolution_forward_ws_merged", &forward_ws_merged);
   m.def("cuda_sparse_convolution_forward_hs", &forward_hs);

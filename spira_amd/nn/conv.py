@@ -214,6 +214,7 @@ class SparseConv(Module):
         norm and before the ReLU of the fused epilogue."""
         x = inputs._features
         epilogue = None
+        epilogue_done = False
         if self._fused_active():
             from .fusion import bn_affine
             scale, shift = bn_affine(self._epi_bn) if self._epi_bn is not None else (None, None)
@@ -224,7 +225,11 @@ class SparseConv(Module):
         elif residual is not None:
             raise ValueError("a residual is only taken by a conv with an active fused epilogue")
         if self.is_trivial:
-            y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
+            if x.is_cuda:
+                y = F.dense_forward(x, self.kernel, epilogue=epilogue)
+                epilogue_done = True
+            else:
+                y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
             coords, stride = inputs._coordinates, inputs._stride
         else:
             if self._kernel_map_cache is None:
@@ -263,7 +268,7 @@ class SparseConv(Module):
                 y = F.sparse_convolution_forward_hs(S, T, x, self.kernel, sm, tm, m[5], dense,
                                                     cfg["gather_tile_size"], cfg["scatter_tile_size"], None,
                                                     cfg["threshold"], epilogue=epilogue)
-        if self.is_trivial and epilogue is not None:
+        if self.is_trivial and epilogue is not None and not epilogue_done:
             scale, shift, res, relu = epilogue
             y = y.float()
             if scale is not None:

@@ -16,7 +16,7 @@ __all__ = [
     "cuda_time_gather", "cuda_time_scatter", "sparse_convolution_forward_ws",
     "sparse_convolution_forward_ws_merged", "sparse_convolution_forward_os",
     "sparse_convolution_forward_hs", "sparse_convolution_forward_hs_merged", "cuda_time_gemm",
-    "set_gemm_parallel_level",
+    "set_gemm_parallel_level", "dense_forward",
 ]
 
 GEMM_PARALLEL_LEVEL = 4
@@ -109,6 +109,14 @@ def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sou
     return _C.cuda_sparse_convolution_forward_hs_merged(num_sources, num_targets, _c(sources), _c(weights),
                                                         _c(naddrs), _c(qnaddrs), _c(nbmaps), _c(out_in_map),
                                                         mapsize, qmapsize, bool(transpose), *_epi(epilogue))
+
+
+def dense_forward(sources, weights, *, epilogue=None):
+    """sources @ weights[0] (a 1x1x1, stride-1 layer) with the fused epilogue,
+    on the output-stationary kernel with the identity map (reference: the
+    torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313)."""
+    _gpu(sources)
+    return _C.cuda_dense_forward(_c(sources), _c(weights), *_epi(epilogue))
 
 
 def sparse_convolution_forward_os(num_sources: int, num_targets: int, out_in_map, sources, weights, *,

@@ -143,3 +143,18 @@ def test_fused_path_off_with_autograd_or_training(dev):
     model.eval()
     with torch.enable_grad():
         assert not conv._fused_active()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("cin,cout", [(128, 96), (3, 32), (24, 40), (256, 256)])
+def test_dense_forward(dev, dtype, cin, cout):
+    """1x1x1 layers on the identity-map kernel: sources @ W[0] with the epilogue."""
+    T = 3000
+    X, W, scale, shift, res = _case(T, T, cin, cout, dtype, dev, seed=7)
+    W = W[:1]
+    ident = np.arange(T, dtype=np.int32).reshape(T, 1)
+    ref_conv = orc.conv_os(ident, T, X.double().numpy(), W.double().numpy())
+    y = F.dense_forward(X.to(dev), W.to(dev))
+    assert rel_err(np_(y.float()), ref_conv) <= TOL[dtype]
+    y = F.dense_forward(X.to(dev), W.to(dev), epilogue=(scale.to(dev), shift.to(dev), res.to(dev), True))
+    assert rel_err(np_(y.float()), _ref(ref_conv, scale, shift, res, True)) <= TOL[dtype]
