@@ -108,7 +108,11 @@ def e2e_leg(torch, args, coords_np):
 
 
 def kmap_leg(torch, keys_np):
+    """Config 2: build_kmap(dataflow=0) per call as the reference times it
+    (HIP events around the Python call, host overhead included) and the
+    search kernel alone (back-to-back launches from C++)."""
     from spira_amd.nn import functional as F
+    from spira_amd.nn.functional import _native
     dev = torch.device("cuda:0")
     keys = torch.from_numpy(keys_np).to(dev)
     timer = Timer(torch)
@@ -116,28 +120,50 @@ def kmap_leg(torch, keys_np):
     out = {}
     for k in (3, 5):
         mean_ms, min_ms = timer(lambda: F.build_kmap(keys, keys, k, 1, 0), reps=20, warmup=3)
+        kern_ms = _native._C.time_kmap_search(keys, keys, (k, k, k), (1, 1, 1), 50)
         K = k ** 3
         nbytes = 8 * S + 8 * T + 4 * K * T
-        out[k] = {"us": mean_ms * 1e3, "min_us": min_ms * 1e3, "bytes": nbytes,
-                  "gbs": nbytes / (mean_ms * 1e-3) / 1e9}
+        out[k] = {"us": mean_ms * 1e3, "min_us": min_ms * 1e3, "kernel_us": kern_ms * 1e3, "bytes": nbytes,
+                  "gbs": nbytes / (kern_ms * 1e-3) / 1e9}
     return out
 
 
-def layer_leg(torch, keys_np, C=64):
-    from oracle import oracle as orc  # noqa: F401  (not used on the timed path)
+def layer_leg(torch, keys_np, channels=(16, 32, 64, 128, 256), reps=20):
+    """Config 3 (LiDAR, k=3, s=1): the output-stationary fp16 layer per
+    channel count, kernel only (back-to-back launches from C++)."""
     from spira_amd.nn import functional as F
+    from spira_amd.nn.functional import _native
     dev = torch.device("cuda:0")
     keys = torch.from_numpy(keys_np).to(dev)
     m = F.build_kmap(keys, keys, 3, 1, 0)
     S = T = keys.shape[0]
+    P = int((m[2][:T] >= 0).sum().item())
+    out = {}
+    for C in channels:
+        X = torch.randn(S, C, device=dev, dtype=torch.float16)
+        W = (torch.randn(27, C, C, device=dev) / np.sqrt(27 * C)).half()
+        ms = _native._C.time_conv_os(S, T, m[2], X, W, reps)
+        flops = 2.0 * P * C * C
+        out[C] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+    return {"pairs": P, "voxels": S, "per_C": out}
+
+
+def dominant_leg(torch, keys_np, C=96, reps=20):
+    """The dominant kernel of the config-4 run: the output-stationary fp16
+    layer at full resolution (200k indoor voxels, k=3, 96 -> 96 channels),
+    kernel only."""
+    from spira_amd.nn import functional as F
+    from spira_amd.nn.functional import _native
+    dev = torch.device("cuda:0")
+    keys = torch.from_numpy(keys_np).to(dev)
+    m = F.build_kmap(keys, keys, 3, 1, 0)
+    S = T = keys.shape[0]
+    P = int((m[2][:T] >= 0).sum().item())
     X = torch.randn(S, C, device=dev, dtype=torch.float16)
     W = (torch.randn(27, C, C, device=dev) / np.sqrt(27 * C)).half()
-    P = int((m[2][:T] >= 0).sum().item())
-    timer = Timer(torch)
-    mean_ms, min_ms = timer(lambda: F.sparse_convolution_forward_os(S, T, m[2], X, W), reps=20, warmup=3)
+    ms = _native._C.time_conv_os(S, T, m[2], X, W, reps)
     flops = 2.0 * P * C * C
-    return {"ms": mean_ms, "min_ms": min_ms, "pairs": P, "flops": flops,
-            "tflops": flops / (mean_ms * 1e-3) / 1e12, "C": C, "voxels": S}
+    return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12, "pairs": P, "C": C}
 
 
 # ---------------------------------------------------------------------------
@@ -243,20 +269,28 @@ def main():
         km = kmap_leg(torch, lkeys)
         res["kmap_build_us"] = km[3]["us"]
         res["kmap_build_us_k5"] = km[5]["us"]
+        res["kmap_kernel_us"] = km[3]["kernel_us"]
+        res["kmap_kernel_us_k5"] = km[5]["kernel_us"]
         res["kmap_roofline"] = {"bound": "hbm", "achieved": km[3]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": km[3]["gbs"] / HBM_PEAK_GBS, "traffic": None,
-                                "kernel": "kmap_search_kernel (config 2, k=3, OS layout)",
+                                "kernel": "kmap_search_kernel<u64,3> (config 2, k=3, OS layout)",
                                 "algorithmic_bytes": km[3]["bytes"]}
         res["kmap_roofline_k5"] = {"achieved": km[5]["gbs"], "frac": km[5]["gbs"] / HBM_PEAK_GBS,
                                    "algorithmic_bytes": km[5]["bytes"]}
         cfg["kmap_voxels"] = int(lkeys.shape[0])
     if "layer" in legs:
         ly = layer_leg(torch, lkeys)
-        res["layer_ms"] = ly["ms"]
-        res["roofline"] = {"bound": "mfma", "achieved": ly["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
-                           "unit": "TFLOP/s", "frac": ly["tflops"] / MFMA_F16_PEAK_TFLOPS, "traffic": None,
-                           "kernel": "os_f16_kernel (config 3, C=64, k=3, 100k LiDAR voxels)",
-                           "algorithmic_flops": ly["flops"], "valid_pairs": ly["pairs"]}
+        res["layer_ms"] = ly["per_C"][64]["ms"]
+        res["layer_sweep"] = {str(c): {"ms": v["ms"], "tflops": v["tflops"],
+                                       "frac": v["tflops"] / MFMA_F16_PEAK_TFLOPS}
+                              for c, v in ly["per_C"].items()}
+        res["layer_pairs"] = ly["pairs"]
+        ikeys, _ = orc.flatten_sort(indoor, True)
+        dm = dominant_leg(torch, ikeys)
+        res["roofline"] = {"bound": "mfma", "achieved": dm["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": dm["tflops"] / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+                           "kernel": "os_kernel<3,0,true> (config 4 full resolution, 200k voxels, k=3, 96->96, fp16)",
+                           "ms": dm["ms"], "algorithmic_flops": dm["flops"], "valid_pairs": dm["pairs"]}
     if not args.no_cpu and model is not None:
         feats = np.random.default_rng(0).standard_normal((indoor.shape[0], 3)).astype(np.float32)
         t0 = time.perf_counter()

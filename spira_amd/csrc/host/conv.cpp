@@ -514,6 +514,33 @@ float time_scatter(int64_t tile, const std::optional<double> &threshold, bool is
   return time_phase(Phase::kScatter, threshold, is_hybrid, W, sm, tm, nb);
 }
 
+// Kernel-only timing of the output-stationary layer: `reps` back-to-back
+// launches on the current stream between two HIP events, after the row
+// order (cached per map) and the prepared weights exist; returns ms per
+// launch.  No reference counterpart: a measurement probe for the roofline
+// report (the reference times its layers from Python,
+// scripts/layerwise_experiment.py:100-186).
+float time_conv_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const torch::Tensor &X,
+                   const torch::Tensor &W, int64_t reps) {
+  check_features(X, W);
+  SPIRA_CHECK_ARG(reps >= 1, "reps must be positive");
+  auto Y = torch::empty({T, W.size(2)}, X.options());
+  const int K = static_cast<int>(W.size(0));
+  run_os(&out_in_map, S, T, X, W, 0, K, Y.data_ptr(), SPIRA_OUT_STORE);  // warm: order, weights
+  auto s = current_stream();
+  hipEvent_t a, b;
+  SPIRA_CHECK_ARG(hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess, "event creation failed");
+  SPIRA_CHECK_ARG(hipEventRecord(a, s) == hipSuccess, "event record failed");
+  for (int64_t i = 0; i < reps; ++i) run_os(&out_in_map, S, T, X, W, 0, K, Y.data_ptr(), SPIRA_OUT_STORE);
+  SPIRA_CHECK_ARG(hipEventRecord(b, s) == hipSuccess, "event record failed");
+  SPIRA_CHECK_ARG(hipEventSynchronize(b) == hipSuccess, "event synchronisation failed");
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, a, b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return ms / static_cast<float>(reps);
+}
+
 // (reference: cuda_free_buffers / cuda_reset_error, torch/cuda_memory_buffer.cu:7-16)
 void free_buffers() { c10::hip::HIPCachingAllocator::emptyCache(); }
 void reset_error() { (void)hipGetLastError(); }
@@ -521,6 +548,7 @@ void reset_error() { (void)hipGetLastError(); }
 void register_conv(pybind11::module_ &m) {
   m.def("cuda_sparse_convolution_forward_os", &forward_os);
   m.def("cuda_dense_forward", &forward_dense);
+  m.def("time_conv_os", &time_conv_os);
   m.def("cuda_sparse_convolution_forward_ws", &forward_ws);
   m.def("cuda_sparse_convolution_forward_ws_merged", &forward_ws_merged);
   m.def("cuda_sparse_convolution_forward_hs", &forward_hs);

@@ -228,7 +228,41 @@ torch::Tensor convert_transposed_os(const torch::Tensor &out_in_map, int64_t num
   return out;
 }
 
+// Kernel-only timing of the map search (output-stationary layout): `reps`
+// back-to-back launches into one preallocated map between two HIP events;
+// returns ms per launch.  No reference counterpart: a measurement probe for
+// the roofline report (the reference times build_kmap from Python,
+// scripts/mapping_experiment.py:81-101).
+float time_kmap_search(const torch::Tensor &sources, const torch::Tensor &targets, const Int3 &kernel_size,
+                       const Int3 &source_stride, int64_t reps) {
+  check_keys(sources, targets);
+  SPIRA_CHECK_ARG(reps >= 1, "reps must be positive");
+  auto [kx, ky, kz] = kernel_size;
+  auto [sx, sy, sz] = source_stride;
+  const int64_t S = sources.size(0), T = targets.size(0), Tp = round128(T);
+  auto map = empty_i32({std::max<int64_t>(Tp, 1), kx * ky * kz}, sources.device());
+  auto s = current_stream();
+  auto launch = [&] {
+    check_rc(spira_hip_kmap_search(sources.data_ptr(), S, targets.data_ptr(), T, key_bits_of(sources), kx, ky, kz,
+                                   sx, sy, sz, SPIRA_KMAP_OS, nullptr, map.data_ptr<int32_t>(), nullptr, s),
+             "time_kmap_search");
+  };
+  launch();
+  hipEvent_t a, b;
+  SPIRA_CHECK_ARG(hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess, "event creation failed");
+  SPIRA_CHECK_ARG(hipEventRecord(a, s) == hipSuccess, "event record failed");
+  for (int64_t i = 0; i < reps; ++i) launch();
+  SPIRA_CHECK_ARG(hipEventRecord(b, s) == hipSuccess, "event record failed");
+  SPIRA_CHECK_ARG(hipEventSynchronize(b) == hipSuccess, "event synchronisation failed");
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, a, b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return ms / static_cast<float>(reps);
+}
+
 void register_mapping(pybind11::module_ &m) {
+  m.def("time_kmap_search", &time_kmap_search);
   m.def("cuda_binary_search", &binary_search);
   m.def("cuda_binary_search_streamed", &binary_search_streamed);
   m.def("cuda_binary_search_no_small_z", &binary_search_no_small_z);

@@ -48,3 +48,13 @@ def test_extension_exports_reference_names():
         "cuda_free_buffers", "cuda_reset_error",
     }
     assert expected <= set(dir(_native._C))
+
+
+def test_spira_alias_resolves_to_spira_amd():
+    """`import spira` (the reference's package name) is this implementation."""
+    import spira
+    import spira_amd
+    assert spira is spira_amd
+    import spira.nn
+    assert spira.nn.SparseConv is spira_amd.nn.SparseConv
+    assert hasattr(spira, "SparseTensor") and hasattr(spira, "tune") and hasattr(spira, "set_kernel_map_cache")
