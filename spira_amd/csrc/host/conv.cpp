@@ -103,6 +103,15 @@ static bool &row_order_flag() {
   return on;
 }
 static bool row_order_enabled() { return row_order_flag(); }
+// Maps with fewer targets than this skip the row order: its sort costs more
+// than the few small blocks it would save.
+static int64_t row_order_min_targets() {
+  static const int64_t v = [] {
+    const char *e = std::getenv("SPIRA_OS_ROW_ORDER_MIN_T");
+    return e ? std::atoll(e) : int64_t(100000);
+  }();
+  return v;
+}
 void set_row_order(bool on) { row_order_flag() = on; }
 
 static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
@@ -205,7 +214,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto ws = workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && K <= 128) {
+  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
