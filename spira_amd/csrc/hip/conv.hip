@@ -376,6 +376,61 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[WN], const int3
   }
 }
 
+// Storage-dtype output of a wave's 32*MT x BN tile through LDS: the
+// accumulators (times scale, plus shift) are staged as fp16 rows, then every
+// lane writes 16-byte chunks of output rows (adding the residual and
+// applying ReLU), so that the output rows are written with full-width
+// vector stores.  Needs Cout % 8 == 0 (16-byte aligned rows) and a staging
+// area of 32*MT x (BN + 8) halves per wave.
+template <int WN, int MT>
+__device__ __forceinline__ void store_tile_vec(const floatx16 (&acc)[MT][WN], const int32_t *orow, int n0, int Cout,
+                                               _Float16 *stage, void *Yv, const Epilogue &epi) {
+  constexpr int BN = 32 * WN, BNP = BN + 8, ROWS = 32 * MT;
+  const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
+#pragma unroll
+  for (int wn = 0; wn < WN; ++wn) {
+    const int col = n0 + wn * 32 + r;
+    float sc = 1.f, sh = 0.f;
+    if (col < Cout) {
+      if (epi.scale) sc = epi.scale[col];
+      if (epi.shift) sh = epi.shift[col];
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = m * 32 + (i / 4) * 8 + kh * 4 + (i % 4);
+        stage[row * BNP + wn * 32 + r] = static_cast<_Float16>(acc[m][wn][i] * sc + sh);
+      }
+  }
+  // the staging rows are private to the wave: LDS keeps its accesses in order
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  constexpr int CPR = BN / 8;  // 16-byte chunks per row
+  _Float16 *Y = static_cast<_Float16 *>(Yv);
+  const _Float16 *R = static_cast<const _Float16 *>(epi.residual);
+  for (int q = lane; q < ROWS * CPR; q += 64) {
+    const int row = q / CPR, ch = q - row * CPR;
+    const int col = n0 + ch * 8;
+    const int32_t o = orow[row];
+    if (o < 0 || col >= Cout) continue;
+    half8 v = *reinterpret_cast<const half8 *>(stage + row * BNP + ch * 8);
+    const int64_t at = static_cast<int64_t>(o) * Cout + col;
+    if (R || epi.relu) {
+      half8 rv = {};
+      if (R) rv = *reinterpret_cast<const half8 *>(R + at);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float f = static_cast<float>(v[e]) + static_cast<float>(rv[e]);
+        if (epi.relu) f = f > 0.f ? f : 0.f;
+        v[e] = static_cast<_Float16>(f);
+      }
+    }
+    *reinterpret_cast<half8 *>(Y + at) = v;
+  }
+}
+
 #ifdef SPIRA_BLOCK_TIMING
 // experiment builds only: per-block wall-clock stamps of the OS kernel
 __device__ int64_t g_block_times[1 << 20];
@@ -489,7 +544,15 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
       orow_s[wave][m * 32 + r] = lr < T ? (order ? order[lr] : static_cast<int32_t>(lr)) : -1;
     }
   }
-  __syncthreads();
+  __syncthreads();  // every wave is done with the ring: it becomes the staging area
+  if constexpr (MODE == kStoreNative) {
+    static_assert(4 * 32 * MT * (C::BN + 8) * 2 <= C::RING, "staging area exceeds the ring");
+    if (op.Cout % 8 == 0) {
+      store_tile_vec<WN, MT>(acc, orow_s[wave], n0, op.Cout,
+                             reinterpret_cast<_Float16 *>(ring_lds) + wave * 32 * MT * (C::BN + 8), Y, epi);
+      return;
+    }
+  }
 #pragma unroll
   for (int m = 0; m < MT; ++m) store_tile<WN, MODE>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Y, epi);
 }
