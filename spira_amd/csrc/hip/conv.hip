@@ -79,21 +79,23 @@ namespace ring {
 constexpr int KC = 32;  // input channels per step
 
 // Ring layout: stage s at byte s * STAGE holds the step's weight chunk
-// (B_BYTES: BN rows x 64 B, XOR-swizzled) followed by its gathered rows
-// (A_BYTES: per wave MT tiles x 2 k-halves x 64 lanes x 16 B, lane-linear).
+// (BN rows x 64 B, XOR-swizzled), shared by the block's four waves.  The
+// gathered rows are private to a wave and go straight into registers (one
+// 16-byte buffer load per lane, tile and k-half: the MFMA A layout), so they
+// cost no LDS bandwidth.
 template <int WN, int MT, int NS_> struct Cfg {
   static constexpr int NS = NS_;  // ring depth: NS - 1 steps load while one computes
   static constexpr int BN = 32 * WN;
   static constexpr int BM = 128 * MT;
   static constexpr int BVEC = (BN * 4 + 255) / 256;  // 16-byte weight vectors per thread and step
   static constexpr int B_BYTES = BVEC * 4096;
-  static constexpr int A_BYTES = MT * 8192;
-  static constexpr int STAGE = B_BYTES + A_BYTES;
+  static constexpr int STAGE = B_BYTES;
   static constexpr int RING = NS * STAGE;
-  static constexpr int LPS = MT * 2 + BVEC;  // LDS-DMA loads per wave and step
+  static constexpr int OUT_STAGE = BM * (BN + 8) * 2;  // fp16 output tile staged by the epilogue
+  static constexpr int LDS = RING > OUT_STAGE ? RING : OUT_STAGE;
+  static constexpr int LPS = MT * 2 + BVEC;  // vector-memory loads per wave and step
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
   static_assert((NS - 1) * STAGE + (WN - 1) * 2048 < 65536, "weight read offset exceeds 16 bits");
-  static_assert((NS - 1) * STAGE + (2 * MT - 1) * 1024 < 65536, "row read offset exceeds 16 bits");
 };
 
 // Tile shape per column-tile width: MT 32-row tiles per wave and the ring
@@ -153,27 +155,26 @@ template <class V> __device__ __forceinline__ void pin(V &v) { asm volatile("" :
 
 // per-lane LDS read bases of the ring
 struct ReadBase {
-  uint32_t a;       // rows: + s * STAGE + (m * 2 + ks) * 1024
   uint32_t b0, b1;  // weights, k-half 0 / 1: + s * STAGE + wn * 2048
 };
-template <class C> __device__ __forceinline__ ReadBase read_base(const char *ring, int wave) {
+template <class C> __device__ __forceinline__ ReadBase read_base(const char *ring) {
   const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
   const uint32_t base = lds_addr(ring);
   const int q = (r >> 2) & 3;  // B swizzle: chunk c of row n sits at n * 4 + (c ^ ((n / 4) % 4))
   ReadBase rb;
-  rb.a = base + C::B_BYTES + wave * C::BM / 4 * 64 + lane * 16;
   rb.b0 = base + (r * 4 + (kh ^ q)) * 16;
   rb.b1 = base + (r * 4 + ((2 | kh) ^ q)) * 16;
   return rb;
 }
 
-// Issue the loads of one step into stage S: A rows idx[m] (or -1) at
-// channels kb..kb+31, weight row `wrow`.  When !live every load is out of
-// range, so each wave issues the same number of loads in every step.
+// Issue the loads of one step: A rows idx[m] (or -1) at channels
+// kb..kb+31 into a[m][k-half], weight row `wrow` into ring stage S.  When
+// !live every load is out of range, so each wave issues the same number of
+// loads in every step.
 template <class C, bool ALIGNED, int S>
 __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
                                       int kb, const Operands &op, __amdgpu_buffer_rsrc_t xr,
-                                      __amdgpu_buffer_rsrc_t wr, int n0) {
+                                      __amdgpu_buffer_rsrc_t wr, int n0, half8 (&a)[C::BM / 128][2]) {
   constexpr int MT = C::BM / 128;
   const int tid = threadIdx.x, lane = tid & 63;
   const int kh = lane >> 5;
@@ -183,21 +184,25 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int k = kb + ks * 16 + kh * 8;
-      char *dst = stage + C::B_BYTES + ((wave * MT + m) * 2 + ks) * 1024;
+      // branch-free: a divergent branch here would make both sides write
+      // the destination registers, and the second write would have to
+      // wait for every load in flight
+      const bool ok = live & (idx[m] >= 0) & (k < op.Cin);
+      const uint32_t at = (static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>(op.Cin) + k) * 2u;
+      const uint32_t off = ok ? at : kOutOfRange;
       if constexpr (!ALIGNED) {
-        // rows that are not 16-byte aligned are staged through registers
+        // rows that are not 16-byte aligned: element loads (still one
+        // vector-memory op per k-half in the count, the first element's)
         half8 v;
+        v[0] = __builtin_bit_cast(_Float16, static_cast<unsigned short>(
+                                                __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0)));
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
+        for (int e = 1; e < 8; ++e)
           v[e] = (live && idx[m] >= 0 && k + e < op.Cin) ? op.X[static_cast<int64_t>(idx[m]) * op.Cin + k + e]
                                                         : static_cast<_Float16>(0.f);
-        *reinterpret_cast<half8 *>(dst + lane * 16) = v;
-        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+        a[m][ks] = v;
       } else {
-        const uint32_t off = (live && idx[m] >= 0 && k < op.Cin)
-                                 ? (static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>(op.Cin) + k) * 2u
-                                 : kOutOfRange;
-        dma16(xr, off, dst);
+        a[m][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
       }
     }
   }
@@ -215,29 +220,24 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
 
 // MFMAs of stage S (rows without a neighbour hold zeros)
 template <class C, int S>
-__device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase &rb) {
+__device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase &rb,
+                                        const half8 (&a)[C::BM / 128][2]) {
   constexpr int MT = C::BM / 128, WN = C::BN / 32;
   unroll<2>([&](auto KS) {
     constexpr int ks = decltype(KS)::value;
-    half8 b[WN], a[MT];
+    half8 b[WN];
     unroll<WN>([&](auto W) {
       constexpr int wn = decltype(W)::value;
       b[wn] = rd16<S * C::STAGE + wn * 2048>(ks ? rb.b1 : rb.b0);
-    });
-    unroll<MT>([&](auto M) {
-      constexpr int m = decltype(M)::value;
-      a[m] = rd16<S * C::STAGE + (m * 2 + ks) * 1024>(rb.a);
     });
     lds_wait();
 #pragma unroll
     for (int wn = 0; wn < WN; ++wn) pin(b[wn]);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) pin(a[m]);
-#pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int wn = 0; wn < WN; ++wn)
-        acc[m][wn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m], b[wn], acc[m][wn], 0, 0, 0);
+        acc[m][wn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m][ks], b[wn], acc[m][wn], 0, 0, 0);
   });
 }
 
@@ -266,7 +266,8 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
-  const ReadBase rb = read_base<C>(ring, wave);
+  const ReadBase rb = read_base<C>(ring);
+  half8 areg[NS][MT][2];  // gathered rows per stage
   auto put = [&](int u, auto St) {
     int32_t idx[MT];
     int wrow = 0;
@@ -277,7 +278,8 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
 #pragma unroll
       for (int m = 0; m < MT; ++m) idx[m] = -1;
     }
-    issue<C, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, wr, n0);
+    issue<C, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, wr, n0,
+                                           areg[decltype(St)::value]);
   };
   unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
   unroll<NS - 1>([&](auto I) {
@@ -294,7 +296,7 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
       __builtin_amdgcn_s_barrier();
       put(s + i + NS - 1, std::integral_constant<int, slot>{});
       fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
-      compute<C, i>(acc, rb);
+      compute<C, i>(acc, rb, areg[i]);
     });
   }
   wait_vm<0>();
@@ -454,7 +456,7 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
                                                     Operands op, void *Y, Epilogue epi) {
   using C = typename ring::TileOf<WN>::C;
   constexpr int MT = C::BM / 128, NS = C::NS;
-  __shared__ __align__(1024) char ring_lds[C::RING];
+  __shared__ __align__(1024) char ring_lds[C::LDS];
   __shared__ __align__(16) int32_t idx_lds[NS][256];  // map entries of a later step, per stage
   __shared__ int32_t orow_s[4][32 * MT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -546,7 +548,6 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   }
   __syncthreads();  // every wave is done with the ring: it becomes the staging area
   if constexpr (MODE == kStoreNative) {
-    static_assert(4 * 32 * MT * (C::BN + 8) * 2 <= C::RING, "staging area exceeds the ring");
     if (op.Cout % 8 == 0) {
       store_tile_vec<WN, MT>(acc, orow_s[wave], n0, op.Cout,
                              reinterpret_cast<_Float16 *>(ring_lds) + wave * 32 * MT * (C::BN + 8), Y, epi);
