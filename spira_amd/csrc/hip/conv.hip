@@ -14,27 +14,33 @@
 //    (MT*WN accumulators of 16 floats); WN = 1, 2, 3, 4 or 8 so that 96- and
 //    256-channel layers do not pad to a power of two;
 //  * the K dimension is walked in steps of 32 input channels of one kernel
-//    offset.  Each step's operands land in a 3-stage LDS ring through
-//    global_load_lds_dwordx4 (direct HBM/L2 -> LDS, no register staging): the
-//    gathered rows lane-linearly (lane L of a wave fetches exactly the 16
-//    bytes its MFMA A slot needs, so the A reads are conflict-free), the
-//    offset's weight chunk with an XOR swizzle that makes the B reads
-//    conflict-free.  Loads run two steps ahead of the MFMAs; a step costs one
-//    workgroup barrier and one vmcnt wait, and rows without a neighbour read a
-//    16-byte zero block instead of branching;
+//    offset.  The offset's weight chunk (shared by the four waves) lands in a
+//    3-stage LDS ring through global_load_lds_dwordx4 (direct HBM/L2 -> LDS)
+//    with an XOR swizzle that makes the B reads conflict-free; the gathered
+//    rows (private to a wave) are loaded straight into the registers of the
+//    MFMA A operand (lane L fetches exactly the 16 bytes its A slot needs).
+//    Loads run two steps ahead of the MFMAs; a step costs one workgroup
+//    barrier and one vmcnt wait, and rows without a neighbour read a 16-byte
+//    zero block instead of branching;
 //  * weights are prepared once per weight tensor into [K, CoutP, CinP]
 //    (transposed, zero-padded to 32 output / 16 input channels), so odd
 //    channel counts (the 3-channel stem) take the same path;
 //  * the output-stationary kernel can walk its rows in neighbour-mask order
 //    (rows with the same neighbour pattern together) and visits only the
-//    offsets some row of the block uses; small layers split the offsets over
-//    blocks (fp32 atomics + finalize);
+//    offsets some row of the block uses.  A block with many steps splits its
+//    offsets over several workgroups (small layers: every block, so that the
+//    grid covers the chip; row-ordered layers: the densest leading blocks,
+//    which would otherwise outlast the rest of the grid); the splits store
+//    fp32 partial tiles and the last one to finish sums them and writes the
+//    output (no fill or finalize pass);
 //  * an optional epilogue folds a per-channel scale / shift (eval-mode batch
 //    norm), a residual add and ReLU into the output write.
 #include "common.hpp"
 #include "../../../include/spira_hip.h"
 
 #include <algorithm>
+#include <atomic>
+#include <cstdlib>
 #include <utility>
 #include <vector>
 
@@ -42,6 +48,8 @@ namespace spira_hip {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uint32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
 
@@ -55,6 +63,26 @@ struct Epilogue {
   const void *residual;  // [T, Cout] in the storage dtype, or null
   int relu;
 };
+
+// Offset splitting of the output-stationary kernel.  Row blocks b < hb may
+// split: block b runs as up to zs workgroups (linear ids z*hb + b, all
+// among the first hb*zs ids so that they start early), each taking an
+// equal share of the block's active offsets, ceil(steps / tgt) of them at
+// most.  Each split adds its fp32 tile atomically into the accumulator
+// part[b*ny + y] and takes a ticket; the last one reads the sum, clears the
+// accumulator and writes the output.  The accumulators (caller workspace)
+// start zeroed and are left zeroed.  Tickets live in kTicketSlots rotating
+// sets of a device array that starts zeroed and is left zeroed (the last
+// split resets its ticket); `tslot` picks the set, so that up to
+// kTicketSlots calls can be in flight at once.  Blocks b >= hb run as one
+// workgroup each.
+struct Split {
+  int hb, zs, tgt, ny, tslot;
+  float *part;
+};
+constexpr int kTicketSlots = 64;
+constexpr int kTicketsPerSlot = 4096;  // >= hb * ny
+__device__ int32_t g_split_tickets[kTicketSlots * kTicketsPerSlot];
 
 // Gathered operands of the MMA core.  Both are addressed through buffer
 // resources with 32-bit byte offsets: a lane whose row is missing (or whose
@@ -76,34 +104,45 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
 
 namespace ring {
 
-constexpr int KC = 32;  // input channels per step
-
 // Ring layout: stage s at byte s * STAGE holds the step's weight chunk
-// (BN rows x 64 B, XOR-swizzled), shared by the block's four waves.  The
-// gathered rows are private to a wave and go straight into registers (one
-// 16-byte buffer load per lane, tile and k-half: the MFMA A layout), so they
-// cost no LDS bandwidth.
-template <int WN, int MT, int NS_> struct Cfg {
+// (BN rows x ROWB = KC * 2 bytes, 16-byte chunks XOR-swizzled per row),
+// shared by the block's four waves.  The gathered rows are private to a wave
+// and go straight into registers (one 16-byte buffer load per lane, tile and
+// 16-channel slice: the MFMA A layout), so they cost no LDS bandwidth.  A
+// step covers KC = 16 * NKS input channels of one kernel offset: NKS = 2
+// (32 channels) or 4 (64 channels, fewer steps and so less per-step
+// synchronisation for wide layers).
+template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int NS = NS_;  // ring depth: NS - 1 steps load while one computes
+  static constexpr int NKS = NKS_;
+  static constexpr int KC = 16 * NKS;  // input channels per step
+  static constexpr int ROWB = KC * 2;  // bytes of a weight row per step
+  static constexpr int CPR = ROWB / 16;  // 16-byte chunks per weight row
   static constexpr int BN = 32 * WN;
   static constexpr int BM = 128 * MT;
-  static constexpr int BVEC = (BN * 4 + 255) / 256;  // 16-byte weight vectors per thread and step
+  static constexpr int BVEC = (BN * CPR + 255) / 256;  // 16-byte weight vectors per thread and step
   static constexpr int B_BYTES = BVEC * 4096;
   static constexpr int STAGE = B_BYTES;
   static constexpr int RING = NS * STAGE;
   static constexpr int OUT_STAGE = BM * (BN + 8) * 2;  // fp16 output tile staged by the epilogue
   static constexpr int LDS = RING > OUT_STAGE ? RING : OUT_STAGE;
-  static constexpr int LPS = MT * 2 + BVEC;  // vector-memory loads per wave and step
+  static constexpr int LPS = MT * NKS + BVEC;  // vector-memory loads per wave and step
+  static_assert(NKS == 2 || NKS == 4, "a step is 32 or 64 channels");
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
-  static_assert((NS - 1) * STAGE + (WN - 1) * 2048 < 65536, "weight read offset exceeds 16 bits");
+  static_assert((NS - 1) * STAGE + (WN - 1) * 32 * ROWB < 65536, "weight read offset exceeds 16 bits");
+  static_assert((NS - 2) * LPS + (NS - 1) < 64, "vmcnt range");
+  // physical chunk of logical chunk c of weight row n: conflict-free 16-byte
+  // reads for 8 consecutive rows at one chunk, independent of n / 32
+  __host__ __device__ static constexpr int swz(int n) { return NKS == 2 ? (n >> 2) & 3 : n & 7; }
 };
 
-// Tile shape per column-tile width: MT 32-row tiles per wave and the ring
-// depth, sized so that two blocks (eight waves) fit a CU's 160 KiB of LDS.
-template <int WN> struct TileOf {
+// Tile shape per column-tile width and step: MT 32-row tiles per wave and
+// the ring depth, sized so that two blocks (eight waves, <= 256 VGPRs each)
+// fit a CU's 160 KiB of LDS.
+template <int WN, int NKS = 2> struct TileOf {
   static constexpr int MT = WN >= 8 ? 1 : (WN >= 3 ? 2 : 1);
-  static constexpr int NS = WN >= 3 ? 3 : 4;
-  using C = Cfg<WN, MT, NS>;
+  static constexpr int NS = NKS == 2 ? (WN >= 3 ? 3 : 4) : (WN >= 3 ? 2 : 3);
+  using C = Cfg<WN, MT, NS, NKS>;
 };
 
 // compile-time loop: f(std::integral_constant<int, I>) for I in [0, N)
@@ -153,28 +192,28 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 // ties a value read by rd16 / rd4 to a point after lds_wait()
 template <class V> __device__ __forceinline__ void pin(V &v) { asm volatile("" : "+v"(v)); }
 
-// per-lane LDS read bases of the ring
-struct ReadBase {
-  uint32_t b0, b1;  // weights, k-half 0 / 1: + s * STAGE + wn * 2048
+// per-lane LDS read bases of the ring: weights of 16-channel slice ks,
+// + s * STAGE + wn * 32 * ROWB
+template <int NKS> struct ReadBase {
+  uint32_t b[NKS];
 };
-template <class C> __device__ __forceinline__ ReadBase read_base(const char *ring) {
+template <class C> __device__ __forceinline__ ReadBase<C::NKS> read_base(const char *ring) {
   const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
   const uint32_t base = lds_addr(ring);
-  const int q = (r >> 2) & 3;  // B swizzle: chunk c of row n sits at n * 4 + (c ^ ((n / 4) % 4))
-  ReadBase rb;
-  rb.b0 = base + (r * 4 + (kh ^ q)) * 16;
-  rb.b1 = base + (r * 4 + ((2 | kh) ^ q)) * 16;
+  ReadBase<C::NKS> rb;
+#pragma unroll
+  for (int ks = 0; ks < C::NKS; ++ks) rb.b[ks] = base + (r * C::CPR + ((2 * ks + kh) ^ C::swz(r))) * 16;
   return rb;
 }
 
 // Issue the loads of one step: A rows idx[m] (or -1) at channels
-// kb..kb+31 into a[m][k-half], weight row `wrow` into ring stage S.  When
+// kb..kb+KC-1 into a[m][slice], weight row `wrow` into ring stage S.  When
 // !live every load is out of range, so each wave issues the same number of
 // loads in every step.
 template <class C, bool ALIGNED, int S>
 __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
                                       int kb, const Operands &op, __amdgpu_buffer_rsrc_t xr,
-                                      __amdgpu_buffer_rsrc_t wr, int n0, half8 (&a)[C::BM / 128][2]) {
+                                      __amdgpu_buffer_rsrc_t wr, int n0, half8 (&a)[C::BM / 128][C::NKS]) {
   constexpr int MT = C::BM / 128;
   const int tid = threadIdx.x, lane = tid & 63;
   const int kh = lane >> 5;
@@ -182,7 +221,7 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < C::NKS; ++ks) {
       const int k = kb + ks * 16 + kh * 8;
       // branch-free: a divergent branch here would make both sides write
       // the destination registers, and the second write would have to
@@ -209,8 +248,8 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
 #pragma unroll
   for (int i = 0; i < C::BVEC; ++i) {
     const int v = i * 256 + tid;
-    const int n = v >> 2, cp = v & 3;
-    const int c = cp ^ ((n >> 2) & 3);
+    const int n = v / C::CPR, cp = v % C::CPR;
+    const int c = cp ^ C::swz(n);
     const uint32_t off = (live && n < C::BN && n0 + n < op.CoutP && kb + c * 8 < op.CinP)
                              ? ((static_cast<uint32_t>(wrow) * op.CoutP + n0 + n) * op.CinP + kb + c * 8) * 2u
                              : kOutOfRange;
@@ -220,15 +259,15 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
 
 // MFMAs of stage S (rows without a neighbour hold zeros)
 template <class C, int S>
-__device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase &rb,
-                                        const half8 (&a)[C::BM / 128][2]) {
+__device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase<C::NKS> &rb,
+                                        const half8 (&a)[C::BM / 128][C::NKS]) {
   constexpr int MT = C::BM / 128, WN = C::BN / 32;
-  unroll<2>([&](auto KS) {
+  unroll<C::NKS>([&](auto KS) {
     constexpr int ks = decltype(KS)::value;
     half8 b[WN];
     unroll<WN>([&](auto W) {
       constexpr int wn = decltype(W)::value;
-      b[wn] = rd16<S * C::STAGE + wn * 2048>(ks ? rb.b1 : rb.b0);
+      b[wn] = rd16<S * C::STAGE + wn * 32 * C::ROWB>(rb.b[ks]);
     });
     lds_wait();
 #pragma unroll
@@ -266,8 +305,8 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
-  const ReadBase rb = read_base<C>(ring);
-  half8 areg[NS][MT][2];  // gathered rows per stage
+  const ReadBase<C::NKS> rb = read_base<C>(ring);
+  half8 areg[NS][MT][C::NKS];  // gathered rows per stage
   auto put = [&](int u, auto St) {
     int32_t idx[MT];
     int wrow = 0;
@@ -449,19 +488,25 @@ __device__ int64_t g_block_times[1 << 20];
 // logical row i is target order[i] and `map` holds the rows in logical order;
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
-template <int WN, int MODE, bool ALIGNED>
+template <int WN, int MODE, bool ALIGNED, int NKS>
 __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
-                                                    Operands op, void *Y, Epilogue epi) {
-  using C = typename ring::TileOf<WN>::C;
+                                                    Split sp, Operands op, void *Y, Epilogue epi) {
+  using C = typename ring::TileOf<WN, NKS>::C;
   constexpr int MT = C::BM / 128, NS = C::NS;
   __shared__ __align__(1024) char ring_lds[C::LDS];
   __shared__ __align__(16) int32_t idx_lds[NS][256];  // map entries of a later step, per stage
   __shared__ int32_t orow_s[4][32 * MT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, kh = lane >> 5;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * C::BM;
+  // linear block id -> (row block, split): split z of block b < hb is id
+  // z * hb + b (consecutive ids go to different XCDs, so neither the dense
+  // leading blocks nor the splits of one block gather on a few XCDs)
+  const int lb = blockIdx.x;
+  const int rb_ = lb < sp.hb * sp.zs ? lb % sp.hb : lb - sp.hb * (sp.zs - 1);
+  const int z = lb < sp.hb * sp.zs ? lb / sp.hb : 0;
+  const int64_t row0 = static_cast<int64_t>(rb_) * C::BM;
   const int n0 = blockIdx.y * C::BN;
   const int j0 = blockIdx.z * jper;
   const int jn = ((j0 + jper) < Kc ? (j0 + jper) : Kc) - j0;
@@ -485,8 +530,30 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
     ulo &= slo;
     uhi &= shi;
   }
-  const int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
-  const int nch = (op.CinP + ring::KC - 1) / ring::KC;
+  int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
+  const int nch = (op.CinP + C::KC - 1) / C::KC;
+  int nsp = 1;  // splits of this block
+  if (rb_ < sp.hb) {
+    nsp = (nact * nch + sp.tgt - 1) / sp.tgt;
+    nsp = nsp < 1 ? 1 : (nsp > sp.zs ? sp.zs : nsp);
+    if (nsp > nact) nsp = nact > 0 ? nact : 1;
+  }
+  if (z >= nsp) {  // block-uniform
+#ifdef SPIRA_BLOCK_TIMING
+    SPIRA_STAMP(2);
+    if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = -1;
+#endif
+    return;
+  }
+  if (nsp > 1) {
+    // this split: active offsets [a0, a1) in increasing order
+    const int a0 = z * nact / nsp, a1 = (z + 1) * nact / nsp;
+    for (int i = 0; i < a0; ++i) {
+      if (ulo) ulo &= ulo - 1;
+      else uhi &= uhi - 1;
+    }
+    nact = a1 - a0;  // the step iterators stop after nact offsets
+  }
   const int nsteps = nact * nch;
   SPIRA_STAMP(1);
 
@@ -531,7 +598,7 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
       if (!mvalid[m]) idx[m] = -1;
     }
     wrow = j0 + pit.j;
-    kb = pit.chunk * ring::KC;
+    kb = pit.chunk * C::KC;
     pit.step(nch);
   };
   ring::run<C, ALIGNED, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
@@ -539,6 +606,40 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
 #ifdef SPIRA_BLOCK_TIMING
   if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = nact;
 #endif
+  if (nsp > 1) {
+    // add this split's tile into the block's accumulator (element-major:
+    // element i of accumulator (m, wn) of a wave is 64 consecutive floats,
+    // one per lane), take a ticket; the last split reads the sum
+    const int64_t tile = static_cast<int64_t>(C::BM) * C::BN;
+    float *slot = sp.part + (static_cast<int64_t>(rb_) * sp.ny + blockIdx.y) * tile + wave * (MT * WN * 1024) + lane;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int wn = 0; wn < WN; ++wn)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          __hip_atomic_fetch_add(slot + ((m * WN + wn) * 16 + i) * 64, acc[m][wn][i], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the adds have been performed
+    __syncthreads();
+    __shared__ int last_s;
+    int32_t *ticket = &g_split_tickets[sp.tslot * kTicketsPerSlot + rb_ * sp.ny + blockIdx.y];
+    if (tid == 0)
+      last_s = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
+    __syncthreads();
+    if (!last_s) return;  // block-uniform
+    if (tid == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int wn = 0; wn < WN; ++wn)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float *q = slot + ((m * WN + wn) * 16 + i) * 64;
+          acc[m][wn][i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(q, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+  }
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -623,9 +724,9 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
 #pragma unroll
     for (int m = 0; m < MT; ++m) idx[m] = src[m];
     wrow = wrow0;
-    kb = u * ring::KC;
+    kb = u * C::KC;
   };
-  const int nch = (op.CinP + ring::KC - 1) / ring::KC;
+  const int nch = (op.CinP + C::KC - 1) / C::KC;
   ring::run<C, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
@@ -674,9 +775,9 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operand
 #pragma unroll
     for (int m = 0; m < MT; ++m) idx[m] = src[m];
     wrow = g;
-    kb = u * ring::KC;
+    kb = u * C::KC;
   };
-  const int nch = (op.CinP + ring::KC - 1) / ring::KC;
+  const int nch = (op.CinP + C::KC - 1) / C::KC;
   ring::run<C, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
@@ -706,12 +807,13 @@ __global__ void prepare_w_kernel(const _Float16 *__restrict__ W, int K, int Cin,
 
 // fp32 partial sums -> storage dtype, with the optional epilogue
 template <typename FT>
-__global__ void finalize_kernel(const float *__restrict__ acc, int64_t T, int Cout, FT *__restrict__ Y,
-                                Epilogue epi) {
+__global__ void finalize_kernel(float *__restrict__ acc, int64_t T, int Cout, FT *__restrict__ Y,
+                                Epilogue epi, int clear) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= T * Cout) return;
   const int c = static_cast<int>(i % Cout);
   float v = acc[i];
+  if (clear) acc[i] = 0.f;
   if (epi.scale) v *= epi.scale[c];
   if (epi.shift) v += epi.shift[c];
   if (epi.residual) v += ld(static_cast<const FT *>(epi.residual) + i);
@@ -910,6 +1012,64 @@ static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
   return std::min(jper, 128);
 }
 
+// Offset-split plan of an output-stationary launch (Kc <= 128): row-ordered
+// layers with 256-column tiles let their densest leading blocks (the order
+// puts the groups with the most neighbour offsets first) split into pieces
+// of about `tgt` steps.  (Small layers split by static offset ranges
+// instead, small_layer_jper; narrower tiles gain nothing from the split.)
+// Overrides for measurements: SPIRA_OS_SPLIT=0 disables,
+// SPIRA_OS_SPLIT_HB / _ZS / _TGT / _MIN_BN, SPIRA_OS_SMALL_TICKET=1 splits
+// small layers this way too.
+struct SplitPlan {
+  int hb = 0, zs = 1, tgt = 1 << 30, ny = 1;
+  size_t bytes = 0;  // fp32 partial tiles
+};
+static int env_int(const char *name, int dflt) {
+  const char *v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+static SplitPlan plan_split(int64_t bx, int64_t by, int bm, int bn, int Kc, int CinP, int kc, bool ordered,
+                            int cus) {
+  SplitPlan p;
+  p.ny = static_cast<int>(by);
+  static const int enabled = env_int("SPIRA_OS_SPLIT", 1);
+  if (!enabled || Kc > 128 || Kc < 2) return p;
+  const int nch = div_up(CinP, kc);
+  int hb = 0, zs = 1, tgt = 1 << 30;
+  static const int small_ticket = env_int("SPIRA_OS_SMALL_TICKET", 0);
+  static const int min_bn = env_int("SPIRA_OS_SPLIT_MIN_BN", 256);
+  if (bx * by < cus) {
+    if (!small_ticket) return p;  // small layers: static offset ranges (small_layer_jper)
+    hb = static_cast<int>(bx);
+    zs = static_cast<int>(std::min<int64_t>(std::min(Kc, 16), div_up(2 * cus, bx * by)));
+    tgt = nch;
+  } else if (ordered && bn >= min_bn) {
+    hb = static_cast<int>(std::min<int64_t>(bx, env_int("SPIRA_OS_SPLIT_HB", 128)));
+    zs = env_int("SPIRA_OS_SPLIT_ZS", 4);
+    tgt = env_int("SPIRA_OS_SPLIT_TGT", std::max(24, 8 * nch) * 32 / kc);
+  }
+  if (hb * by > kTicketsPerSlot) hb = static_cast<int>(kTicketsPerSlot / by);
+  if (hb <= 0 || zs <= 1) return p;
+  p.hb = hb;
+  p.zs = zs;
+  p.tgt = std::max(1, tgt);
+  p.bytes = static_cast<size_t>(hb) * by * bm * bn * sizeof(float);
+  return p;
+}
+// Offsets per grid-z split: static offset ranges (fp32 atomics + a finalize
+// pass) for layers of more than 128 offsets and for small layers (fewer
+// blocks than CUs), unless the latter split per block
+static int small_layer_jper(int64_t blocks_xy, int Kc, int cus) {
+  static const int small_ticket = env_int("SPIRA_OS_SMALL_TICKET", 0);
+  static const int enabled = env_int("SPIRA_OS_SPLIT", 1);
+  if (Kc > 128 || (blocks_xy < cus && !(small_ticket && enabled))) return choose_jper(blocks_xy, Kc, cus);
+  return Kc;
+}
+static int next_ticket_slot() {
+  static std::atomic<int> n{0};
+  return n.fetch_add(1, std::memory_order_relaxed) % kTicketSlots;
+}
+
 // Operands of the MMA core; byte sizes must fit the 31-bit buffer offsets
 static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, const void *WT, int K, int Cout) {
   op.Cin = Cin;
@@ -936,23 +1096,34 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
     default: CALL(8); break;      \
   }
 
-template <int MODE, bool AL>
+template <int MODE, bool AL, int NKS>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op, void *Y,
-                      const Epilogue &epi) {
+                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const Split &sp, const Operands &op,
+                      void *Y, const Epilogue &epi) {
 #define SPIRA_OS_CALL(W)                                                                                         \
-  hipLaunchKernelGGL((os_kernel<W, MODE, AL>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
-                     jper, op, Y, epi)
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
+                     jper, sp, op, Y, epi)
   SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
 #undef SPIRA_OS_CALL
 }
 
+// 16-channel slices per step of the output-stationary kernel: 64-channel
+// steps once the (padded) input has 64 channels or more, else 32.
+// SPIRA_OS_KC=32 / 64 overrides (measurements).
+static int os_nks(int CinP) {
+  static const int kc = env_int("SPIRA_OS_KC", 0);
+  if (kc == 32) return 2;
+  if (kc == 64) return 4;
+  return CinP >= 64 ? 4 : 2;
+}
+
 template <int MODE>
 static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op, void *Y,
-                          const Epilogue &epi) {
-  if (op.Cin % 8 == 0) launch_os<MODE, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-  else launch_os<MODE, false>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const Split &sp,
+                          const Operands &op, void *Y, const Epilogue &epi) {
+  if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, sp, op, Y, epi);
+  else if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, sp, op, Y, epi);
+  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, sp, op, Y, epi);
 }
 
 template <bool AL>
@@ -1042,14 +1213,21 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
 
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
                                 size_t *bytes) {
-  (void)c_in;
   *bytes = 0;
-  if (!mfma_path(dtype) || out_mode != SPIRA_OUT_STORE || num_targets <= 0) return kOk;
+  if (!mfma_path(dtype) || num_targets <= 0) return kOk;
+  if (num_offsets > 128 && out_mode != SPIRA_OUT_STORE) return kOk;
   const int wn = wn_for(c_out);
   const int bm = bm_for(wn);
-  const int64_t blocks = div_up(num_targets, bm) * div_up(pad_out(c_out), 32 * wn);
-  if (choose_jper(blocks, num_offsets, device_cu_count()) < num_offsets)
-    *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
+  const int64_t bx = div_up(num_targets, bm), by = div_up(pad_out(c_out), 32 * wn);
+  const int cus = device_cu_count();
+  if (small_layer_jper(bx * by, num_offsets, cus) < num_offsets) {
+    if (out_mode == SPIRA_OUT_STORE) *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
+  } else {
+    // the larger of the plans with and without a row order
+    for (bool ordered : {false, true})
+      *bytes = std::max(*bytes, plan_split(bx, by, bm, 32 * wn, num_offsets, pad_in(c_in),
+                                                    c_in % 8 ? 32 : 16 * os_nks(pad_in(c_in)), ordered, cus).bytes);
+  }
   return kOk;
 }
 
@@ -1074,9 +1252,21 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     const int wn = wn_for(c_out);
     const int bm = bm_for(wn);
     const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
-    const int jper = choose_jper(bx * by, num_offsets, device_cu_count());
+    const int cus = device_cu_count();
+    const int jper = small_layer_jper(bx * by, num_offsets, cus);
     const int splits = static_cast<int>(div_up(num_offsets, jper));
-    dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(by), static_cast<unsigned>(splits));
+    Split sp{0, 1, 1 << 30, static_cast<int>(by), 0, nullptr};
+    if (splits == 1) {
+      const SplitPlan pl = plan_split(bx, by, bm, 32 * wn, num_offsets, CinP,
+                                        c_in % 8 ? 32 : 16 * os_nks(CinP), group_masks != nullptr, cus);
+      if (pl.hb > 0) {
+        SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= pl.bytes,
+                          "conv_os: workspace too small (spira_hip_conv_os_workspace)");
+        sp = Split{pl.hb, pl.zs, pl.tgt, pl.ny, next_ticket_slot(), static_cast<float *>(workspace)};
+      }
+    }
+    dim3 grid(static_cast<unsigned>(bx + static_cast<int64_t>(sp.hb) * (sp.zs - 1)), static_cast<unsigned>(by),
+              static_cast<unsigned>(splits));
     SPIRA_HIP_REQUIRE(num_targets * num_offsets * 4 < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
     // (out_in_map may be null: the identity map, handled in the kernel)
     Operands op;
@@ -1084,11 +1274,11 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     if (rc0) return rc0;
     if (splits == 1) {
       if (out_mode == SPIRA_OUT_STORE)
-        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, targets, epi);
       else if (out_mode == SPIRA_OUT_STORE_F32)
-        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, targets, epi);
       else
-        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, targets, epi);
     } else {
       float *acc = nullptr;
       if (out_mode == SPIRA_OUT_STORE) {
@@ -1098,15 +1288,16 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
       } else {
         acc = static_cast<float *>(targets);
       }
-      if (out_mode != SPIRA_OUT_ADD_F32) {
+      // (the workspace arrives zeroed and the finalize pass clears it again)
+      if (out_mode == SPIRA_OUT_STORE_F32) {
         int rc = fill_f32(acc, num_targets * c_out, 0.f, stream);
         if (rc) return rc;
       }
-      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, acc, epi);
+      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, acc, epi);
       SPIRA_HIP_LAUNCH_CHECK();
       if (out_mode == SPIRA_OUT_STORE)
         hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(num_targets * c_out, 256)), dim3(256), 0, stream,
-                           acc, num_targets, c_out, static_cast<_Float16 *>(targets), epi);
+                           acc, num_targets, c_out, static_cast<_Float16 *>(targets), epi, 1);
     }
   } else {
     if (out_mode == SPIRA_OUT_STORE)
@@ -1248,11 +1439,11 @@ int spira_hip_finalize(const float *acc, int64_t num_targets, int c_out, int dty
   if (n <= 0) return kOk;
   const Epilogue epi = make_epi(scale, shift, residual, relu);
   if (dtype == SPIRA_F16)
-    hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream, acc, num_targets, c_out,
-                       static_cast<_Float16 *>(targets), epi);
+    hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(n, 256)), dim3(256), 0, stream,
+                       const_cast<float *>(acc), num_targets, c_out, static_cast<_Float16 *>(targets), epi, 0);
   else
-    hipLaunchKernelGGL(finalize_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, acc, num_targets, c_out,
-                       static_cast<float *>(targets), epi);
+    hipLaunchKernelGGL(finalize_kernel<float>, dim3(div_up(n, 256)), dim3(256), 0, stream, const_cast<float *>(acc),
+                       num_targets, c_out, static_cast<float *>(targets), epi, 0);
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }

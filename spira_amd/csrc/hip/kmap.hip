@@ -31,6 +31,7 @@
 
 #include <rocprim/rocprim.hpp>
 
+#include <algorithm>
 #include <vector>
 
 namespace spira_hip {
@@ -448,31 +449,90 @@ __global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict
   iota[row0 + threadIdx.x] = static_cast<int32_t>(row0 + threadIdx.x);
 }
 
-// ordered[i, :] = map[order[i], :] and, per group of 128 ordered rows, the
-// 128-bit union of their valid columns (when gmask is given, K <= 128).  A
-// block covers 2 groups: its threads walk the 256 x K ordered elements
-// linearly (coalesced stores, row-contiguous loads) and OR-reduce the
-// column bits through LDS.
+// Per group of 128 sorted rows: the 128-bit union of their valid columns
+// (gm[g * 2 + w]) and a sort key that puts the groups with the most columns
+// first (128 - popcount) and keeps a trailing partial group last (255).
+// K <= 57: the unions come from the sort keys (their low K bits are the
+// rows' column masks), one wave per group.
+__global__ __launch_bounds__(256) void group_union_keys_kernel(const uint64_t *__restrict__ keys_sorted, int K,
+                                                               int64_t T, uint64_t *__restrict__ gm,
+                                                               uint32_t *__restrict__ gkey,
+                                                               int32_t *__restrict__ giota) {
+  const int64_t G = (T + 127) / 128;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (g >= G) return;
+  uint64_t m = 0;
+  if (keys_sorted) {
+    const uint64_t pm = (uint64_t(1) << K) - 1;
+    for (int r = lane; r < 128; r += 64) {
+      const int64_t row = g * 128 + r;
+      if (row < T) m |= keys_sorted[row] & pm;
+    }
+    for (int o = 32; o > 0; o >>= 1) m |= static_cast<uint64_t>(__shfl_xor(m, o, 64));
+    if (lane == 0) {
+      gm[g * 2] = m;
+      gm[g * 2 + 1] = 0;
+    }
+  }
+  if (lane == 0) {
+    const int pc = __popcll(gm[g * 2]) + __popcll(gm[g * 2 + 1]);
+    gkey[g] = (g + 1) * 128 > T ? 255u : static_cast<uint32_t>(128 - pc);
+    giota[g] = static_cast<int32_t>(g);
+  }
+}
+
+// Logical row L of the final order is sorted row gperm[L / 128] * 128 +
+// L % 128 (groups permuted, rows inside a group kept): order[L] = that
+// target, ordered[L, :] = its map row, gmask[L / 128] = its group's union.
+// Without gperm the groups keep their sorted places.  A block covers 2
+// groups: its threads walk the 256 x K ordered elements linearly (coalesced
+// stores, row-contiguous loads).  gm_in / gmask may be null (no masks); with
+// gperm == null and gm_in == null the unions are computed here instead, by
+// an OR-reduction of the column bits through LDS (K <= 128).
 __global__ __launch_bounds__(256) void order_rows_kernel(const int32_t *__restrict__ map,
-                                                         const int32_t *__restrict__ order, int64_t T, int K,
-                                                         int32_t *__restrict__ ordered, uint64_t *__restrict__ gmask) {
+                                                         const int32_t *__restrict__ sorted,
+                                                         const int32_t *__restrict__ gperm, int64_t T, int K,
+                                                         int32_t *__restrict__ order, int32_t *__restrict__ ordered,
+                                                         const uint64_t *__restrict__ gm_in,
+                                                         uint64_t *__restrict__ gmask) {
   __shared__ uint64_t red[2][2][4];  // [group][word][wave]
+  __shared__ int32_t src_s[256];
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 256;
   const int64_t rows = (T - row0) < 256 ? (T - row0) : 256;
+  if (threadIdx.x < rows) {
+    const int64_t L = row0 + threadIdx.x;
+    const int64_t sp = gperm ? static_cast<int64_t>(gperm[L / 128]) * 128 + (L % 128) : L;
+    const int32_t t = sorted[sp];
+    src_s[threadIdx.x] = t;
+    if (order) order[L] = t;
+  }
+  __syncthreads();
+  const bool reduce = gmask && !gm_in;
   const int64_t n = rows * K;
   uint64_t m[2][2] = {{0, 0}, {0, 0}};
-  for (int64_t e = threadIdx.x; e < n; e += 256) {
-    const int64_t r = e / K;
-    const int c = static_cast<int>(e - r * K);
-    const int32_t v = map[static_cast<int64_t>(order[row0 + r]) * K + c];
-    if (ordered) ordered[row0 * K + e] = v;
-    if (v >= 0 && c < 128) {
-      const int gi = r >= 128 ? 1 : 0;
-      if (c < 64) m[gi][0] |= uint64_t(1) << c;
-      else m[gi][1] |= uint64_t(1) << (c - 64);
+  if (ordered || reduce) {
+    for (int64_t e = threadIdx.x; e < n; e += 256) {
+      const int64_t r = e / K;
+      const int c = static_cast<int>(e - r * K);
+      const int32_t v = map[static_cast<int64_t>(src_s[r]) * K + c];
+      if (ordered) ordered[row0 * K + e] = v;
+      if (reduce && v >= 0 && c < 128) {
+        const int gi = r >= 128 ? 1 : 0;
+        if (c < 64) m[gi][0] |= uint64_t(1) << c;
+        else m[gi][1] |= uint64_t(1) << (c - 64);
+      }
     }
   }
   if (!gmask) return;
+  if (gm_in) {
+    if (threadIdx.x < 4) {
+      const int gi = threadIdx.x >> 1, w = threadIdx.x & 1;
+      const int64_t g = row0 / 128 + gi;
+      if (g * 128 < T) gmask[g * 2 + w] = gm_in[(gperm ? gperm[g] : g) * 2 + w];
+    }
+    return;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi)
@@ -490,14 +550,46 @@ __global__ __launch_bounds__(256) void order_rows_kernel(const int32_t *__restri
   }
 }
 
-static size_t row_order_parts(int64_t T, size_t *sort_bytes) {
-  size_t b = 0;
-  (void)rocprim::radix_sort_pairs(nullptr, b, static_cast<const uint64_t *>(nullptr),
+// Workspace of the row order: sort keys (in / out), row ids, sorted rows,
+// the group pass (unions, keys in / out, ids, permutation) and the larger of
+// the two sorts' temporary storage.
+struct RowOrderParts {
+  uint64_t *keys, *keys_out, *gm;
+  int32_t *iota, *sorted, *giota, *gperm;
+  uint32_t *gkey, *gkey_out;
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+static RowOrderParts row_order_parts(int64_t T, void *base) {
+  const int64_t G = (T + 127) / 128;
+  size_t b1 = 0, b2 = 0;
+  (void)rocprim::radix_sort_pairs(nullptr, b1, static_cast<const uint64_t *>(nullptr),
                                   static_cast<uint64_t *>(nullptr), static_cast<const int32_t *>(nullptr),
                                   static_cast<int32_t *>(nullptr), static_cast<size_t>(T), 0, 64);
-  *sort_bytes = b;
-  auto a = [](size_t x) { return (x + 255) / 256 * 256; };
-  return 2 * a(T * sizeof(uint64_t)) + a(T * sizeof(int32_t)) + a(b);
+  (void)rocprim::radix_sort_pairs(nullptr, b2, static_cast<const uint32_t *>(nullptr),
+                                  static_cast<uint32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
+                                  static_cast<int32_t *>(nullptr), static_cast<size_t>(G), 0, 8);
+  RowOrderParts r{};
+  r.tmp_bytes = std::max(b1, b2);
+  char *p = static_cast<char *>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char *q = p ? p + off : nullptr;
+    off += (bytes + 255) / 256 * 256;
+    return q;
+  };
+  r.keys = reinterpret_cast<uint64_t *>(take(T * sizeof(uint64_t)));
+  r.keys_out = reinterpret_cast<uint64_t *>(take(T * sizeof(uint64_t)));
+  r.iota = reinterpret_cast<int32_t *>(take(T * sizeof(int32_t)));
+  r.sorted = reinterpret_cast<int32_t *>(take(T * sizeof(int32_t)));
+  r.gm = reinterpret_cast<uint64_t *>(take(G * 2 * sizeof(uint64_t)));
+  r.gkey = reinterpret_cast<uint32_t *>(take(G * sizeof(uint32_t)));
+  r.gkey_out = reinterpret_cast<uint32_t *>(take(G * sizeof(uint32_t)));
+  r.giota = reinterpret_cast<int32_t *>(take(G * sizeof(int32_t)));
+  r.gperm = reinterpret_cast<int32_t *>(take(G * sizeof(int32_t)));
+  r.tmp = take(r.tmp_bytes);
+  r.total = off;
+  return r;
 }
 
 static size_t scan_temp_bytes(int64_t n) {
@@ -605,8 +697,7 @@ int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t strea
 }
 
 int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes) {
-  size_t sb = 0;
-  *bytes = num_targets <= 0 ? 0 : row_order_parts(num_targets, &sb);
+  *bytes = num_targets <= 0 ? 0 : row_order_parts(num_targets, nullptr).total;
   return kOk;
 }
 
@@ -617,30 +708,46 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
   SPIRA_HIP_REQUIRE(num_offsets >= 1, "kmap_row_order: no offsets");
   SPIRA_HIP_REQUIRE(group_masks == nullptr || num_offsets <= 128, "kmap_row_order: group masks need <= 128 offsets");
   if (num_targets == 0) return kOk;
-  size_t sb = 0;
-  const size_t need = row_order_parts(num_targets, &sb);
-  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= need, "kmap_row_order: workspace too small");
-  auto a = [](size_t x) { return (x + 255) / 256 * 256; };
-  char *p = static_cast<char *>(workspace);
-  uint64_t *keys = reinterpret_cast<uint64_t *>(p);
-  p += a(num_targets * sizeof(uint64_t));
-  uint64_t *keys_out = reinterpret_cast<uint64_t *>(p);
-  p += a(num_targets * sizeof(uint64_t));
-  int32_t *iota = reinterpret_cast<int32_t *>(p);
-  p += a(num_targets * sizeof(int32_t));
+  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= row_order_parts(num_targets, nullptr).total,
+                    "kmap_row_order: workspace too small");
+  RowOrderParts w = row_order_parts(num_targets, workspace);
   const int rb = num_offsets <= 32 ? 256 : 64;
   SPIRA_HIP_REQUIRE(static_cast<size_t>(rb) * num_offsets * sizeof(int32_t) <= 64 * 1024,
                     "kmap_row_order: at most 256 offsets");
   hipLaunchKernelGGL(row_mask_kernel, dim3(div_up(num_targets, rb)), dim3(256), rb * num_offsets * sizeof(int32_t),
-                     stream, out_in_map, num_targets, num_offsets, rb, keys, iota);
+                     stream, out_in_map, num_targets, num_offsets, rb, w.keys, w.iota);
   SPIRA_HIP_LAUNCH_CHECK();
-  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, sb, keys, keys_out, iota, order, static_cast<size_t>(num_targets), 0,
-                                          row_key_bits(num_offsets), stream));
-  if (ordered_map || group_masks) {
-    hipLaunchKernelGGL(order_rows_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, order,
-                       num_targets, num_offsets, ordered_map, group_masks);
+  size_t tb = w.tmp_bytes;
+  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, w.keys, w.keys_out, w.iota, w.sorted,
+                                          static_cast<size_t>(num_targets), 0, row_key_bits(num_offsets), stream));
+  const int64_t G = div_up(num_targets, 128);
+  const int32_t *gperm = nullptr;
+  const uint64_t *gm = nullptr;
+  if (group_masks) {
+    // group unions, then the groups with the most columns first: the
+    // densest blocks start first and lead the grid, where the conv kernel
+    // lets them split
+    const bool from_keys = num_offsets <= 57;  // the sort keys hold the whole column mask
+    if (!from_keys) {
+      hipLaunchKernelGGL(order_rows_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map,
+                         w.sorted, static_cast<const int32_t *>(nullptr), num_targets, num_offsets,
+                         static_cast<int32_t *>(nullptr), static_cast<int32_t *>(nullptr),
+                         static_cast<const uint64_t *>(nullptr), w.gm);
+      SPIRA_HIP_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(group_union_keys_kernel, dim3(div_up(G, 4)), dim3(256), 0, stream,
+                       from_keys ? w.keys_out : static_cast<const uint64_t *>(nullptr), num_offsets, num_targets,
+                       w.gm, w.gkey, w.giota);
     SPIRA_HIP_LAUNCH_CHECK();
+    tb = w.tmp_bytes;
+    SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, w.gkey, w.gkey_out, w.giota, w.gperm, static_cast<size_t>(G),
+                                            0, 8, stream));
+    gperm = w.gperm;
+    gm = w.gm;
   }
+  hipLaunchKernelGGL(order_rows_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, w.sorted,
+                     gperm, num_targets, num_offsets, order, ordered_map, gm, group_masks);
+  SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }
 

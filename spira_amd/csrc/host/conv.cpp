@@ -146,6 +146,17 @@ static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
   return cache.emplace(key, std::move(e)).first->second;
 }
 
+// The row order of an output-stationary map as the fp16 kernel uses it:
+// (order, group masks as int64 [ceil(T / 128) * 2], ordered map).  No
+// reference counterpart: exposed for tests.
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> kmap_row_order(const torch::Tensor &map, int64_t T) {
+  require_device(map, "out_in_map");
+  SPIRA_CHECK_ARG(map.dim() == 2 && map.scalar_type() == torch::kInt32 && map.size(0) >= T,
+                  "out_in_map must be int32 [>= T, K]");
+  const OrderEntry &e = row_order_of(map, T);
+  return {e.order.narrow(0, 0, T), e.masks, e.ordered_map.narrow(0, 0, T)};
+}
+
 static void check_features(const torch::Tensor &X, const torch::Tensor &W) {
   SPIRA_CHECK_ARG(X.dim() == 2, "sources must be [N, C_in]");
   SPIRA_CHECK_ARG(W.dim() == 3, "weights must be [K, C_in, C_out]");
@@ -191,6 +202,21 @@ static Epi epi_of(const std::optional<torch::Tensor> &scale, const std::optional
   return e;
 }
 
+// The output-stationary workspace holds fp32 accumulators that every call
+// leaves zeroed; one zero-filled buffer per (device, stream) is kept and
+// grown (calls on one stream run in order, so they share it safely).
+static torch::Tensor zeroed_workspace(size_t bytes, const torch::Device &dev) {
+  static std::unordered_map<uint64_t, torch::Tensor> pool;
+  if (bytes == 0) return torch::Tensor();
+  const hipStream_t s = current_stream();
+  const uint64_t key = (reinterpret_cast<uint64_t>(s) << 8) ^ static_cast<uint64_t>(dev.index() & 0xff);
+  auto &t = pool[key];
+  if (!t.defined() || static_cast<size_t>(t.numel()) < bytes)
+    t = torch::zeros({static_cast<int64_t>((bytes + 255) / 256 * 256)},
+                     torch::TensorOptions(dev).dtype(torch::kUInt8));
+  return t;
+}
+
 static bool epi_empty(const Epi &e) { return !e.scale && !e.shift && !e.residual && !e.relu; }
 
 static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
@@ -211,7 +237,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto P = prepared_weights(W);
   size_t wsb = 0;
   check_rc(spira_hip_conv_os_workspace(T, K, W.size(1), W.size(2), dtype, mode, &wsb), "conv_os");
-  auto ws = workspace(wsb, dev);
+  auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
   if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128) {
@@ -221,7 +247,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
     mp = oe.ordered_map.data_ptr<int32_t>();
   }
   check_rc(spira_hip_conv_os(T, K, mp, order, masks, X.data_ptr(), S, W.size(1), wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
-                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, ws.data_ptr(), wsb,
+                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, ws.defined() ? ws.data_ptr() : nullptr, wsb,
                              current_stream()),
            "sparse_convolution_forward_os");
 }
@@ -568,6 +594,7 @@ void register_conv(pybind11::module_ &m) {
   m.def("cuda_free_buffers", &free_buffers);
   m.def("cuda_reset_error", &reset_error);
   m.def("set_os_row_order", &set_row_order);
+  m.def("kmap_row_order", &kmap_row_order);
 }
 
 }  // namespace spira_host

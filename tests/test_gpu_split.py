@@ -1,0 +1,117 @@
+"""Offset splitting of the output-stationary kernel on a 200k-voxel scene
+(row-ordered: its densest leading row blocks run as several workgroups whose
+fp32 partial tiles the last one sums) and on small layers (every block
+splits).  Checked against the float64 oracle on every row; tolerance
+max |error| <= 1e-2 * RMS(reference) for fp16 storage."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from spira_amd import scenes
+from spira_amd.nn import functional as F
+
+from helpers import np_, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def indoor():
+    k, _ = orc.flatten_sort(scenes.indoor(), True)
+    m = orc.build_kmap(k, k, (3, 3, 3), (1, 1, 1), 0)[2]
+    return k, m
+
+
+def _case(S, cin, cout, dev, seed):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(S, cin, generator=g).half()
+    W = (torch.randn(27, cin, cout, generator=g) / np.sqrt(27 * cin)).half()
+    return X, W
+
+
+@pytest.mark.parametrize("cin,cout", [(32, 32), (96, 96), (64, 128), (128, 256)])
+def test_ordered_layer_splits(dev, indoor, cin, cout):
+    k, m = indoor
+    S = T = len(k)
+    X, W = _case(S, cin, cout, dev, seed=cin + cout)
+    md = torch.from_numpy(m).to(dev)
+    y = np_(F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev)).float())
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(y, ref) <= 1e-2
+    # two calls in a row give the same result up to the fp32 summation order
+    y2 = np_(F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev)).float())
+    assert rel_err(y2, y) <= 1e-2
+
+
+def test_ordered_layer_epilogue(dev, indoor):
+    k, m = indoor
+    S = T = len(k)
+    cin = cout = 96
+    X, W = _case(S, cin, cout, dev, seed=5)
+    g = torch.Generator().manual_seed(6)
+    scale = 0.5 + torch.rand(cout, generator=g)
+    shift = 0.1 * torch.randn(cout, generator=g)
+    res = torch.randn(T, cout, generator=g).half()
+    md = torch.from_numpy(m).to(dev)
+    y = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev),
+                                        epilogue=(scale.to(dev), shift.to(dev), res.to(dev), True))
+    conv = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    ref = np.maximum(conv * scale.double().numpy() + shift.double().numpy() + res.double().numpy(), 0)
+    assert rel_err(np_(y.float()), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("T,cin,cout", [(300, 64, 64), (2000, 32, 96), (5000, 256, 256), (40, 3, 16)])
+def test_small_layer_splits(dev, T, cin, cout):
+    c = scenes.spheres_planes(n=T, grid=32, seed=T)
+    k, _ = orc.flatten_sort(c, True)
+    T = S = len(k)
+    m = orc.build_kmap(k, k, (3, 3, 3), (1, 1, 1), 0)[2]
+    X, W = _case(S, cin, cout, dev, seed=T)
+    y = F.sparse_convolution_forward_os(S, T, torch.from_numpy(m).to(dev), X.to(dev), W.to(dev))
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(np_(y.float()), ref) <= 1e-2
+
+
+def _check_row_order(m, T, order, masks, omap):
+    K = m.shape[1]
+    valid = m[:T] >= 0
+    # a permutation of the targets, and the map rows in that order
+    assert np.array_equal(np.sort(order), np.arange(T))
+    assert np.array_equal(omap, m[order])
+    # group masks: the valid-column union of every 128 ordered rows
+    G = (T + 127) // 128
+    v = np.zeros((G * 128, K), bool)
+    v[:T] = valid[order]
+    union = v.reshape(G, 128, K).any(1)
+    bits = np.zeros((G, 128), bool)
+    bits[:, :K] = union
+    words = np.packbits(bits.reshape(G, 2, 64)[:, :, ::-1], axis=2, bitorder="big").view(">u8")[:, :, 0]
+    assert np.array_equal(masks.view(np.uint64).reshape(G, 2), words.astype(np.uint64))
+    # full groups by union size, most columns first; the partial group last
+    pc = union.sum(1)
+    full = G if T % 128 == 0 else G - 1
+    assert np.all(np.diff(pc[:full]) <= 0)
+    # inside a group the rows run by neighbour count (most first), then column pattern
+    cnt = valid[order].sum(1)
+    for g in range(G):
+        c = cnt[g * 128:(g + 1) * 128]
+        assert np.all(np.diff(c) <= 0)
+
+
+def test_row_order_k3(dev, indoor):
+    from spira_amd.nn.functional._native import _C
+    k, m = indoor
+    T = len(k)
+    order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(m).to(dev), T))
+    _check_row_order(m, T, order, masks, omap)
+
+
+def test_row_order_k5(dev):
+    from spira_amd.nn.functional._native import _C
+    c = scenes.spheres_planes(n=20000, grid=64, seed=3)
+    k, _ = orc.flatten_sort(c, True)
+    T = len(k) - 77  # a partial last group
+    m = orc.build_kmap(k, k, (5, 5, 5), (1, 1, 1), 0)[2]
+    order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(m).to(dev), T))
+    _check_row_order(m, T, order, masks, omap)
