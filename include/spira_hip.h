@@ -157,12 +157,11 @@ int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int d
 int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, int c_out, int dtype, void *prepared,
                               hipStream_t stream);
 
-/* Workspace bytes of spira_hip_conv_os: fp32 accumulators for the blocks
- * whose offsets are split over several workgroups (small layers; the
- * densest leading blocks of a row-ordered layer).  The workspace must be
- * zero-filled before its first use; every call leaves it zero-filled, so a
- * caller keeps one buffer per stream (calls that overlap on one buffer
- * race). */
+/* Workspace bytes of spira_hip_conv_os: an fp32 [num_targets, c_out]
+ * partial-sum buffer when a small layer (fewer row blocks than CUs) splits
+ * its offsets over blocks.  The workspace must be zero-filled before its
+ * first use; every call leaves it zero-filled, so a caller keeps one buffer
+ * per stream (calls that overlap on one buffer race). */
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
                                 size_t *bytes);
 

@@ -10,12 +10,16 @@
 //
 // MI355X design (fp16 storage, fp32 accumulation on v_mfma_f32_32x32x16_f16).
 // All three dataflows share one MMA core:
-//  * a block is 4 waves; a wave owns MT tiles of 32 rows x 32*WN columns
-//    (MT*WN accumulators of 16 floats); WN = 1, 2, 3, 4 or 8 so that 96- and
-//    256-channel layers do not pad to a power of two;
-//  * the K dimension is walked in steps of 32 input channels of one kernel
-//    offset.  The offset's weight chunk (shared by the four waves) lands in a
-//    3-stage LDS ring through global_load_lds_dwordx4 (direct HBM/L2 -> LDS)
+//  * a block is 4 waves; a wave owns a tile of 32 rows x 32*WN columns (WN
+//    accumulators of 16 floats); WN = 1, 2, 3 or 4 (wider layers take
+//    several 128-column tiles), so that 96-channel layers do not pad to a
+//    power of two.  The tiles are small on purpose: the kernels are bound by
+//    latency, not by any one unit, and small tiles let 3-4 waves share each
+//    SIMD;
+//  * the K dimension is walked in steps of 32 or 64 input channels of one
+//    kernel offset.  The offset's weight chunk (shared by the four waves)
+//    lands in a 2-4 stage LDS ring through global_load_lds_dwordx4 (direct
+//    HBM/L2 -> LDS)
 //    with an XOR swizzle that makes the B reads conflict-free; the gathered
 //    rows (private to a wave) are loaded straight into the registers of the
 //    MFMA A operand (lane L fetches exactly the 16 bytes its A slot needs).
@@ -27,19 +31,14 @@
 //    channel counts (the 3-channel stem) take the same path;
 //  * the output-stationary kernel can walk its rows in neighbour-mask order
 //    (rows with the same neighbour pattern together) and visits only the
-//    offsets some row of the block uses.  A block with many steps splits its
-//    offsets over several workgroups (small layers: every block, so that the
-//    grid covers the chip; row-ordered layers: the densest leading blocks,
-//    which would otherwise outlast the rest of the grid); the splits store
-//    fp32 partial tiles and the last one to finish sums them and writes the
-//    output (no fill or finalize pass);
+//    offsets some row of the block uses; small layers split the offsets over
+//    blocks (fp32 atomics into a workspace that stays zeroed + finalize);
 //  * an optional epilogue folds a per-channel scale / shift (eval-mode batch
 //    norm), a residual add and ReLU into the output write.
 #include "common.hpp"
 #include "../../../include/spira_hip.h"
 
 #include <algorithm>
-#include <atomic>
 #include <cstdlib>
 #include <utility>
 #include <vector>
@@ -64,26 +63,6 @@ struct Epilogue {
   int relu;
 };
 
-// Offset splitting of the output-stationary kernel.  Row blocks b < hb may
-// split: block b runs as up to zs workgroups (linear ids z*hb + b, all
-// among the first hb*zs ids so that they start early), each taking an
-// equal share of the block's active offsets, ceil(steps / tgt) of them at
-// most.  Each split adds its fp32 tile atomically into the accumulator
-// part[b*ny + y] and takes a ticket; the last one reads the sum, clears the
-// accumulator and writes the output.  The accumulators (caller workspace)
-// start zeroed and are left zeroed.  Tickets live in kTicketSlots rotating
-// sets of a device array that starts zeroed and is left zeroed (the last
-// split resets its ticket); `tslot` picks the set, so that up to
-// kTicketSlots calls can be in flight at once.  Blocks b >= hb run as one
-// workgroup each.
-struct Split {
-  int hb, zs, tgt, ny, tslot;
-  float *part;
-};
-constexpr int kTicketSlots = 64;
-constexpr int kTicketsPerSlot = 4096;  // >= hb * ny
-__device__ int32_t g_split_tickets[kTicketSlots * kTicketsPerSlot];
-
 // Gathered operands of the MMA core.  Both are addressed through buffer
 // resources with 32-bit byte offsets: a lane whose row is missing (or whose
 // channels lie in the padding) uses an offset past the end, and the buffer
@@ -101,6 +80,19 @@ constexpr int kRsrcWord3 = 0x00020000;         // raw (untyped) buffer, 32-bit d
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), kRsrcWord3);
 }
+
+#ifdef SPIRA_BLOCK_TIMING
+// experiment builds only: per-step cycle stamps of wave 0 of a few blocks
+__device__ int64_t g_step_times[8 * 64 * 4];
+#define SPIRA_STEP_STAMP(step, ph)                                                            \
+  {                                                                                           \
+    const int sel_ = (blockIdx.x % 97 == 0 && blockIdx.x / 97 < 8) ? blockIdx.x / 97 : -1;    \
+    if (sel_ >= 0 && threadIdx.x == 0 && (step) >= 0 && (step) < 64)                                       \
+      g_step_times[(sel_ * 64 + (step)) * 4 + (ph)] = __builtin_amdgcn_s_memtime();           \
+  }
+#else
+#define SPIRA_STEP_STAMP(step, ph)
+#endif
 
 namespace ring {
 
@@ -125,7 +117,9 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int STAGE = B_BYTES;
   static constexpr int RING = NS * STAGE;
   static constexpr int OUT_STAGE = BM * (BN + 8) * 2;  // fp16 output tile staged by the epilogue
-  static constexpr int LDS = RING > OUT_STAGE ? RING : OUT_STAGE;
+  static constexpr int MAP_TILE_K = 27;                 // map columns held in LDS (kernels of <= 27 offsets)
+  static constexpr int MAP_TILE = BM * MAP_TILE_K * 4;  // the block's map rows, after the ring
+  static constexpr int LDS = RING + MAP_TILE > OUT_STAGE ? RING + MAP_TILE : OUT_STAGE;
   static constexpr int LPS = MT * NKS + BVEC;  // vector-memory loads per wave and step
   static_assert(NKS == 2 || NKS == 4, "a step is 32 or 64 channels");
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
@@ -136,12 +130,14 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   __host__ __device__ static constexpr int swz(int n) { return NKS == 2 ? (n >> 2) & 3 : n & 7; }
 };
 
-// Tile shape per column-tile width and step: MT 32-row tiles per wave and
-// the ring depth, sized so that two blocks (eight waves, <= 256 VGPRs each)
-// fit a CU's 160 KiB of LDS.
+// Tile shape per column-tile width and step: one 32-row tile per wave (the
+// kernels are latency-bound: more resident waves beat larger wave tiles),
+// the ring depth, and the waves per SIMD the register budget targets: 4 for
+// up to 96 columns (<= 128 VGPRs, four 40 KiB blocks per CU), 3 for 128.
 template <int WN, int NKS = 2> struct TileOf {
-  static constexpr int MT = WN >= 8 ? 1 : (WN >= 3 ? 2 : 1);
+  static constexpr int MT = 1;
   static constexpr int NS = NKS == 2 ? (WN >= 3 ? 3 : 4) : (WN >= 3 ? 2 : 3);
+  static constexpr int WAVES = WN <= 3 ? 4 : 3;
   using C = Cfg<WN, MT, NS, NKS>;
 };
 
@@ -331,10 +327,14 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
     unroll<NS>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int slot = (i + NS - 1) % NS;
+      SPIRA_STEP_STAMP(s + i, 0);
       wait_vm<(NS - 2) * C::LPS + (NS - 1) * PL>();
+      SPIRA_STEP_STAMP(s + i, 1);
       __builtin_amdgcn_s_barrier();
+      SPIRA_STEP_STAMP(s + i, 2);
       put(s + i + NS - 1, std::integral_constant<int, slot>{});
       fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
+      SPIRA_STEP_STAMP(s + i, 3);
       compute<C, i>(acc, rb, areg[i]);
     });
   }
@@ -489,24 +489,22 @@ __device__ int64_t g_block_times[1 << 20];
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
 template <int WN, int MODE, bool ALIGNED, int NKS>
-__global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ map,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
-                                                    Split sp, Operands op, void *Y, Epilogue epi) {
+                                                    Operands op, void *Y, Epilogue epi) {
   using C = typename ring::TileOf<WN, NKS>::C;
   constexpr int MT = C::BM / 128, NS = C::NS;
   __shared__ __align__(1024) char ring_lds[C::LDS];
-  __shared__ __align__(16) int32_t idx_lds[NS][256];  // map entries of a later step, per stage
-  __shared__ int32_t orow_s[4][32 * MT];
+  // map entries of a later step, per stage (untiled maps; the map tile's place)
+  int32_t(*idx_lds)[256] = reinterpret_cast<int32_t(*)[256]>(ring_lds + C::RING);
+  static_assert(NS * 256 * 4 <= C::MAP_TILE, "index slots exceed the map tile");
+  // output row per tile row (epilogue); 64 per wave so that during the
+  // step loop a wave's dummy map fetches (tiled maps) can land here
+  __shared__ int32_t orow_s[4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, kh = lane >> 5;
-  // linear block id -> (row block, split): split z of block b < hb is id
-  // z * hb + b (consecutive ids go to different XCDs, so neither the dense
-  // leading blocks nor the splits of one block gather on a few XCDs)
-  const int lb = blockIdx.x;
-  const int rb_ = lb < sp.hb * sp.zs ? lb % sp.hb : lb - sp.hb * (sp.zs - 1);
-  const int z = lb < sp.hb * sp.zs ? lb / sp.hb : 0;
-  const int64_t row0 = static_cast<int64_t>(rb_) * C::BM;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * C::BM;
   const int n0 = blockIdx.y * C::BN;
   const int j0 = blockIdx.z * jper;
   const int jn = ((j0 + jper) < Kc ? (j0 + jper) : Kc) - j0;
@@ -530,30 +528,8 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
     ulo &= slo;
     uhi &= shi;
   }
-  int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
+  const int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
   const int nch = (op.CinP + C::KC - 1) / C::KC;
-  int nsp = 1;  // splits of this block
-  if (rb_ < sp.hb) {
-    nsp = (nact * nch + sp.tgt - 1) / sp.tgt;
-    nsp = nsp < 1 ? 1 : (nsp > sp.zs ? sp.zs : nsp);
-    if (nsp > nact) nsp = nact > 0 ? nact : 1;
-  }
-  if (z >= nsp) {  // block-uniform
-#ifdef SPIRA_BLOCK_TIMING
-    SPIRA_STAMP(2);
-    if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = -1;
-#endif
-    return;
-  }
-  if (nsp > 1) {
-    // this split: active offsets [a0, a1) in increasing order
-    const int a0 = z * nact / nsp, a1 = (z + 1) * nact / nsp;
-    for (int i = 0; i < a0; ++i) {
-      if (ulo) ulo &= ulo - 1;
-      else uhi &= uhi - 1;
-    }
-    nact = a1 - a0;  // the step iterators stop after nact offsets
-  }
   const int nsteps = nact * nch;
   SPIRA_STAMP(1);
 
@@ -562,12 +538,17 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   bool mvalid[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) mvalid[m] = row0 + wave * 32 * MT + m * 32 + r < T;
-  // Map entries of step u: lane L of a wave fetches row L (MT = 2) or row
-  // L % 32 (MT = 1) of the wave's rows into the stage's index slot; rows past
-  // T read nothing (out of range) and are masked when resolved.
-  // No map: the identity (logical row i reads source i); the fetches then
-  // load nothing (out of range) but keep the vmcnt arithmetic.
+  // Map entries.  Kernels of at most 27 offsets: the block's BM map rows are
+  // copied into LDS once (row stride KP = Kc | 1 words, odd, so that the
+  // per-row reads of one column are conflict-free) and every step reads its
+  // column there.  Larger kernels: lane L of a wave fetches the entry of row
+  // L (MT = 2) or L % 32 (MT = 1) of the wave's rows for step u into the
+  // stage's index slot, NS steps ahead.  Rows past T read nothing (out of
+  // range) and are masked when resolved.  No map: the identity (logical row
+  // i reads source i); the fetches then load nothing (out of range) but keep
+  // the vmcnt arithmetic.
   const bool ident = map == nullptr;
+  const bool tiled = !ident && Kc <= C::MAP_TILE_K;
   const int frow = MT == 2 ? lane : r;
   const int64_t flr = row0 + wave * 32 * MT + frow;
   const uint32_t fbase = (flr < T && !ident) ? static_cast<uint32_t>(flr * Kc + j0) * 4u : kOutOfRange;
@@ -578,18 +559,48 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
   fit.init(ulo, uhi);
   pit = fit;
   int fu = 0;
+  const int KP = Kc | 1;
+  int32_t *tile = reinterpret_cast<int32_t *>(ring_lds + C::RING);
+  if (tiled) {
+    // slot s = round * 256 + tid holds element (row0 + s / KP, s % KP)
+    int rr = tid / KP, cc = tid - rr * KP;
+    const int drow = 256 / KP, dcol = 256 - drow * KP;
+    const int rounds = (C::BM * KP + 255) / 256;
+    for (int i = 0; i < rounds; ++i) {
+      const int64_t grow = row0 + rr;
+      const uint32_t off = (cc < Kc && grow < T) ? static_cast<uint32_t>(grow * Kc + cc) * 4u : kOutOfRange;
+      ring::dma4(mr, off, tile + i * 256 + uwave * 64);
+      rr += drow;
+      cc += dcol;
+      if (cc >= KP) {
+        cc -= KP;
+        ++rr;
+      }
+    }
+    ring::wait_vm<0>();
+    __syncthreads();
+  }
+  const uint32_t tbase = ring::lds_addr(tile) + ((wave * 32 * MT + r) * KP + j0) * 4;
   auto fetch = [&](int u, auto St) {
     (void)u;
-    const uint32_t off = (fbase == kOutOfRange || fu >= nsteps) ? kOutOfRange : fbase + fit.j * 4u;
-    ring::dma4(mr, off, &idx_lds[decltype(St)::value][uwave * 64]);
+    // (tiled: an out-of-range fetch that only keeps the vmcnt arithmetic)
+    const uint32_t off = (tiled || fbase == kOutOfRange || fu >= nsteps) ? kOutOfRange : fbase + fit.j * 4u;
+    ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value][uwave * 64]);
     ++fu;
     fit.step(nch);
   };
   auto resolve = [&](int u, auto St, int32_t (&idx)[MT], int &wrow, int &kb) {
     (void)u;
-    ring::unroll<MT>([&](auto M) {
-      idx[decltype(M)::value] = ring::rd4<decltype(St)::value * 1024 + decltype(M)::value * 128>(ibase);
-    });
+    if (tiled) {
+      const uint32_t col = static_cast<uint32_t>(pit.j) * 4u;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        asm volatile("ds_read_b32 %0, %1" : "=v"(idx[m]) : "v"(tbase + m * 32 * KP * 4 + col) : "memory");
+    } else {
+      ring::unroll<MT>([&](auto M) {
+        idx[decltype(M)::value] = ring::rd4<decltype(St)::value * 1024 + decltype(M)::value * 128>(ibase);
+      });
+    }
     ring::lds_wait();
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -606,40 +617,6 @@ __global__ __launch_bounds__(256, 2) void os_kernel(const int32_t *__restrict__ 
 #ifdef SPIRA_BLOCK_TIMING
   if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = nact;
 #endif
-  if (nsp > 1) {
-    // add this split's tile into the block's accumulator (element-major:
-    // element i of accumulator (m, wn) of a wave is 64 consecutive floats,
-    // one per lane), take a ticket; the last split reads the sum
-    const int64_t tile = static_cast<int64_t>(C::BM) * C::BN;
-    float *slot = sp.part + (static_cast<int64_t>(rb_) * sp.ny + blockIdx.y) * tile + wave * (MT * WN * 1024) + lane;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int wn = 0; wn < WN; ++wn)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          __hip_atomic_fetch_add(slot + ((m * WN + wn) * 16 + i) * 64, acc[m][wn][i], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // the adds have been performed
-    __syncthreads();
-    __shared__ int last_s;
-    int32_t *ticket = &g_split_tickets[sp.tslot * kTicketsPerSlot + rb_ * sp.ny + blockIdx.y];
-    if (tid == 0)
-      last_s = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
-    __syncthreads();
-    if (!last_s) return;  // block-uniform
-    if (tid == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int wn = 0; wn < WN; ++wn)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float *q = slot + ((m * WN + wn) * 16 + i) * 64;
-          acc[m][wn][i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(q, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-  }
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -981,12 +958,14 @@ static inline bool mfma_path(int dtype) { return dtype == SPIRA_F16; }
 static inline int pad_in(int c) { return static_cast<int>(round_up(c, 16)); }
 static inline int pad_out(int c) { return static_cast<int>(round_up(c, 32)); }
 
+// column-tile width (x 32 columns): wider layers take several 128-column
+// tiles (more, shorter blocks; a 256-column tile would halve the resident
+// waves for the same work)
 static inline int wn_for(int Cout) {
   if (Cout <= 32) return 1;
   if (Cout <= 64) return 2;
   if (Cout <= 96) return 3;
-  if (Cout <= 128) return 4;
-  return 8;
+  return 4;
 }
 // rows per block of the MMA kernels for a column-tile width
 static inline int bm_for(int wn) {
@@ -994,8 +973,7 @@ static inline int bm_for(int wn) {
     case 1: return ring::TileOf<1>::C::BM;
     case 2: return ring::TileOf<2>::C::BM;
     case 3: return ring::TileOf<3>::C::BM;
-    case 4: return ring::TileOf<4>::C::BM;
-    default: return ring::TileOf<8>::C::BM;
+    default: return ring::TileOf<4>::C::BM;
   }
 }
 
@@ -1012,62 +990,9 @@ static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
   return std::min(jper, 128);
 }
 
-// Offset-split plan of an output-stationary launch (Kc <= 128): row-ordered
-// layers with 256-column tiles let their densest leading blocks (the order
-// puts the groups with the most neighbour offsets first) split into pieces
-// of about `tgt` steps.  (Small layers split by static offset ranges
-// instead, small_layer_jper; narrower tiles gain nothing from the split.)
-// Overrides for measurements: SPIRA_OS_SPLIT=0 disables,
-// SPIRA_OS_SPLIT_HB / _ZS / _TGT / _MIN_BN, SPIRA_OS_SMALL_TICKET=1 splits
-// small layers this way too.
-struct SplitPlan {
-  int hb = 0, zs = 1, tgt = 1 << 30, ny = 1;
-  size_t bytes = 0;  // fp32 partial tiles
-};
 static int env_int(const char *name, int dflt) {
   const char *v = std::getenv(name);
   return v && *v ? std::atoi(v) : dflt;
-}
-static SplitPlan plan_split(int64_t bx, int64_t by, int bm, int bn, int Kc, int CinP, int kc, bool ordered,
-                            int cus) {
-  SplitPlan p;
-  p.ny = static_cast<int>(by);
-  static const int enabled = env_int("SPIRA_OS_SPLIT", 1);
-  if (!enabled || Kc > 128 || Kc < 2) return p;
-  const int nch = div_up(CinP, kc);
-  int hb = 0, zs = 1, tgt = 1 << 30;
-  static const int small_ticket = env_int("SPIRA_OS_SMALL_TICKET", 0);
-  static const int min_bn = env_int("SPIRA_OS_SPLIT_MIN_BN", 256);
-  if (bx * by < cus) {
-    if (!small_ticket) return p;  // small layers: static offset ranges (small_layer_jper)
-    hb = static_cast<int>(bx);
-    zs = static_cast<int>(std::min<int64_t>(std::min(Kc, 16), div_up(2 * cus, bx * by)));
-    tgt = nch;
-  } else if (ordered && bn >= min_bn) {
-    hb = static_cast<int>(std::min<int64_t>(bx, env_int("SPIRA_OS_SPLIT_HB", 128)));
-    zs = env_int("SPIRA_OS_SPLIT_ZS", 4);
-    tgt = env_int("SPIRA_OS_SPLIT_TGT", std::max(24, 8 * nch) * 32 / kc);
-  }
-  if (hb * by > kTicketsPerSlot) hb = static_cast<int>(kTicketsPerSlot / by);
-  if (hb <= 0 || zs <= 1) return p;
-  p.hb = hb;
-  p.zs = zs;
-  p.tgt = std::max(1, tgt);
-  p.bytes = static_cast<size_t>(hb) * by * bm * bn * sizeof(float);
-  return p;
-}
-// Offsets per grid-z split: static offset ranges (fp32 atomics + a finalize
-// pass) for layers of more than 128 offsets and for small layers (fewer
-// blocks than CUs), unless the latter split per block
-static int small_layer_jper(int64_t blocks_xy, int Kc, int cus) {
-  static const int small_ticket = env_int("SPIRA_OS_SMALL_TICKET", 0);
-  static const int enabled = env_int("SPIRA_OS_SPLIT", 1);
-  if (Kc > 128 || (blocks_xy < cus && !(small_ticket && enabled))) return choose_jper(blocks_xy, Kc, cus);
-  return Kc;
-}
-static int next_ticket_slot() {
-  static std::atomic<int> n{0};
-  return n.fetch_add(1, std::memory_order_relaxed) % kTicketSlots;
 }
 
 // Operands of the MMA core; byte sizes must fit the 31-bit buffer offsets
@@ -1092,17 +1017,16 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
     case 1: CALL(1); break;       \
     case 2: CALL(2); break;       \
     case 3: CALL(3); break;       \
-    case 4: CALL(4); break;       \
-    default: CALL(8); break;      \
+    default: CALL(4); break;      \
   }
 
 template <int MODE, bool AL, int NKS>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const Split &sp, const Operands &op,
+                      const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                       void *Y, const Epilogue &epi) {
 #define SPIRA_OS_CALL(W)                                                                                         \
   hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
-                     jper, sp, op, Y, epi)
+                     jper, op, Y, epi)
   SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
 #undef SPIRA_OS_CALL
 }
@@ -1119,11 +1043,11 @@ static int os_nks(int CinP) {
 
 template <int MODE>
 static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const Split &sp,
-                          const Operands &op, void *Y, const Epilogue &epi) {
-  if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, sp, op, Y, epi);
-  else if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, sp, op, Y, epi);
-  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, sp, op, Y, epi);
+                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
+                          void *Y, const Epilogue &epi) {
+  if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  else if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
 }
 
 template <bool AL>
@@ -1191,6 +1115,9 @@ extern "C" {
 int spira_hip_debug_block_times(int64_t *out, int n) {
   return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_block_times), sizeof(int64_t) * n) == hipSuccess ? 0 : 1;
 }
+int spira_hip_debug_step_times(int64_t *out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_step_times), sizeof(int64_t) * 8 * 64 * 4) == hipSuccess ? 0 : 1;
+}
 #endif
 
 int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes) {
@@ -1213,21 +1140,14 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
 
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
                                 size_t *bytes) {
+  (void)c_in;
   *bytes = 0;
-  if (!mfma_path(dtype) || num_targets <= 0) return kOk;
-  if (num_offsets > 128 && out_mode != SPIRA_OUT_STORE) return kOk;
+  if (!mfma_path(dtype) || out_mode != SPIRA_OUT_STORE || num_targets <= 0) return kOk;
   const int wn = wn_for(c_out);
   const int bm = bm_for(wn);
-  const int64_t bx = div_up(num_targets, bm), by = div_up(pad_out(c_out), 32 * wn);
-  const int cus = device_cu_count();
-  if (small_layer_jper(bx * by, num_offsets, cus) < num_offsets) {
-    if (out_mode == SPIRA_OUT_STORE) *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
-  } else {
-    // the larger of the plans with and without a row order
-    for (bool ordered : {false, true})
-      *bytes = std::max(*bytes, plan_split(bx, by, bm, 32 * wn, num_offsets, pad_in(c_in),
-                                                    c_in % 8 ? 32 : 16 * os_nks(pad_in(c_in)), ordered, cus).bytes);
-  }
+  const int64_t blocks = div_up(num_targets, bm) * div_up(pad_out(c_out), 32 * wn);
+  if (choose_jper(blocks, num_offsets, device_cu_count()) < num_offsets)
+    *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
   return kOk;
 }
 
@@ -1252,21 +1172,10 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     const int wn = wn_for(c_out);
     const int bm = bm_for(wn);
     const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
-    const int cus = device_cu_count();
-    const int jper = small_layer_jper(bx * by, num_offsets, cus);
+    // small layers (fewer blocks than CUs) split their offsets over grid z
+    const int jper = choose_jper(bx * by, num_offsets, device_cu_count());
     const int splits = static_cast<int>(div_up(num_offsets, jper));
-    Split sp{0, 1, 1 << 30, static_cast<int>(by), 0, nullptr};
-    if (splits == 1) {
-      const SplitPlan pl = plan_split(bx, by, bm, 32 * wn, num_offsets, CinP,
-                                        c_in % 8 ? 32 : 16 * os_nks(CinP), group_masks != nullptr, cus);
-      if (pl.hb > 0) {
-        SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= pl.bytes,
-                          "conv_os: workspace too small (spira_hip_conv_os_workspace)");
-        sp = Split{pl.hb, pl.zs, pl.tgt, pl.ny, next_ticket_slot(), static_cast<float *>(workspace)};
-      }
-    }
-    dim3 grid(static_cast<unsigned>(bx + static_cast<int64_t>(sp.hb) * (sp.zs - 1)), static_cast<unsigned>(by),
-              static_cast<unsigned>(splits));
+    dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(by), static_cast<unsigned>(splits));
     SPIRA_HIP_REQUIRE(num_targets * num_offsets * 4 < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
     // (out_in_map may be null: the identity map, handled in the kernel)
     Operands op;
@@ -1274,11 +1183,11 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     if (rc0) return rc0;
     if (splits == 1) {
       if (out_mode == SPIRA_OUT_STORE)
-        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, targets, epi);
+        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
       else if (out_mode == SPIRA_OUT_STORE_F32)
-        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, targets, epi);
+        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
       else
-        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, targets, epi);
+        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
     } else {
       float *acc = nullptr;
       if (out_mode == SPIRA_OUT_STORE) {
@@ -1293,7 +1202,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
         int rc = fill_f32(acc, num_targets * c_out, 0.f, stream);
         if (rc) return rc;
       }
-      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, sp, op, acc, epi);
+      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, acc, epi);
       SPIRA_HIP_LAUNCH_CHECK();
       if (out_mode == SPIRA_OUT_STORE)
         hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(num_targets * c_out, 256)), dim3(256), 0, stream,

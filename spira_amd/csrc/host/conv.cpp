@@ -236,7 +236,8 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   }
   auto P = prepared_weights(W);
   size_t wsb = 0;
-  check_rc(spira_hip_conv_os_workspace(T, K, W.size(1), W.size(2), dtype, mode, &wsb), "conv_os");
+  const int64_t cin_run = (dtype == SPIRA_F16 && W.size(1) % 8 != 0) ? (W.size(1) + 7) / 8 * 8 : W.size(1);
+  check_rc(spira_hip_conv_os_workspace(T, K, cin_run, W.size(2), dtype, mode, &wsb), "conv_os");
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
@@ -246,7 +247,14 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
     mp = oe.ordered_map.data_ptr<int32_t>();
   }
-  check_rc(spira_hip_conv_os(T, K, mp, order, masks, X.data_ptr(), S, W.size(1), wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
+  // fp16 rows whose width is not a multiple of 8 channels (the 3-channel
+  // stem) are padded with zero channels to 16-byte rows, which the MMA
+  // kernel gathers with one vector load each; the prepared weights already
+  // hold zeros there (they are padded to 16 input channels)
+  const int64_t cin = cin_run;
+  torch::Tensor Xp = X;
+  if (cin != W.size(1)) Xp = torch::constant_pad_nd(X.narrow(0, 0, S), {0, cin - W.size(1)});
+  check_rc(spira_hip_conv_os(T, K, mp, order, masks, Xp.data_ptr(), S, cin, wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
                              dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, ws.defined() ? ws.data_ptr() : nullptr, wsb,
                              current_stream()),
            "sparse_convolution_forward_os");

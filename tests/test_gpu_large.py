@@ -1,8 +1,10 @@
-"""Offset splitting of the output-stationary kernel on a 200k-voxel scene
-(row-ordered: its densest leading row blocks run as several workgroups whose
-fp32 partial tiles the last one sums) and on small layers (every block
-splits).  Checked against the float64 oracle on every row; tolerance
-max |error| <= 1e-2 * RMS(reference) for fp16 storage."""
+"""Output-stationary layers at full size and the row order they run in: a
+200k-voxel indoor scene (row-ordered: targets grouped by neighbour pattern,
+the 128-row groups with the most neighbour offsets first) at several widths,
+with the fused epilogue, and small layers (fewer blocks than CUs: offsets
+split over blocks, fp32 atomics + finalize).  Checked against the float64
+oracle on every row; tolerance max |error| <= 1e-2 * RMS(reference) for fp16
+storage.  The row order is checked for its defining properties."""
 import numpy as np
 import pytest
 import torch
@@ -31,7 +33,7 @@ def _case(S, cin, cout, dev, seed):
 
 
 @pytest.mark.parametrize("cin,cout", [(32, 32), (96, 96), (64, 128), (128, 256)])
-def test_ordered_layer_splits(dev, indoor, cin, cout):
+def test_ordered_layer(dev, indoor, cin, cout):
     k, m = indoor
     S = T = len(k)
     X, W = _case(S, cin, cout, dev, seed=cin + cout)
@@ -62,7 +64,7 @@ def test_ordered_layer_epilogue(dev, indoor):
 
 
 @pytest.mark.parametrize("T,cin,cout", [(300, 64, 64), (2000, 32, 96), (5000, 256, 256), (40, 3, 16)])
-def test_small_layer_splits(dev, T, cin, cout):
+def test_small_layer(dev, T, cin, cout):
     c = scenes.spheres_planes(n=T, grid=32, seed=T)
     k, _ = orc.flatten_sort(c, True)
     T = S = len(k)
