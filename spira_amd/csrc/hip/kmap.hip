@@ -428,8 +428,9 @@ __host__ __device__ __forceinline__ int row_key_bits(int K) {
 }
 // One block stages RB consecutive map rows in LDS with coalesced loads (RB =
 // 256 rows for K <= 32, else 64), then thread t < RB builds row t's key.
+template <typename KT>
 __global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict__ map, int64_t T, int K, int RB,
-                                                       uint64_t *__restrict__ keys, int32_t *__restrict__ iota) {
+                                                       KT *__restrict__ keys, int32_t *__restrict__ iota) {
   extern __shared__ int32_t rows_lds[];
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RB;
   const int64_t nr = (T - row0) < RB ? (T - row0) : RB;
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict
     cnt += v;
     if (v && j < P) m |= uint64_t(1) << j;
   }
-  keys[row0 + threadIdx.x] = (static_cast<uint64_t>(K - cnt) << P) | m;
+  keys[row0 + threadIdx.x] = static_cast<KT>((static_cast<uint64_t>(K - cnt) << P) | m);
   iota[row0 + threadIdx.x] = static_cast<int32_t>(row0 + threadIdx.x);
 }
 
@@ -454,7 +455,8 @@ __global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict
 // first (128 - popcount) and keeps a trailing partial group last (255).
 // K <= 57: the unions come from the sort keys (their low K bits are the
 // rows' column masks), one wave per group.
-__global__ __launch_bounds__(256) void group_union_keys_kernel(const uint64_t *__restrict__ keys_sorted, int K,
+template <typename KT>
+__global__ __launch_bounds__(256) void group_union_keys_kernel(const KT *__restrict__ keys_sorted, int K,
                                                                int64_t T, uint64_t *__restrict__ gm,
                                                                uint32_t *__restrict__ gkey,
                                                                int32_t *__restrict__ giota) {
@@ -467,7 +469,7 @@ __global__ __launch_bounds__(256) void group_union_keys_kernel(const uint64_t *_
     const uint64_t pm = (uint64_t(1) << K) - 1;
     for (int r = lane; r < 128; r += 64) {
       const int64_t row = g * 128 + r;
-      if (row < T) m |= keys_sorted[row] & pm;
+      if (row < T) m |= static_cast<uint64_t>(keys_sorted[row]) & pm;
     }
     for (int o = 32; o > 0; o >>= 1) m |= static_cast<uint64_t>(__shfl_xor(m, o, 64));
     if (lane == 0) {
@@ -479,6 +481,67 @@ __global__ __launch_bounds__(256) void group_union_keys_kernel(const uint64_t *_
     const int pc = __popcll(gm[g * 2]) + __popcll(gm[g * 2 + 1]);
     gkey[g] = (g + 1) * 128 > T ? 255u : static_cast<uint32_t>(128 - pc);
     giota[g] = static_cast<int32_t>(g);
+  }
+}
+
+// Stable counting sort of the G group keys (values < 256): gperm = the
+// group ids by key.  One wave: an LDS histogram, its exclusive scan, then
+// chunks of 64 keys in order, each lane placed at its bin's running base
+// plus its rank among the chunk's lanes with the same key (peer masks from
+// eight ballots); the highest lane of each key advances the base.
+constexpr int kGroupOrderMax = 49152;
+__global__ __launch_bounds__(64) void group_order_kernel(const uint32_t *__restrict__ gkey, int G,
+                                                         int32_t *__restrict__ gperm) {
+  __shared__ int base_s[256];
+  __shared__ uint8_t key_s[kGroupOrderMax];
+  const int lane = threadIdx.x;
+  for (int b = lane; b < 256; b += 64) base_s[b] = 0;
+  __builtin_amdgcn_wave_barrier();
+  for (int i = lane; i < G; i += 64) {
+    const uint32_t k = gkey[i] & 255;
+    key_s[i] = static_cast<uint8_t>(k);
+    atomicAdd(&base_s[k], 1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  {
+    // exclusive scan: lane l owns bins 4l .. 4l+3
+    int c[4], t = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c[q] = base_s[lane * 4 + q];
+      t += c[q];
+    }
+    int incl = t;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    int run = incl - t;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      base_s[lane * 4 + q] = run;
+      run += c[q];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  for (int c0 = 0; c0 < G; c0 += 64) {
+    const int i = c0 + lane;
+    const bool valid = i < G;
+    const int k = valid ? static_cast<int>(key_s[i]) : 0;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t b = __ballot(valid && ((k >> bit) & 1));
+      peers &= ((k >> bit) & 1) ? b : ~b;
+    }
+    const int pos = valid ? base_s[k] + __popcll(peers & below) : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      gperm[pos] = i;
+      if ((peers >> lane) == 1) base_s[k] += __popcll(peers);  // the highest lane of its key
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -562,15 +625,18 @@ struct RowOrderParts {
 };
 static RowOrderParts row_order_parts(int64_t T, void *base) {
   const int64_t G = (T + 127) / 128;
-  size_t b1 = 0, b2 = 0;
+  size_t b1 = 0, b2 = 0, b3 = 0;
   (void)rocprim::radix_sort_pairs(nullptr, b1, static_cast<const uint64_t *>(nullptr),
                                   static_cast<uint64_t *>(nullptr), static_cast<const int32_t *>(nullptr),
                                   static_cast<int32_t *>(nullptr), static_cast<size_t>(T), 0, 64);
+  (void)rocprim::radix_sort_pairs(nullptr, b3, static_cast<const uint32_t *>(nullptr),
+                                  static_cast<uint32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
+                                  static_cast<int32_t *>(nullptr), static_cast<size_t>(T), 0, 32);
   (void)rocprim::radix_sort_pairs(nullptr, b2, static_cast<const uint32_t *>(nullptr),
                                   static_cast<uint32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
                                   static_cast<int32_t *>(nullptr), static_cast<size_t>(G), 0, 8);
   RowOrderParts r{};
-  r.tmp_bytes = std::max(b1, b2);
+  r.tmp_bytes = std::max(std::max(b1, b2), b3);
   char *p = static_cast<char *>(base);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -714,19 +780,33 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
   const int rb = num_offsets <= 32 ? 256 : 64;
   SPIRA_HIP_REQUIRE(static_cast<size_t>(rb) * num_offsets * sizeof(int32_t) <= 64 * 1024,
                     "kmap_row_order: at most 256 offsets");
-  hipLaunchKernelGGL(row_mask_kernel, dim3(div_up(num_targets, rb)), dim3(256), rb * num_offsets * sizeof(int32_t),
-                     stream, out_in_map, num_targets, num_offsets, rb, w.keys, w.iota);
-  SPIRA_HIP_LAUNCH_CHECK();
+  // 32-bit sort keys when they fit (kernels of <= 27 offsets): the sort
+  // moves half the key bytes
+  const int kbits = row_key_bits(num_offsets);
+  const bool k32 = kbits <= 32;
   size_t tb = w.tmp_bytes;
-  SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, w.keys, w.keys_out, w.iota, w.sorted,
-                                          static_cast<size_t>(num_targets), 0, row_key_bits(num_offsets), stream));
+  if (k32) {
+    uint32_t *keys = reinterpret_cast<uint32_t *>(w.keys), *keys_out = reinterpret_cast<uint32_t *>(w.keys_out);
+    hipLaunchKernelGGL(row_mask_kernel<uint32_t>, dim3(div_up(num_targets, rb)), dim3(256),
+                       rb * num_offsets * sizeof(int32_t), stream, out_in_map, num_targets, num_offsets, rb, keys,
+                       w.iota);
+    SPIRA_HIP_LAUNCH_CHECK();
+    SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, keys, keys_out, w.iota, w.sorted,
+                                            static_cast<size_t>(num_targets), 0, kbits, stream));
+  } else {
+    hipLaunchKernelGGL(row_mask_kernel<uint64_t>, dim3(div_up(num_targets, rb)), dim3(256),
+                       rb * num_offsets * sizeof(int32_t), stream, out_in_map, num_targets, num_offsets, rb, w.keys,
+                       w.iota);
+    SPIRA_HIP_LAUNCH_CHECK();
+    SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, w.keys, w.keys_out, w.iota, w.sorted,
+                                            static_cast<size_t>(num_targets), 0, kbits, stream));
+  }
   const int64_t G = div_up(num_targets, 128);
   const int32_t *gperm = nullptr;
   const uint64_t *gm = nullptr;
   if (group_masks) {
     // group unions, then the groups with the most columns first: the
-    // densest blocks start first and lead the grid, where the conv kernel
-    // lets them split
+    // longest blocks start first
     const bool from_keys = num_offsets <= 57;  // the sort keys hold the whole column mask
     if (!from_keys) {
       hipLaunchKernelGGL(order_rows_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map,
@@ -735,13 +815,24 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
                          static_cast<const uint64_t *>(nullptr), w.gm);
       SPIRA_HIP_LAUNCH_CHECK();
     }
-    hipLaunchKernelGGL(group_union_keys_kernel, dim3(div_up(G, 4)), dim3(256), 0, stream,
-                       from_keys ? w.keys_out : static_cast<const uint64_t *>(nullptr), num_offsets, num_targets,
-                       w.gm, w.gkey, w.giota);
+    if (k32)
+      hipLaunchKernelGGL(group_union_keys_kernel<uint32_t>, dim3(div_up(G, 4)), dim3(256), 0, stream,
+                         from_keys ? reinterpret_cast<const uint32_t *>(w.keys_out) : nullptr, num_offsets,
+                         num_targets, w.gm, w.gkey, w.giota);
+    else
+      hipLaunchKernelGGL(group_union_keys_kernel<uint64_t>, dim3(div_up(G, 4)), dim3(256), 0, stream,
+                         from_keys ? w.keys_out : static_cast<const uint64_t *>(nullptr), num_offsets, num_targets,
+                         w.gm, w.gkey, w.giota);
     SPIRA_HIP_LAUNCH_CHECK();
-    tb = w.tmp_bytes;
-    SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, w.gkey, w.gkey_out, w.giota, w.gperm, static_cast<size_t>(G),
-                                            0, 8, stream));
+    // (a few thousand groups: one wave beats a device-wide sort's launches)
+    if (G <= kGroupOrderMax) {
+      hipLaunchKernelGGL(group_order_kernel, dim3(1), dim3(64), 0, stream, w.gkey, static_cast<int>(G), w.gperm);
+      SPIRA_HIP_LAUNCH_CHECK();
+    } else {
+      tb = w.tmp_bytes;
+      SPIRA_HIP_TRY(rocprim::radix_sort_pairs(w.tmp, tb, w.gkey, w.gkey_out, w.giota, w.gperm,
+                                              static_cast<size_t>(G), 0, 8, stream));
+    }
     gperm = w.gperm;
     gm = w.gm;
   }
