@@ -982,7 +982,11 @@ static inline int bm_for(int wn) {
 // active-offset set)
 static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
   int jper = Kc;
-  const int64_t want = static_cast<int64_t>(cus);
+  static const int mult = [] {
+    const char *e = std::getenv("SPIRA_OS_JPER_WANT");
+    return e && *e ? std::atoi(e) : 1;
+  }();
+  const int64_t want = static_cast<int64_t>(cus) * mult;
   if (blocks_xy < want && Kc > 1) {
     const int64_t splits = std::min<int64_t>(Kc, div_up(want, blocks_xy));
     jper = static_cast<int>(div_up(Kc, splits));
@@ -1138,12 +1142,26 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
   return kOk;
 }
 
+// Column-tile width of the output-stationary kernel: the widest tile, made
+// narrower (more column blocks, each re-gathering its rows) while the grid
+// has fewer than SPIRA_OS_MIN_BLOCKS (default 1) blocks per CU.  (Measured
+// on the end-to-end network: more than one block per CU this way, or by
+// more offset splits, costs more in re-gathered rows / atomics than the
+// added occupancy returns.)
+static int os_wn(int64_t num_targets, int c_out, int cus) {
+  static const int mult = env_int("SPIRA_OS_MIN_BLOCKS", 1);
+  int wn = wn_for(c_out);
+  const int64_t bx = div_up(num_targets, bm_for(1));
+  while (wn > 1 && bx * div_up(pad_out(c_out), 32 * wn) < static_cast<int64_t>(mult) * cus) wn = wn == 3 ? 1 : wn / 2;
+  return wn;
+}
+
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
                                 size_t *bytes) {
   (void)c_in;
   *bytes = 0;
   if (!mfma_path(dtype) || out_mode != SPIRA_OUT_STORE || num_targets <= 0) return kOk;
-  const int wn = wn_for(c_out);
+  const int wn = os_wn(num_targets, c_out, device_cu_count());
   const int bm = bm_for(wn);
   const int64_t blocks = div_up(num_targets, bm) * div_up(pad_out(c_out), 32 * wn);
   if (choose_jper(blocks, num_offsets, device_cu_count()) < num_offsets)
@@ -1169,7 +1187,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
   if (mfma_path(dtype)) {
     SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
     const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
-    const int wn = wn_for(c_out);
+    const int wn = os_wn(num_targets, c_out, device_cu_count());
     const int bm = bm_for(wn);
     const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
     // small layers (fewer blocks than CUs) split their offsets over grid z
