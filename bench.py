@@ -31,6 +31,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+# HBM bytes per launch of the dominant kernel (os_kernel<3,0,true,4>, 200k
+# voxels, 96 -> 96): rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE over
+# `bench.py --no-cpu --only layer,calib`, each scaled by what the counter
+# reads for the calibration leg's 256 MiB copy (FETCH_SIZE x 2.000,
+# WRITE_SIZE x 1.000): 68116 KiB fetched, 37624 KiB written.
+DOMINANT_TRAFFIC_BYTES = 68116 * 1024 * 2.0 + 37624 * 1024 * 1.0
 
 
 def parse():
@@ -41,7 +47,8 @@ def parse():
     p.add_argument("--dataflow", type=int, default=0, help="map dataflow used by every layer")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-fuse", action="store_true", help="run batch norm / ReLU / residual adds unfused")
-    p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer")
+    p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer (calib: a plain 256 MiB "
+                                              "device copy, the reference point of the HBM byte counters)")
     return p.parse_args()
 
 
@@ -166,6 +173,19 @@ def dominant_leg(torch, keys_np, C=96, reps=20):
     return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12, "pairs": P, "C": C}
 
 
+def calib_leg(torch, mib=256, reps=5):
+    """A plain device-to-device copy of a known size: reads and writes
+    `mib` MiB per launch.  Run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    it gives the factor that turns those counters into bytes."""
+    dev = torch.device("cuda:0")
+    x = torch.empty(mib * (1 << 20) // 2, dtype=torch.float16, device=dev).uniform_()
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    return {"bytes_each_way": mib * (1 << 20), "reps": reps}
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the same end-to-end pipeline on the host through the oracle
 # ---------------------------------------------------------------------------
@@ -288,9 +308,14 @@ def main():
         ikeys, _ = orc.flatten_sort(indoor, True)
         dm = dominant_leg(torch, ikeys)
         res["roofline"] = {"bound": "mfma", "achieved": dm["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
-                           "unit": "TFLOP/s", "frac": dm["tflops"] / MFMA_F16_PEAK_TFLOPS, "traffic": None,
-                           "kernel": "os_kernel<3,0,true> (config 4 full resolution, 200k voxels, k=3, 96->96, fp16)",
+                           "unit": "TFLOP/s", "frac": dm["tflops"] / MFMA_F16_PEAK_TFLOPS,
+                           "traffic": DOMINANT_TRAFFIC_BYTES,
+                           "traffic_gbs": DOMINANT_TRAFFIC_BYTES / (dm["ms"] * 1e-3) / 1e9,
+                           "kernel": "os_kernel<3,0,true,4> (config 4 full resolution, 200k voxels, k=3, 96->96, "
+                                     "fp16, 64-channel steps)",
                            "ms": dm["ms"], "algorithmic_flops": dm["flops"], "valid_pairs": dm["pairs"]}
+    if "calib" in legs:
+        res["calib"] = calib_leg(torch)
     if not args.no_cpu and model is not None:
         feats = np.random.default_rng(0).standard_normal((indoor.shape[0], 3)).astype(np.float32)
         t0 = time.perf_counter()
