@@ -589,19 +589,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     ++fu;
     fit.step(nch);
   };
-  auto resolve = [&](int u, auto St, int32_t (&idx)[MT], int &wrow, int &kb) {
-    (void)u;
-    if (tiled) {
-      const uint32_t col = static_cast<uint32_t>(pit.j) * 4u;
+  // Tiled maps: the indices of the next step are read from the tile right
+  // after a step's are resolved, so their LDS latency hides behind the
+  // following compute (whose B-read wait also covers them); only the
+  // prologue's steps (no compute in between) wait for their own read.
+  int32_t pre[MT];
+  auto read_tile = [&]() {
+    const uint32_t col = static_cast<uint32_t>(pit.j) * 4u;
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
-        asm volatile("ds_read_b32 %0, %1" : "=v"(idx[m]) : "v"(tbase + m * 32 * KP * 4 + col) : "memory");
+    for (int m = 0; m < MT; ++m)
+      asm volatile("ds_read_b32 %0, %1" : "=v"(pre[m]) : "v"(tbase + m * 32 * KP * 4 + col) : "memory");
+  };
+  if (tiled) read_tile();
+  auto resolve = [&](int u, auto St, int32_t (&idx)[MT], int &wrow, int &kb) {
+    if (tiled) {
+      if (u < NS) ring::lds_wait();  // prologue puts: no compute since the read
+#pragma unroll
+      for (int m = 0; m < MT; ++m) idx[m] = pre[m];
     } else {
       ring::unroll<MT>([&](auto M) {
         idx[decltype(M)::value] = ring::rd4<decltype(St)::value * 1024 + decltype(M)::value * 128>(ibase);
       });
+      ring::lds_wait();
     }
-    ring::lds_wait();
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       ring::pin(idx[m]);
@@ -611,6 +621,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     wrow = j0 + pit.j;
     kb = pit.chunk * C::KC;
     pit.step(nch);
+    if (tiled) read_tile();
   };
   ring::run<C, ALIGNED, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   SPIRA_STAMP(2);
