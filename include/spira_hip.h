@@ -193,6 +193,21 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
                       void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
                       int relu, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* spira_hip_conv_os over the channel concatenation [sources | sources2] of two
+ * fp16 feature arrays ([num_sources, c_in] and [num_sources, c_in2]; c_in a
+ * multiple of 16, c_in2 of 8) without materialising it: the gather picks
+ * each 16-channel slice from the part that holds it.  `prepared` holds the
+ * weights of the whole [K, c_in + c_in2, c_out] layer; every other argument
+ * is as in spira_hip_conv_os.  (Replaces the skip-connection torch.cat in
+ * front of a decoder layer, source/spira/operators.py:11-13; no counterpart
+ * in the reference's C++.) */
+int spira_hip_conv_os_concat(int64_t num_targets, int num_offsets, const int32_t *out_in_map,
+                             const int32_t *row_order, const uint64_t *group_masks, const void *sources,
+                             const void *sources2, int64_t num_sources, int c_in, int c_in2, const void *prepared,
+                             int c_out, void *targets, int out_mode, const float *scale, const float *shift,
+                             const void *residual, int relu, void *workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
 /* Fused weight-stationary pass over a compacted pair list: for compacted row r
  * (pairs naddrs[r]..naddrs[r+1] of in_idx/out_idx) target_acc[out] +=
  * sources[in] @ weights[weight_offset + r]; with mirror_rows = Kw > 0 also

@@ -68,8 +68,11 @@ struct Epilogue {
 // channels lie in the padding) uses an offset past the end, and the buffer
 // unit then returns zeros instead of reading memory.
 struct Operands {
-  const _Float16 *X;  // [rows, Cin] gathered rows
+  const _Float16 *X;  // [rows, C1] gathered rows: input channels 0 .. C1-1
   uint32_t xbytes;
+  const _Float16 *X2;  // [rows, Cin - C1]: channels C1 .. Cin-1 (a channel concatenation), or null
+  uint32_t x2bytes;
+  int C1;  // channels held by X (Cin without X2; a multiple of 16 with it)
   int Cin, CinP;
   const _Float16 *WT;  // prepared weights [K, CoutP, CinP]
   uint32_t wbytes;
@@ -209,7 +212,8 @@ template <class C> __device__ __forceinline__ ReadBase<C::NKS> read_base(const c
 template <class C, bool ALIGNED, int S>
 __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
                                       int kb, const Operands &op, __amdgpu_buffer_rsrc_t xr,
-                                      __amdgpu_buffer_rsrc_t wr, int n0, half8 (&a)[C::BM / 128][C::NKS]) {
+                                      __amdgpu_buffer_rsrc_t xr2, __amdgpu_buffer_rsrc_t wr, int n0,
+                                      half8 (&a)[C::BM / 128][C::NKS]) {
   constexpr int MT = C::BM / 128;
   const int tid = threadIdx.x, lane = tid & 63;
   const int kh = lane >> 5;
@@ -223,7 +227,11 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
       // the destination registers, and the second write would have to
       // wait for every load in flight
       const bool ok = live & (idx[m] >= 0) & (k < op.Cin);
-      const uint32_t at = (static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>(op.Cin) + k) * 2u;
+      // the 16-channel slice lies wholly in X or in X2 (C1 % 16 == 0): a
+      // block-uniform choice of buffer
+      const bool second = kb + ks * 16 >= op.C1;
+      const uint32_t rowc = static_cast<uint32_t>(second ? op.Cin - op.C1 : op.C1);
+      const uint32_t at = (static_cast<uint32_t>(idx[m]) * rowc + (second ? k - op.C1 : k)) * 2u;
       const uint32_t off = ok ? at : kOutOfRange;
       if constexpr (!ALIGNED) {
         // rows that are not 16-byte aligned: element loads (still one
@@ -237,7 +245,7 @@ __device__ __forceinline__ void issue(char *ring, int wave, bool live, const int
                                                         : static_cast<_Float16>(0.f);
         a[m][ks] = v;
       } else {
-        a[m][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        a[m][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, off, 0, 0));
       }
     }
   }
@@ -300,6 +308,7 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
   constexpr int MT = C::BM / 128, NS = C::NS;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
+  const __amdgpu_buffer_rsrc_t xr2 = make_rsrc(op.X2 ? op.X2 : op.X, op.X2 ? op.x2bytes : 0u);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
   const ReadBase<C::NKS> rb = read_base<C>(ring);
   half8 areg[NS][MT][C::NKS];  // gathered rows per stage
@@ -313,7 +322,7 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
 #pragma unroll
       for (int m = 0; m < MT; ++m) idx[m] = -1;
     }
-    issue<C, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, wr, n0,
+    issue<C, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, xr2, wr, n0,
                                            areg[decltype(St)::value]);
   };
   unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
@@ -1011,16 +1020,22 @@ static int env_int(const char *name, int dflt) {
 }
 
 // Operands of the MMA core; byte sizes must fit the 31-bit buffer offsets
-static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, const void *WT, int K, int Cout) {
-  op.Cin = Cin;
-  op.CinP = pad_in(Cin);
+// (X2 / C2: the second half of a channel concatenation, or null / 0)
+static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, const void *WT, int K, int Cout,
+                         const void *X2 = nullptr, int C2 = 0) {
+  op.Cin = Cin + C2;
+  op.C1 = Cin;
+  op.CinP = pad_in(op.Cin);
   op.Cout = Cout;
   op.CoutP = pad_out(Cout);
-  const int64_t xb = xrows * Cin * 2, wb = static_cast<int64_t>(K) * op.CoutP * op.CinP * 2;
-  SPIRA_HIP_REQUIRE(xb < (int64_t(1) << 31) && wb < (int64_t(1) << 31),
+  const int64_t xb = xrows * Cin * 2, x2b = xrows * C2 * 2,
+                wb = static_cast<int64_t>(K) * op.CoutP * op.CinP * 2;
+  SPIRA_HIP_REQUIRE(xb < (int64_t(1) << 31) && x2b < (int64_t(1) << 31) && wb < (int64_t(1) << 31),
                     "fp16 features / weights of one layer must stay below 2 GiB");
   op.X = static_cast<const _Float16 *>(X);
   op.xbytes = static_cast<uint32_t>(xb);
+  op.X2 = static_cast<const _Float16 *>(X2);
+  op.x2bytes = static_cast<uint32_t>(x2b);
   op.WT = static_cast<const _Float16 *>(WT);
   op.wbytes = static_cast<uint32_t>(wb);
   return kOk;
@@ -1180,12 +1195,19 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
   return kOk;
 }
 
-int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
-                      const uint64_t *group_masks, const void *sources,
-                      int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
-                      void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
-                      int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+// conv_os over sources (c_in channels) or over the channel concatenation
+// [sources | sources2] (c_in + c_in2 channels; fp16, c_in % 16 == 0,
+// c_in2 % 8 == 0)
+static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
+                        const uint64_t *group_masks, const void *sources, const void *sources2, int64_t num_sources,
+                        int c_in, int c_in2, const void *weights, const void *prepared, int c_out, int dtype,
+                        void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
+                        int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_os: dtype must be fp16 or fp32");
+  SPIRA_HIP_REQUIRE(c_in2 == 0 || (sources2 && dtype == SPIRA_F16 && c_in % 16 == 0 && c_in2 % 8 == 0),
+                    "conv_os_concat: fp16 only, the first part's channels a multiple of 16, the second's of 8");
   SPIRA_HIP_REQUIRE(out_mode >= SPIRA_OUT_STORE && out_mode <= SPIRA_OUT_ADD_F32, "conv_os: bad out_mode");
   SPIRA_HIP_REQUIRE(c_in > 0 && c_out > 0 && num_offsets > 0, "conv_os: empty channel / offset dimension");
   SPIRA_HIP_REQUIRE(out_mode == SPIRA_OUT_STORE || (!scale && !shift && !residual && !relu),
@@ -1197,7 +1219,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
   const Epilogue epi = make_epi(scale, shift, residual, relu);
   if (mfma_path(dtype)) {
     SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
-    const int CinP = pad_in(c_in), CoutP = pad_out(c_out);
+    const int CoutP = pad_out(c_out);
     const int wn = os_wn(num_targets, c_out, device_cu_count());
     const int bm = bm_for(wn);
     const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
@@ -1208,7 +1230,7 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
     SPIRA_HIP_REQUIRE(num_targets * num_offsets * 4 < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
     // (out_in_map may be null: the identity map, handled in the kernel)
     Operands op;
-    int rc0 = make_operands(op, sources, num_sources, c_in, prepared, num_offsets, c_out);
+    int rc0 = make_operands(op, sources, num_sources, c_in, prepared, num_offsets, c_out, sources2, c_in2);
     if (rc0) return rc0;
     if (splits == 1) {
       if (out_mode == SPIRA_OUT_STORE)
@@ -1250,6 +1272,30 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
   }
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
+}
+
+extern "C" {
+
+int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
+                      const uint64_t *group_masks, const void *sources,
+                      int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
+                      void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
+                      int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  return conv_os_impl(num_targets, num_offsets, out_in_map, row_order, group_masks, sources, nullptr, num_sources,
+                      c_in, 0, weights, prepared, c_out, dtype, targets, out_mode, scale, shift, residual, relu,
+                      workspace, workspace_bytes, stream);
+}
+
+int spira_hip_conv_os_concat(int64_t num_targets, int num_offsets, const int32_t *out_in_map,
+                             const int32_t *row_order, const uint64_t *group_masks, const void *sources,
+                             const void *sources2, int64_t num_sources, int c_in, int c_in2, const void *prepared,
+                             int c_out, void *targets, int out_mode, const float *scale, const float *shift,
+                             const void *residual, int relu, void *workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(sources2 != nullptr && c_in2 > 0, "conv_os_concat: needs a second source part");
+  return conv_os_impl(num_targets, num_offsets, out_in_map, row_order, group_masks, sources, sources2, num_sources,
+                      c_in, c_in2, nullptr, prepared, c_out, SPIRA_F16, targets, out_mode, scale, shift, residual,
+                      relu, workspace, workspace_bytes, stream);
 }
 
 int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int32_t *in_idx, const int32_t *out_idx,

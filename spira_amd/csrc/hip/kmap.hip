@@ -485,24 +485,26 @@ __global__ __launch_bounds__(256) void group_union_keys_kernel(const KT *__restr
 }
 
 // Stable counting sort of the G group keys (values < 256): gperm = the
-// group ids by key.  One wave: an LDS histogram, its exclusive scan, then
-// chunks of 64 keys in order, each lane placed at its bin's running base
-// plus its rank among the chunk's lanes with the same key (peer masks from
-// eight ballots); the highest lane of each key advances the base.
+// group ids by key.  The block stages the keys in LDS and builds their
+// histogram; then one wave scans it and walks chunks of 64 keys in order,
+// each lane placed at its bin's running base plus its rank among the
+// chunk's lanes with the same key (peer masks from eight ballots); the
+// highest lane of each key advances the base.
 constexpr int kGroupOrderMax = 49152;
-__global__ __launch_bounds__(64) void group_order_kernel(const uint32_t *__restrict__ gkey, int G,
-                                                         int32_t *__restrict__ gperm) {
+__global__ __launch_bounds__(256) void group_order_kernel(const uint32_t *__restrict__ gkey, int G,
+                                                          int32_t *__restrict__ gperm) {
   __shared__ int base_s[256];
   __shared__ uint8_t key_s[kGroupOrderMax];
-  const int lane = threadIdx.x;
-  for (int b = lane; b < 256; b += 64) base_s[b] = 0;
-  __builtin_amdgcn_wave_barrier();
-  for (int i = lane; i < G; i += 64) {
+  base_s[threadIdx.x] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < G; i += 256) {
     const uint32_t k = gkey[i] & 255;
     key_s[i] = static_cast<uint8_t>(k);
     atomicAdd(&base_s[k], 1);
   }
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
   {
     // exclusive scan: lane l owns bins 4l .. 4l+3
     int c[4], t = 0;
@@ -826,7 +828,7 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
     SPIRA_HIP_LAUNCH_CHECK();
     // (a few thousand groups: one wave beats a device-wide sort's launches)
     if (G <= kGroupOrderMax) {
-      hipLaunchKernelGGL(group_order_kernel, dim3(1), dim3(64), 0, stream, w.gkey, static_cast<int>(G), w.gperm);
+      hipLaunchKernelGGL(group_order_kernel, dim3(1), dim3(256), 0, stream, w.gkey, static_cast<int>(G), w.gperm);
       SPIRA_HIP_LAUNCH_CHECK();
     } else {
       tb = w.tmp_bytes;

@@ -157,13 +157,21 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> kmap_row_order(const tor
   return {e.order.narrow(0, 0, T), e.masks, e.ordered_map.narrow(0, 0, T)};
 }
 
-static void check_features(const torch::Tensor &X, const torch::Tensor &W) {
+// (X2: the second part of a channel concatenation [X | X2], or null)
+static void check_features(const torch::Tensor &X, const torch::Tensor &W, const torch::Tensor *X2 = nullptr) {
   SPIRA_CHECK_ARG(X.dim() == 2, "sources must be [N, C_in]");
   SPIRA_CHECK_ARG(W.dim() == 3, "weights must be [K, C_in, C_out]");
   require_device(X, "sources");
   require_device(W, "weights");
   SPIRA_CHECK_ARG(X.scalar_type() == W.scalar_type(), "sources and weights must share a dtype");
-  SPIRA_CHECK_ARG(X.size(1) == W.size(1), "sources have ", X.size(1), " channels, weights expect ", W.size(1));
+  int64_t c = X.size(1);
+  if (X2) {
+    SPIRA_CHECK_ARG(X2->dim() == 2 && X2->size(0) == X.size(0) && X2->scalar_type() == X.scalar_type(),
+                    "the second source part must be [N, C2] of the sources' dtype");
+    require_device(*X2, "sources2");
+    c += X2->size(1);
+  }
+  SPIRA_CHECK_ARG(c == W.size(1), "sources have ", c, " channels, weights expect ", W.size(1));
   dtype_of(X);
 }
 
@@ -219,10 +227,14 @@ static torch::Tensor zeroed_workspace(size_t bytes, const torch::Device &dev) {
 
 static bool epi_empty(const Epi &e) { return !e.scale && !e.shift && !e.residual && !e.relu; }
 
-static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X, const torch::Tensor &W,
-                   int w0, int K, void *out, int mode, const Epi &epi = Epi()) {
-  const auto dev = X.device();
-  const int dtype = dtype_of(X);
+static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X0, const torch::Tensor &W,
+                   int w0, int K, void *out, int mode, const Epi &epi = Epi(), const torch::Tensor *X2 = nullptr) {
+  const auto dev = X0.device();
+  const int dtype = dtype_of(X0);
+  // a channel concatenation [X0 | X2] is gathered from its two parts when
+  // the split falls on a 16-channel slice (fp16), else materialised here
+  const bool split = X2 && dtype == SPIRA_F16 && X0.size(1) % 16 == 0 && X2->size(1) % 8 == 0;
+  const torch::Tensor X = (X2 && !split) ? torch::cat({X0, *X2}, 1) : X0;
   const int32_t *mp = nullptr;
   if (map) {
     SPIRA_CHECK_ARG(map->dim() == 2 && map->scalar_type() == torch::kInt32, "out_in_map must be 2-D int32");
@@ -236,7 +248,8 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   }
   auto P = prepared_weights(W);
   size_t wsb = 0;
-  const int64_t cin_run = (dtype == SPIRA_F16 && W.size(1) % 8 != 0) ? (W.size(1) + 7) / 8 * 8 : W.size(1);
+  const int64_t cin_run =
+      (!split && dtype == SPIRA_F16 && W.size(1) % 8 != 0) ? (W.size(1) + 7) / 8 * 8 : W.size(1);
   check_rc(spira_hip_conv_os_workspace(T, K, cin_run, W.size(2), dtype, mode, &wsb), "conv_os");
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
@@ -251,27 +264,37 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   // stem) are padded with zero channels to 16-byte rows, which the MMA
   // kernel gathers with one vector load each; the prepared weights already
   // hold zeros there (they are padded to 16 input channels)
+  void *wsp = ws.defined() ? ws.data_ptr() : nullptr;
+  if (split) {
+    check_rc(spira_hip_conv_os_concat(T, K, mp, order, masks, X.data_ptr(), X2->data_ptr(), S, X.size(1), X2->size(1),
+                                      prow_ptr(P, W, w0), W.size(2), out, mode, epi.scale, epi.shift, epi.residual,
+                                      epi.relu, wsp, wsb, current_stream()),
+             "sparse_convolution_forward_os");
+    return;
+  }
   const int64_t cin = cin_run;
   torch::Tensor Xp = X;
   if (cin != W.size(1)) Xp = torch::constant_pad_nd(X.narrow(0, 0, S), {0, cin - W.size(1)});
   check_rc(spira_hip_conv_os(T, K, mp, order, masks, Xp.data_ptr(), S, cin, wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
-                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, ws.defined() ? ws.data_ptr() : nullptr, wsb,
+                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, wsp, wsb,
                              current_stream()),
            "sparse_convolution_forward_os");
 }
 
 // (reference: CUDASparseConvolutionForward_OS, :448-496)
+// (x2: the second part of a channel-concatenated input [X | x2], or None)
 torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const torch::Tensor &X,
                          const torch::Tensor &W, const std::optional<torch::Tensor> &scale,
                          const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
-                         bool relu) {
-  check_features(X, W);
+                         bool relu, const std::optional<torch::Tensor> &x2) {
+  const torch::Tensor *X2 = x2.has_value() ? &*x2 : nullptr;
+  check_features(X, W, X2);
   SPIRA_CHECK_ARG(out_in_map.dim() == 2, "out_in_map must be 2-D");
   SPIRA_CHECK_ARG(W.size(0) == out_in_map.size(1), "weights have ", W.size(0), " offsets, map has ",
                   out_in_map.size(1));
   auto Y = torch::empty({T, W.size(2)}, X.options());
   run_os(&out_in_map, S, T, X, W, 0, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE,
-         epi_of(scale, shift, residual, relu, T, W.size(2), X));
+         epi_of(scale, shift, residual, relu, T, W.size(2), X), X2);
   return Y;
 }
 
@@ -280,12 +303,14 @@ torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, 
 // the torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313).
 torch::Tensor forward_dense(const torch::Tensor &X, const torch::Tensor &W, const std::optional<torch::Tensor> &scale,
                             const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
-                            bool relu) {
-  check_features(X, W);
+                            bool relu, const std::optional<torch::Tensor> &x2) {
+  const torch::Tensor *X2 = x2.has_value() ? &*x2 : nullptr;
+  check_features(X, W, X2);
   SPIRA_CHECK_ARG(W.size(0) == 1, "a dense layer has one weight offset, got ", W.size(0));
   const int64_t T = X.size(0);
   auto Y = torch::empty({T, W.size(2)}, X.options());
-  run_os(nullptr, T, T, X, W, 0, 1, Y.data_ptr(), SPIRA_OUT_STORE, epi_of(scale, shift, residual, relu, T, W.size(2), X));
+  run_os(nullptr, T, T, X, W, 0, 1, Y.data_ptr(), SPIRA_OUT_STORE, epi_of(scale, shift, residual, relu, T, W.size(2), X),
+         X2);
   return Y;
 }
 

@@ -212,7 +212,14 @@ class SparseConv(Module):
     def forward(self, inputs: SparseTensor, residual: Optional[SparseTensor] = None) -> SparseTensor:
         """residual (fused res blocks only): features added after the batch
         norm and before the ReLU of the fused epilogue."""
-        x = inputs._features
+        # an unmaterialised channel concatenation (spira_amd.cat) goes to the
+        # output-stationary kernels as its two parts
+        parts = inputs._parts
+        if parts is not None and (self.is_trivial or self._tunable_config["map_dataflow"] == 0
+                                  or self._tunable_config["force_os"]):
+            x, x2 = parts
+        else:
+            x, x2 = inputs._features, None
         epilogue = None
         epilogue_done = False
         if self._fused_active():
@@ -226,7 +233,7 @@ class SparseConv(Module):
             raise ValueError("a residual is only taken by a conv with an active fused epilogue")
         if self.is_trivial:
             if x.is_cuda:
-                y = F.dense_forward(x, self.kernel, epilogue=epilogue)
+                y = F.dense_forward(x, self.kernel, epilogue=epilogue, sources2=x2)
                 epilogue_done = True
             else:
                 y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
@@ -247,7 +254,7 @@ class SparseConv(Module):
             S, T = (m[1], m[0]) if self.transposed else (m[0], m[1])
             cfg = self._tunable_config
             if d == 0 or force_os:
-                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue)
+                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue, sources2=x2)
             elif d == 1:
                 y = F.sparse_convolution_forward_ws_merged(S, T, x, self.kernel, m[5], m[6], m[3], m[7], m[8],
                                                            self.transposed, epilogue=epilogue)

@@ -111,16 +111,21 @@ def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sou
                                                         mapsize, qmapsize, bool(transpose), *_epi(epilogue))
 
 
-def dense_forward(sources, weights, *, epilogue=None):
+def dense_forward(sources, weights, *, epilogue=None, sources2=None):
     """sources @ weights[0] (a 1x1x1, stride-1 layer) with the fused epilogue,
     on the output-stationary kernel with the identity map (reference: the
-    torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313)."""
+    torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313).
+    ``sources2``: the input is the channel concatenation [sources | sources2],
+    gathered from its two parts without materialising it."""
     _gpu(sources)
-    return _C.cuda_dense_forward(_c(sources), _c(weights), *_epi(epilogue))
+    return _C.cuda_dense_forward(_c(sources), _c(weights), *_epi(epilogue), _c(sources2))
 
 
 def sparse_convolution_forward_os(num_sources: int, num_targets: int, out_in_map, sources, weights, *,
-                                  epilogue=None):
+                                  epilogue=None, sources2=None):
+    """``sources2``: the layer input is the channel concatenation
+    [sources | sources2] (a decoder's skip connection), gathered from its two
+    parts without materialising it."""
     _gpu(sources)
     return _C.cuda_sparse_convolution_forward_os(num_sources, num_targets, _c(out_in_map), _c(sources),
-                                                 _c(weights), *_epi(epilogue))
+                                                 _c(weights), *_epi(epilogue), _c(sources2))

@@ -1,7 +1,7 @@
 """Sparse tensor container (reference: source/spira/tensors.py:10-65)."""
 from __future__ import annotations
 
-from typing import Tuple, Union
+from typing import List, Optional, Tuple, Union
 
 import torch
 
@@ -18,12 +18,34 @@ class SparseTensor:
     permutes the features to match.  ``stride`` is the per-axis tensor stride.
     """
 
-    def __init__(self, coordinates: torch.Tensor, features: torch.Tensor,
+    def __init__(self, coordinates: torch.Tensor, features: Optional[torch.Tensor],
                  stride: Union[int, Tuple[int, ...]] = 1, double: bool = False):
         self._coordinates = coordinates
-        self._features = features
+        self._feats = features
+        # a channel concatenation not yet materialised (spira_amd.cat): the
+        # output-stationary kernels gather straight from the two parts
+        self._parts: Optional[List[torch.Tensor]] = None
         self._double = double
         self._stride = as_tuple(stride, size=3, name="strides")
+
+    @property
+    def _features(self) -> torch.Tensor:
+        if self._feats is None and self._parts is not None:
+            self._feats = torch.cat(self._parts, dim=1)
+            self._parts = None
+        return self._feats
+
+    @_features.setter
+    def _features(self, value: torch.Tensor) -> None:
+        self._feats = value
+        self._parts = None
+
+    @classmethod
+    def _concatenated(cls, parts: List[torch.Tensor], coordinates: torch.Tensor,
+                      stride: Union[int, Tuple[int, ...]]) -> "SparseTensor":
+        t = cls(coordinates=coordinates, features=None, stride=stride)
+        t._parts = list(parts)
+        return t
 
     @property
     def coordinates(self) -> torch.Tensor:

@@ -158,3 +158,46 @@ def test_dense_forward(dev, dtype, cin, cout):
     assert rel_err(np_(y.float()), ref_conv) <= TOL[dtype]
     y = F.dense_forward(X.to(dev), W.to(dev), epilogue=(scale.to(dev), shift.to(dev), res.to(dev), True))
     assert rel_err(np_(y.float()), _ref(ref_conv, scale, shift, res, True)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("c1,c2", [(96, 32), (32, 32), (256, 128), (48, 24), (40, 24), (64, 3)])
+def test_concat_input_without_copy(dev, keys, c1, c2):
+    """A layer whose input is the channel concatenation [A | B] (a decoder's
+    skip connection) gathers from the two parts when the split falls on a
+    16-channel slice, and materialises the concatenation otherwise; both
+    match the oracle on the concatenated features, with the epilogue."""
+    S = T = len(keys)
+    g = torch.Generator().manual_seed(c1 + c2)
+    A = torch.randn(S, c1, generator=g).half()
+    B = torch.randn(S, c2, generator=g).half()
+    W = (torch.randn(27, c1 + c2, 64, generator=g) / np.sqrt(27 * (c1 + c2))).half()
+    scale = torch.rand(64, generator=g) + 0.5
+    shift = torch.randn(64, generator=g)
+    res = torch.randn(T, 64, generator=g).half()
+    Xn = torch.cat([A, B], 1).double().numpy()
+    m = orc.build_kmap(keys, keys, (3, 3, 3), (1, 1, 1), 0)[2]
+    ref_conv = orc.conv_os(m, T, Xn, W.double().numpy())
+    epi = (scale.to(dev), shift.to(dev), res.to(dev), True)
+    y = F.sparse_convolution_forward_os(S, T, _t(m, dev), A.to(dev), W.to(dev), epilogue=epi, sources2=B.to(dev))
+    assert rel_err(np_(y.float()), _ref(ref_conv, scale, shift, res, True)) <= TOL[torch.float16]
+    # the 1x1x1 path
+    ident = np.arange(T, dtype=np.int32).reshape(T, 1)
+    ref_dense = orc.conv_os(ident, T, Xn, W[:1].double().numpy())
+    yd = F.dense_forward(A.to(dev), W[:1].to(dev), sources2=B.to(dev))
+    assert rel_err(np_(yd.float()), ref_dense) <= TOL[torch.float16]
+
+
+def test_lazy_cat_materialises_on_access(dev):
+    a = spira_amd.SparseTensor(coordinates=torch.zeros(10, dtype=torch.int64, device=dev),
+                               features=torch.randn(10, 32, device=dev).half())
+    b = spira_amd.SparseTensor(coordinates=a.coordinates, features=torch.randn(10, 16, device=dev).half())
+    c = spira_amd.cat([a, b])
+    assert c._parts is not None
+    assert torch.equal(c.features, torch.cat([a.features, b.features], 1))
+    assert c._parts is None
+    # splits off a 16-channel slice and fp32 parts are concatenated right away
+    e = spira_amd.SparseTensor(coordinates=a.coordinates, features=torch.randn(10, 24, device=dev).half())
+    d = spira_amd.cat([e, b])
+    assert d._parts is None and d.features.shape == (10, 40)
+    f = spira_amd.SparseTensor(coordinates=a.coordinates, features=torch.randn(10, 32, device=dev))
+    assert spira_amd.cat([f, f])._parts is None
