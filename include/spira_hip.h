@@ -133,6 +133,22 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
                              uint64_t *group_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
+/* Workspace bytes for spira_hip_voxelize. */
+int spira_hip_voxelize_workspace(int64_t num_points, size_t *bytes);
+
+/* Voxelization front-end: coords = floor(points / voxel) in float64 (points
+ * [num_points, 3] float32, or float64 with points_f64), then the first point
+ * of every value of x*73856093 ^ y*19349663 ^ z*83492791 (the coordinates
+ * cast to uint64; distinct voxels with colliding hashes collapse to the
+ * first), sorted lexicographically by (x, y, z).  The *count (device) first
+ * rows of coords [num_points, 3] int32 are the result; the count is written
+ * on the stream (no host synchronisation).  Voxels at x = y = z = INT32_MAX
+ * are not supported (the sentinel).  (reference: sparse_quantize and
+ * ravel_hash, datasets/helpers.py:8-30.) */
+int spira_hip_voxelize(const void *points, int64_t num_points, int points_f64, double vx, double vy, double vz,
+                       int32_t *coords, uint32_t *count, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
 /* ptr[0..n) = value (reference: the cudaMemsetAsync(-1) mask initialisation,
  * cuda/functions/query_sorted_index.cu:475-477). */
 int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t stream);

@@ -14,6 +14,7 @@ dtypes and tuple layouts as the reference's ``_C`` entry points:
 * ``build_kmap``        -- torch/cuda_sparse_convolution_mapping.cu:211-892
 * ``build_kmap_no_small_z`` -- torch/cuda_sparse_convolution_mapping.cu:1647-1690
 * ``convert_transposed_os`` -- torch/cuda_sparse_convolution_mapping.cu:1809-1830
+* ``sparse_quantize``   -- datasets/helpers.py:8-31 (voxelization front-end)
 * ``conv_*``            -- float64 feature sums with each dataflow's semantics
   (cuda/functions/sparse_convolution.cu, kernels/output_stat.cuh, weight_stat.cuh)
 
@@ -160,6 +161,26 @@ def downsample(keys: np.ndarray, stride) -> np.ndarray:
     m = np.uint64(downsample_mask(bits, stride))
     u = np.unique(to_u64(keys) & m)
     return from_u64(u, bits)
+
+
+def ravel_hash(coords: np.ndarray) -> np.ndarray:
+    """x*73856093 ^ y*19349663 ^ z*83492791 over the int32 coordinates
+    sign-extended to uint64, products modulo 2^64 (datasets/helpers.py:8-12)."""
+    u = np.asarray(coords, dtype=np.int32).astype(np.int64).view(np.uint64)
+    with np.errstate(over="ignore"):
+        return (u[:, 0] * np.uint64(73856093)) ^ (u[:, 1] * np.uint64(19349663)) ^ (u[:, 2] * np.uint64(83492791))
+
+
+def sparse_quantize(points: np.ndarray, voxel_size=1.0, hash_fn=ravel_hash) -> np.ndarray:
+    """floor(points / voxel_size) in float64 cast to int32; the first point of
+    every hash value is kept; the kept voxels are sorted by (x, y, z)
+    (datasets/helpers.py:14-31).  ``hash_fn`` exists so that tests can force
+    hash collisions."""
+    v = np.broadcast_to(np.asarray(voxel_size, dtype=np.float64), (3,))
+    c = np.floor(np.asarray(points).astype(np.float64) / v).astype(np.int32).reshape(-1, 3)
+    _, first = np.unique(hash_fn(c), return_index=True)
+    c = c[first]
+    return c[np.lexsort((c[:, 2], c[:, 1], c[:, 0]))]
 
 
 # ----------------------------------------------------------------------------

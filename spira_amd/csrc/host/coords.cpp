@@ -102,7 +102,31 @@ std::vector<torch::Tensor> streamed_output_generate(const torch::Tensor &keys, c
   return res;
 }
 
+// GPU voxelization (reference: sparse_quantize, datasets/helpers.py:14-30):
+// points [N, 3] float32 / float64 on the device -> sorted unique voxel
+// coordinates [M, 3] int32 (one host read of M).
+torch::Tensor voxelize(const torch::Tensor &points, double vx, double vy, double vz) {
+  require_device(points, "points");
+  SPIRA_CHECK_ARG(points.dim() == 2 && points.size(1) == 3, "points must be [N, 3]");
+  SPIRA_CHECK_ARG(points.scalar_type() == torch::kFloat || points.scalar_type() == torch::kDouble,
+                  "points must be float32 or float64");
+  auto p = points.contiguous();
+  const int64_t n = p.size(0);
+  auto coords = empty_i32({std::max<int64_t>(n, 1), 3}, p.device());
+  auto count = torch::zeros({1}, torch::TensorOptions(p.device()).dtype(torch::kInt32));
+  size_t wsb = 0;
+  check_rc(spira_hip_voxelize_workspace(n, &wsb), "voxelize");
+  auto ws = workspace(wsb, p.device());
+  check_rc(spira_hip_voxelize(p.data_ptr(), n, p.scalar_type() == torch::kDouble ? 1 : 0, vx, vy, vz,
+                              coords.data_ptr<int32_t>(), reinterpret_cast<uint32_t *>(count.data_ptr<int32_t>()),
+                              wsb ? ws.data_ptr() : nullptr, wsb, current_stream()),
+           "voxelize");
+  const int64_t m = count.cpu().item<int32_t>();
+  return coords.slice(0, 0, m);
+}
+
 void register_coords(pybind11::module_ &m) {
+  m.def("voxelize", &voxelize);
   m.def("cuda_flatten_sort", &flatten_sort);
   m.def("cuda_unflatten", &unflatten);
   m.def("cuda_downsample", &downsample);

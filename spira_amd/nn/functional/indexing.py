@@ -16,13 +16,23 @@ from ._native import _C
 
 __all__ = [
     "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os",
-    "build_kmap_streamed", "streamed_output_generate", "build_kmap_no_small_z",
+    "build_kmap_streamed", "streamed_output_generate", "build_kmap_no_small_z", "sparse_quantize",
 ]
 
 
 def _require_gpu(t: torch.Tensor) -> None:
     if not t.is_cuda:
         raise NotImplementedError("spira_amd runs on the GPU only")
+
+
+def sparse_quantize(points: torch.Tensor, voxel_size: ScalarOrTuple[float] = 1.0) -> torch.Tensor:
+    """Voxelize ``[N, 3]`` float32 / float64 points on the GPU: floor(points /
+    voxel_size), one voxel per value of the reference's coordinate hash (its
+    first point), sorted lexicographically; returns ``[M, 3] int32`` (reference:
+    sparse_quantize, datasets/helpers.py:14-30, which does this on the host)."""
+    _require_gpu(points)
+    vx, vy, vz = (float(v) for v in as_tuple(voxel_size, size=3, name="voxel_size"))
+    return _C.voxelize(points, vx, vy, vz)
 
 
 def flat_sort(coordinates: torch.Tensor, double: bool = False):

@@ -333,3 +333,68 @@ def test_dataflows_agree_in_float64():
         else:
             y = orc.conv_ws_gs(S, T, X, Wh, m[3], m[4], woffset=dense, Y=y)
         assert np.allclose(y, full, atol=1e-12), d
+
+
+# ---------------------------------------------------------------- voxelization
+
+def test_ravel_hash_matches_python_integers():
+    """Hash of negative coordinates: int32 -> uint64 sign extension and
+    products modulo 2^64, computed here with unbounded Python integers."""
+    r = np.random.default_rng(11)
+    c = np.concatenate([r.integers(-2**31, 2**31, size=(200, 3)),
+                        [[-1, -1, -1], [0, 0, 0], [2**31 - 1, -2**31, 5]]]).astype(np.int32)
+    h = orc.ravel_hash(c)
+    m = (1 << 64) - 1
+    for row, got in zip(c.tolist(), h.tolist()):
+        x, y, z = (v & m for v in row)
+        assert got == ((x * 73856093) & m) ^ ((y * 19349663) & m) ^ ((z * 83492791) & m)
+
+
+def _quantize_py(pts, vs):
+    """Brute force with Python integers: walk the points in order, keep the
+    first voxel of every hash value, sort the kept voxels as tuples."""
+    import math
+    m = (1 << 64) - 1
+    kept = {}
+    for row in pts.tolist():
+        v = tuple(math.floor(float(p) / s) for p, s in zip(row, vs))
+        x, y, z = (a & m for a in v)
+        h = ((x * 73856093) & m) ^ ((y * 19349663) & m) ^ ((z * 83492791) & m)
+        kept.setdefault(h, v)
+    return sorted(kept.values())
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_sparse_quantize_matches_brute_force(dtype):
+    """Small signed coordinates collide under this hash often (about one
+    voxel in seven here), so the collision rule is exercised, not just the
+    sorted floor set."""
+    r = np.random.default_rng(12)
+    pts = r.uniform(-7.5, 7.5, size=(3000, 3)).astype(dtype)
+    vs = (0.5, 0.75, 1.25)
+    got = orc.sparse_quantize(pts, vs)
+    assert got.dtype == np.int32 and got.tolist() == [list(t) for t in _quantize_py(pts, vs)]
+    floor_set = {tuple(t) for t in np.floor(pts.astype(np.float64) / np.array(vs)).astype(np.int64).tolist()}
+    assert len(got) < len(floor_set)  # collisions present
+
+
+def test_sparse_quantize_without_collisions_is_sorted_floor_set():
+    r = np.random.default_rng(13)
+    pts = r.uniform(0, 64, size=(2000, 3))
+    got = orc.sparse_quantize(pts, 1.0)
+    floor_set = sorted({tuple(t) for t in np.floor(pts).astype(np.int64).tolist()})
+    assert len(set(orc.ravel_hash(np.array(floor_set, dtype=np.int32)).tolist())) == len(floor_set)
+    assert got.tolist() == [list(t) for t in floor_set]
+
+
+def test_sparse_quantize_scalar_voxel_and_edges():
+    assert orc.sparse_quantize(np.zeros((0, 3)), 1.0).shape == (0, 3)
+    assert orc.sparse_quantize(np.array([[-0.5, 0.0, 2.0]]), 1.0).tolist() == [[-1, 0, 2]]
+    assert orc.sparse_quantize(np.array([[1.0, 1.0, 1.0]]), 0.5).tolist() == [[2, 2, 2]]
+
+
+def test_sparse_quantize_collision_keeps_first_point():
+    """Colliding voxels collapse to the one whose point comes first."""
+    pts = np.array([[5, 0, 0], [1, 0, 0], [3, 0, 0], [2, 0, 0]], dtype=np.float64)
+    got = orc.sparse_quantize(pts, 1.0, hash_fn=lambda c: (c[:, 0] % 2).astype(np.uint64))
+    assert got.tolist() == [[2, 0, 0], [5, 0, 0]]
