@@ -48,14 +48,39 @@ int spira_hip_flatten_sort_workspace(int64_t n, int key_bits, size_t *bytes);
 int spira_hip_flatten_sort(const int32_t *coords, int64_t n, int key_bits, void *keys_out, int32_t *perm_out,
                            void *workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes for spira_hip_downsample. */
+/* Workspace bytes for spira_hip_downsample, _plan and _execute. */
 int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes);
 
 /* out = sorted unique (keys & stride mask); *d_count (device) = number of
- * unique keys.  Strides must be powers of two (reference: cuda_downsample,
- * torch/cuda_arg_sort_coordinates.cu:68-105; SortUnique arg_sort_coodrinates.cu:139-192). */
+ * unique keys.  Strides must be powers of two.  Blocks once on `stream` to
+ * read the plan (below); the count stays on the device (reference:
+ * cuda_downsample, torch/cuda_arg_sort_coordinates.cu:68-105; SortUnique
+ * arg_sort_coodrinates.cu:139-192). */
 int spira_hip_downsample(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz, void *out_keys,
                          uint32_t *d_count, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* The two halves of spira_hip_downsample, so that a caller downsampling one
+ * key set to several strides reads every plan with one host synchronisation
+ * (reference: cuda_streamed_output_generate, torch/cuda_arg_sort_coordinates.cu:107-200).
+ * _plan (n > 0) writes the record below to device memory and fills the
+ * workspace's segment tables; _execute takes a host copy of that record and
+ * the same workspace, untouched in between.  Sorted keys whose runs of equal
+ * masked x hold at most 32768 keys take the segmented path; any other input
+ * takes the general sort + unique path.  Same result either way. */
+typedef struct spira_hip_downsample_plan {
+  uint32_t unsorted;     /* some key is smaller than its predecessor          */
+  uint32_t num_segments; /* runs of equal masked x                            */
+  uint32_t max_segment;  /* keys in the longest run                           */
+  uint32_t reserved;
+  uint64_t varying;      /* OR over all keys of (masked key ^ first masked key) */
+} spira_hip_downsample_plan_t;
+
+int spira_hip_downsample_plan(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz,
+                              spira_hip_downsample_plan_t *plan, void *workspace, size_t workspace_bytes,
+                              hipStream_t stream);
+int spira_hip_downsample_execute(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz,
+                                 const spira_hip_downsample_plan_t *plan, void *out_keys, uint32_t *d_count,
+                                 void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ----------------------------------------------------------- kernel maps */
 

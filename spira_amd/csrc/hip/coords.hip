@@ -2,7 +2,7 @@
 //
 // Reference semantics: compress.cuh:9-46 (pack/unpack),
 // arg_sort_coodrinates.cu:36-192 (sort, sort+unique),
-// torch/cuda_arg_sort_coordinates.cu:68-200 (downsample masks).
+// (stride downsampling: downsample.hip).
 #include "common.hpp"
 #include "../../../include/spira_hip.h"
 
@@ -64,21 +64,6 @@ __global__ void unpack_kernel(int64_t n, const CT *__restrict__ keys, int32_t *_
   c[2] = static_cast<int32_t>(k & Layout<CT>::ZONES);
 }
 
-template <typename CT>
-__global__ void mask_kernel(int64_t n, const CT *__restrict__ in, CT mask, CT *__restrict__ out) {
-  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  out[i] = in[i] & mask;
-}
-
-template <typename CT> CT stride_mask(int sx, int sy, int sz) {
-  // per-axis clear of the low log2(stride) bits (torch/cuda_arg_sort_coordinates.cu:86-89)
-  CT xm = Layout<CT>::XONES & ~static_cast<CT>(static_cast<uint32_t>(sx - 1));
-  CT ym = Layout<CT>::YONES & ~static_cast<CT>(static_cast<uint32_t>(sy - 1));
-  CT zm = Layout<CT>::ZONES & ~static_cast<CT>(static_cast<uint32_t>(sz - 1));
-  return static_cast<CT>((xm << Layout<CT>::XS) | (ym << Layout<CT>::YS) | zm);
-}
-
 static inline bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 // ---------------------------------------------------------------------------
@@ -92,23 +77,10 @@ template <typename CT> static size_t sort_temp_bytes(int64_t n) {
   return bytes;
 }
 
-template <typename CT> static size_t unique_temp_bytes(int64_t n) {
-  size_t sort_b = 0, uniq_b = 0;
-  (void)rocprim::radix_sort_keys(nullptr, sort_b, static_cast<const CT *>(nullptr), static_cast<CT *>(nullptr),
-                           static_cast<size_t>(n), 0, 8 * sizeof(CT));
-  (void)rocprim::unique(nullptr, uniq_b, static_cast<const CT *>(nullptr), static_cast<CT *>(nullptr),
-                  static_cast<uint32_t *>(nullptr), static_cast<size_t>(n));
-  return sort_b > uniq_b ? sort_b : uniq_b;
-}
-
 static inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 template <typename CT> static size_t flatten_ws(int64_t n) {
   return align256(n * sizeof(CT)) + align256(n * sizeof(int32_t)) + align256(sort_temp_bytes<CT>(n));
-}
-
-template <typename CT> static size_t downsample_ws(int64_t n) {
-  return 2 * align256(n * sizeof(CT)) + align256(unique_temp_bytes<CT>(n));
 }
 
 template <typename CT>
@@ -127,33 +99,6 @@ static int flatten_sort_impl(const int32_t *coords, int64_t n, CT *keys_out, int
   SPIRA_HIP_LAUNCH_CHECK();
   SPIRA_HIP_TRY(rocprim::radix_sort_pairs(p, tb, keys_in, keys_out, iota, perm_out, static_cast<size_t>(n), 0,
                                           8 * sizeof(CT), s));
-  return kOk;
-}
-
-template <typename CT>
-static int downsample_impl(const CT *keys, int64_t n, int sx, int sy, int sz, CT *out, uint32_t *d_count,
-                           void *ws, size_t ws_bytes, hipStream_t s) {
-  SPIRA_HIP_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "downsample: n out of range");
-  SPIRA_HIP_REQUIRE(is_pow2(sx) && is_pow2(sy) && is_pow2(sz), "downsample: strides must be powers of two");
-  if (n == 0) {
-    SPIRA_HIP_TRY(hipMemsetAsync(d_count, 0, sizeof(uint32_t), s));
-    return kOk;
-  }
-  SPIRA_HIP_REQUIRE(ws != nullptr && ws_bytes >= downsample_ws<CT>(n), "downsample: workspace too small");
-  char *p = static_cast<char *>(ws);
-  CT *masked = reinterpret_cast<CT *>(p);
-  p += align256(n * sizeof(CT));
-  CT *sorted = reinterpret_cast<CT *>(p);
-  p += align256(n * sizeof(CT));
-  size_t tb = unique_temp_bytes<CT>(n);
-  hipLaunchKernelGGL(mask_kernel<CT>, dim3(div_up(n, 256)), dim3(256), 0, s, n, keys,
-                     stride_mask<CT>(sx, sy, sz), masked);
-  SPIRA_HIP_LAUNCH_CHECK();
-  size_t b = tb;
-  SPIRA_HIP_TRY(rocprim::radix_sort_keys(p, b, masked, sorted, static_cast<size_t>(n), 0, 8 * sizeof(CT), s));
-  b = tb;
-  SPIRA_HIP_TRY(rocprim::unique(p, b, sorted, out, d_count, static_cast<size_t>(n),
-                                rocprim::equal_to<CT>(), s));
   return kOk;
 }
 
@@ -205,24 +150,6 @@ int spira_hip_flatten_sort(const int32_t *coords, int64_t n, int key_bits, void 
                                        workspace_bytes, stream);
   return flatten_sort_impl<uint32_t>(coords, n, static_cast<uint32_t *>(keys_out), perm_out, workspace,
                                      workspace_bytes, stream);
-}
-
-int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes) {
-  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample: key_bits must be 32 or 64");
-  *bytes = n <= 0 ? 0 : (key_bits == 64 ? downsample_ws<uint64_t>(n) : downsample_ws<uint32_t>(n));
-  return kOk;
-}
-
-int spira_hip_downsample(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz, void *out_keys,
-                         uint32_t *d_count, void *workspace, size_t workspace_bytes, hipStream_t stream) {
-  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample: key_bits must be 32 or 64");
-  if (key_bits == 64)
-    return downsample_impl<uint64_t>(static_cast<const uint64_t *>(keys), n, sx, sy, sz,
-                                     static_cast<uint64_t *>(out_keys), d_count, workspace, workspace_bytes,
-                                     stream);
-  return downsample_impl<uint32_t>(static_cast<const uint32_t *>(keys), n, sx, sy, sz,
-                                   static_cast<uint32_t *>(out_keys), d_count, workspace, workspace_bytes,
-                                   stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,581 @@
+// Stride downsampling of packed voxel keys: sorted unique (key & stride mask).
+//
+// Reference semantics: torch/cuda_arg_sort_coordinates.cu:68-105 (mask every
+// key with the per-axis stride mask, sort, unique) and :107-200 (one such
+// downsample per target stride).
+//
+// Sorted input (the usual case: the keys of an ordered tensor) makes the
+// masked keys sorted by their x field already: every run of keys with equal
+// masked x ("segment") is contiguous, and only the (y, z) part inside a
+// segment needs sorting.  The segmented path:
+//   plan:    ds_tiles_kernel   per 1024-key tile: segment-start count, OR of
+//                              the masked keys' varying bits, sortedness,
+//                              longest segment starting in the tile;
+//            ds_starts_kernel  segment starts in key order (one block per
+//                              tile) + block 0 reduces the tiles into the plan;
+//   (the host reads the plan: a few bytes)
+//   execute: ds_segment_kernel one 1024-thread block per segment: the
+//                              segment's varying bits as 32- or 64-bit sort
+//                              keys in registers, stable LDS radix passes of
+//                              8 bits (ballot-built peer masks for the ranks),
+//                              then unique + compaction;
+//            ds_offsets_kernel exclusive scan of the per-segment counts;
+//            ds_copy_kernel    segments into the output.
+// Unsorted input, or a segment longer than the largest block tile, takes the
+// general path: mask, device-wide radix sort (rocPRIM), unique.
+#include "common.hpp"
+#include "../../../include/spira_hip.h"
+
+#include <rocprim/rocprim.hpp>
+
+namespace spira_hip {
+
+template <typename CT>
+__global__ void mask_kernel(int64_t n, const CT *__restrict__ in, CT mask, CT *__restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = in[i] & mask;
+}
+
+template <typename CT> CT stride_mask(int sx, int sy, int sz) {
+  // per-axis clear of the low log2(stride) bits (torch/cuda_arg_sort_coordinates.cu:86-89)
+  CT xm = Layout<CT>::XONES & ~static_cast<CT>(static_cast<uint32_t>(sx - 1));
+  CT ym = Layout<CT>::YONES & ~static_cast<CT>(static_cast<uint32_t>(sy - 1));
+  CT zm = Layout<CT>::ZONES & ~static_cast<CT>(static_cast<uint32_t>(sz - 1));
+  return static_cast<CT>((xm << Layout<CT>::XS) | (ym << Layout<CT>::YS) | zm);
+}
+
+// bits of the x field kept by the mask: a contiguous top range, so the keys
+// of one segment are exactly the key interval [h, h | ~xmask]
+template <typename CT> CT x_keep_mask(CT mask) {
+  return mask & static_cast<CT>(Layout<CT>::XONES << Layout<CT>::XS);
+}
+
+static inline bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+static inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+constexpr int kTile = 1024;       // keys per plan tile (256 threads x 4)
+constexpr int kSegThreads = 1024;  // threads of a segment block
+
+__global__ void zero_count_kernel(uint32_t *c) { *c = 0; }
+
+// ---------------------------------------------------------------------------
+// plan
+// ---------------------------------------------------------------------------
+template <typename CT>
+__global__ __launch_bounds__(256) void ds_tiles_kernel(const CT *__restrict__ keys, int64_t n, CT mask, CT xmask,
+                                                       uint32_t *__restrict__ tile_starts,
+                                                       CT *__restrict__ tile_vary,
+                                                       uint32_t *__restrict__ tile_flags) {
+  __shared__ uint32_t s_cnt, s_unsorted, s_maxseg;
+  __shared__ CT s_vary[4];
+  const int tid = threadIdx.x;
+  if (tid == 0) s_cnt = 0, s_unsorted = 0, s_maxseg = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  const CT m0 = keys[0] & mask;
+  CT vary = 0;
+  uint32_t cnt = 0, unsorted = 0, maxseg = 0;
+#pragma unroll
+  for (int j = 0; j < kTile / 256; ++j) {
+    const int64_t i = base + j * 256 + tid;
+    if (i < n) {
+      const CT k = keys[i];
+      vary |= (k & mask) ^ m0;
+      const bool start = i == 0 || (keys[i - 1] & xmask) != (k & xmask);
+      if (i > 0 && keys[i - 1] > k) unsorted = 1;
+      if (start) {
+        ++cnt;
+        // segment end: first key above the segment's key interval (exact when
+        // the keys are sorted; otherwise the plan is rejected on `unsorted`)
+        const CT hi = (k & xmask) | static_cast<CT>(~xmask);
+        int64_t lo = i + 1, up = n;
+        while (lo < up) {
+          const int64_t mid = (lo + up) >> 1;
+          if (keys[mid] <= hi) lo = mid + 1; else up = mid;
+        }
+        const int64_t len = lo - i;
+        const uint32_t l32 = len > 0x7FFFFFFF ? 0x7FFFFFFFu : static_cast<uint32_t>(len);
+        maxseg = l32 > maxseg ? l32 : maxseg;
+      }
+    }
+  }
+  // block reductions
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    vary |= static_cast<CT>(__shfl_xor(vary, o, 64));
+    cnt += __shfl_xor(cnt, o, 64);
+    unsorted |= __shfl_xor(unsorted, o, 64);
+    const uint32_t m = __shfl_xor(maxseg, o, 64);
+    maxseg = m > maxseg ? m : maxseg;
+  }
+  if (lane_id() == 0) {
+    s_vary[tid >> 6] = vary;
+    atomicAdd(&s_cnt, cnt);
+    atomicOr(&s_unsorted, unsorted);
+    atomicMax(&s_maxseg, maxseg);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    tile_starts[blockIdx.x] = s_cnt;
+    tile_vary[blockIdx.x] = s_vary[0] | s_vary[1] | s_vary[2] | s_vary[3];
+    tile_flags[2 * blockIdx.x] = s_unsorted;
+    tile_flags[2 * blockIdx.x + 1] = s_maxseg;
+  }
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void ds_starts_kernel(const CT *__restrict__ keys, int64_t n, CT xmask,
+                                                        int64_t ntiles, const uint32_t *__restrict__ tile_starts,
+                                                        const CT *__restrict__ tile_vary,
+                                                        const uint32_t *__restrict__ tile_flags,
+                                                        uint32_t *__restrict__ seg_start,
+                                                        spira_hip_downsample_plan_t *__restrict__ plan) {
+  __shared__ uint32_t s_wave[4][kTile / 256];
+  __shared__ uint64_t s_red[4][4];
+  const int tid = threadIdx.x, w = tid >> 6;
+  const int64_t t = blockIdx.x;
+  // segments starting before this tile
+  uint64_t before = 0;
+  for (int64_t u = tid; u < t; u += 256) before += tile_starts[u];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o, 64);
+  if (lane_id() == 0) s_red[0][w] = before;
+  // starts of this tile, ranked in key order (round j, then wave, then lane)
+  const int64_t base = t * kTile;
+  bool st[kTile / 256];
+  int pre[kTile / 256];
+#pragma unroll
+  for (int j = 0; j < kTile / 256; ++j) {
+    const int64_t i = base + j * 256 + tid;
+    st[j] = i < n && (i == 0 || (keys[i - 1] & xmask) != (keys[i] & xmask));
+    const uint64_t b = ballot(st[j]);
+    pre[j] = lane_prefix(b);
+    if (lane_id() == 0) s_wave[w][j] = __popcll(b);
+  }
+  __syncthreads();
+  const uint64_t off0 = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+#pragma unroll
+  for (int j = 0; j < kTile / 256; ++j) {
+    if (!st[j]) continue;
+    uint64_t off = off0;
+    for (int jj = 0; jj < j; ++jj) off += s_wave[0][jj] + s_wave[1][jj] + s_wave[2][jj] + s_wave[3][jj];
+    for (int ww = 0; ww < w; ++ww) off += s_wave[ww][j];
+    seg_start[off + pre[j]] = static_cast<uint32_t>(base + j * 256 + tid);
+  }
+  if (t != 0) return;
+  // block 0: the plan
+  uint64_t nseg = 0;
+  CT vary = 0;
+  uint32_t unsorted = 0, maxseg = 0;
+  for (int64_t u = tid; u < ntiles; u += 256) {
+    nseg += tile_starts[u];
+    vary |= tile_vary[u];
+    unsorted |= tile_flags[2 * u];
+    maxseg = tile_flags[2 * u + 1] > maxseg ? tile_flags[2 * u + 1] : maxseg;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    nseg += __shfl_xor(nseg, o, 64);
+    vary |= static_cast<CT>(__shfl_xor(vary, o, 64));
+    unsorted |= __shfl_xor(unsorted, o, 64);
+    const uint32_t m = __shfl_xor(maxseg, o, 64);
+    maxseg = m > maxseg ? m : maxseg;
+  }
+  __syncthreads();
+  if (lane_id() == 0) {
+    s_red[1][w] = nseg;
+    s_red[2][w] = static_cast<uint64_t>(vary);
+    s_red[3][w] = (static_cast<uint64_t>(unsorted) << 32) | maxseg;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t ns = 0, vy = 0;
+    uint32_t us = 0, ms = 0;
+    for (int q = 0; q < 4; ++q) {
+      ns += s_red[1][q];
+      vy |= s_red[2][q];
+      us |= static_cast<uint32_t>(s_red[3][q] >> 32);
+      const uint32_t m = static_cast<uint32_t>(s_red[3][q]);
+      ms = m > ms ? m : ms;
+    }
+    plan->unsorted = us;
+    plan->num_segments = static_cast<uint32_t>(ns);
+    plan->max_segment = ms;
+    plan->reserved = 0;
+    plan->varying = vy;
+    seg_start[ns] = static_cast<uint32_t>(n);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// execute
+// ---------------------------------------------------------------------------
+template <typename KT> __device__ __forceinline__ uint32_t digit_of(KT k, int shift) {
+  return static_cast<uint32_t>(k >> shift) & 255u;
+}
+
+// One block per segment.  Sort key: bits [lo, lo + nbits) of the masked key
+// (the bits that vary over the whole input below the x field; every other
+// bit is constant inside a segment).  Item j of lane l in wave w holds
+// segment position w*C + j*64 + l (C = ITEMS*64): position order is
+// (wave, round, lane), which the ranks keep (stable LSD passes).
+template <typename CT, typename KT, int ITEMS>
+__global__ __launch_bounds__(kSegThreads) void ds_segment_kernel(const CT *__restrict__ keys, CT mask, int lo,
+                                                                 int nbits, const uint32_t *__restrict__ seg_start,
+                                                                 CT *__restrict__ tmp,
+                                                                 uint32_t *__restrict__ seg_count) {
+  constexpr int W = kSegThreads / 64, C = ITEMS * 64;
+  __shared__ KT buf[W * C];
+  __shared__ uint32_t cnt[W][256];
+  __shared__ uint32_t dbase[256];
+  __shared__ uint32_t wsum[W];
+  const int tid = threadIdx.x, w = tid >> 6, lane = lane_id();
+  const int64_t s = blockIdx.x;
+  const int64_t start = seg_start[s];
+  const int len = static_cast<int>(seg_start[s + 1] - start);
+  // rounds of this wave holding segment positions
+  int rounds = (len - w * C + 63) >> 6;
+  rounds = rounds < 0 ? 0 : (rounds > ITEMS ? ITEMS : rounds);
+  const KT rmask = nbits >= static_cast<int>(8 * sizeof(KT)) ? static_cast<KT>(~KT(0))
+                                                             : static_cast<KT>((KT(1) << nbits) - 1);
+  KT key[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const int p = w * C + j * 64 + lane;
+    key[j] = p < len ? static_cast<KT>(((keys[start + p] & mask) >> lo)) & rmask : static_cast<KT>(~KT(0));
+  }
+  const int npass = (nbits + 7) >> 3;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int shift = 8 * pass;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cnt[w][lane + 64 * q] = 0;
+    uint32_t rank[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      if (j < rounds) {
+        const uint32_t d = digit_of(key[j], shift);
+        uint64_t peers = ~uint64_t(0);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const uint64_t bb = ballot((d >> b) & 1u);
+          peers &= ((d >> b) & 1u) ? bb : ~bb;
+        }
+        const int lower = lane_prefix(peers);
+        const uint32_t prev = cnt[w][d];
+        rank[j] = prev + lower;
+        if (lower == 0) cnt[w][d] = prev + __popcll(peers);
+      }
+    }
+    __syncthreads();
+    if (tid < 256) {
+      // exclusive over waves per digit, then over digits
+      uint32_t run = 0;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) {
+        const uint32_t c = cnt[ww][tid];
+        cnt[ww][tid] = run;
+        run += c;
+      }
+      uint32_t inc = run;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+      }
+      if (lane == 63) wsum[w] = inc;
+      dbase[tid] = inc - run;
+    }
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t add = 0;
+      for (int ww = 0; ww < w; ++ww) add += wsum[ww];
+      dbase[tid] += add;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      if (j < rounds) {
+        const uint32_t d = digit_of(key[j], shift);
+        buf[dbase[d] + cnt[w][d] + rank[j]] = key[j];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      if (j < rounds) key[j] = buf[w * C + j * 64 + lane];
+    __syncthreads();
+  }
+  // unique + compaction in position order
+  if (npass == 0) {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      if (j < rounds) buf[w * C + j * 64 + lane] = key[j];
+    __syncthreads();
+  }
+  bool head[ITEMS];
+  uint32_t total = 0;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const int p = w * C + j * 64 + lane;
+    head[j] = j < rounds && p < len && (p == 0 || buf[p - 1] != key[j]);
+    total += __popcll(ballot(head[j]));
+  }
+  if (lane == 0) wsum[w] = total;
+  __syncthreads();
+  uint32_t out = 0;
+  for (int ww = 0; ww < w; ++ww) out += wsum[ww];
+  const CT keep = static_cast<CT>(~(static_cast<CT>(rmask) << lo));
+  const CT hi_bits = (keys[start] & mask) & keep;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint64_t b = ballot(head[j]);
+    if (head[j]) tmp[start + out + lane_prefix(b)] = hi_bits | (static_cast<CT>(key[j]) << lo);
+    out += __popcll(b);
+  }
+  if (tid == 0) {
+    uint32_t all = 0;
+    for (int ww = 0; ww < W; ++ww) all += wsum[ww];
+    seg_count[s] = all;
+  }
+}
+
+// exclusive scan of the segment counts (one block); total -> *d_count
+__global__ __launch_bounds__(1024) void ds_offsets_kernel(const uint32_t *__restrict__ seg_count, int64_t nseg,
+                                                          uint32_t *__restrict__ seg_off,
+                                                          uint32_t *__restrict__ d_count) {
+  __shared__ uint32_t wsum[16];
+  __shared__ uint32_t carry;
+  const int tid = threadIdx.x, w = tid >> 6, lane = lane_id();
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int64_t b = 0; b < nseg; b += 1024) {
+    const int64_t i = b + tid;
+    const uint32_t v = i < nseg ? seg_count[i] : 0;
+    uint32_t inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t u = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += u;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    uint32_t add = carry;
+    for (int ww = 0; ww < w; ++ww) add += wsum[ww];
+    if (i < nseg) seg_off[i] = add + inc - v;
+    __syncthreads();
+    if (tid == 1023) carry = add + inc;
+    __syncthreads();
+  }
+  if (tid == 0) *d_count = carry;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void ds_copy_kernel(const CT *__restrict__ tmp,
+                                                      const uint32_t *__restrict__ seg_start,
+                                                      const uint32_t *__restrict__ seg_count,
+                                                      const uint32_t *__restrict__ seg_off, CT *__restrict__ out) {
+  const int64_t s = blockIdx.x;
+  const int64_t src = seg_start[s], dst = seg_off[s];
+  const uint32_t c = seg_count[s];
+  for (uint32_t i = threadIdx.x; i < c; i += 256) out[dst + i] = tmp[src + i];
+}
+
+// ---------------------------------------------------------------------------
+// workspace
+// ---------------------------------------------------------------------------
+template <typename CT> static size_t general_temp_bytes(int64_t n) {
+  size_t sort_b = 0, uniq_b = 0;
+  (void)rocprim::radix_sort_keys(nullptr, sort_b, static_cast<const CT *>(nullptr), static_cast<CT *>(nullptr),
+                                 static_cast<size_t>(n), 0, 8 * sizeof(CT));
+  (void)rocprim::unique(nullptr, uniq_b, static_cast<const CT *>(nullptr), static_cast<CT *>(nullptr),
+                        static_cast<uint32_t *>(nullptr), static_cast<size_t>(n));
+  return sort_b > uniq_b ? sort_b : uniq_b;
+}
+
+template <typename CT> struct DsParts {
+  spira_hip_downsample_plan_t *plan;  // used by the one-call entry point
+  uint32_t *tile_starts, *tile_flags, *seg_start, *seg_count, *seg_off;
+  CT *tile_vary, *tmp;
+  CT *masked, *sorted;  // general path
+  void *temp;
+  size_t temp_bytes, total;
+};
+
+template <typename CT> static DsParts<CT> ds_parts(int64_t n, void *base) {
+  DsParts<CT> p{};
+  const int64_t ntiles = div_up(n, kTile);
+  char *b = static_cast<char *>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char *q = b ? b + off : nullptr;
+    off += align256(bytes);
+    return q;
+  };
+  p.plan = reinterpret_cast<spira_hip_downsample_plan_t *>(take(sizeof(spira_hip_downsample_plan_t)));
+  p.tile_starts = reinterpret_cast<uint32_t *>(take(ntiles * sizeof(uint32_t)));
+  p.tile_flags = reinterpret_cast<uint32_t *>(take(2 * ntiles * sizeof(uint32_t)));
+  p.tile_vary = reinterpret_cast<CT *>(take(ntiles * sizeof(CT)));
+  p.seg_start = reinterpret_cast<uint32_t *>(take((n + 1) * sizeof(uint32_t)));
+  p.seg_count = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
+  p.seg_off = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
+  p.tmp = reinterpret_cast<CT *>(take(n * sizeof(CT)));
+  p.masked = reinterpret_cast<CT *>(take(n * sizeof(CT)));
+  p.sorted = reinterpret_cast<CT *>(take(n * sizeof(CT)));
+  p.temp_bytes = general_temp_bytes<CT>(n);
+  p.temp = take(p.temp_bytes);
+  p.total = off;
+  return p;
+}
+
+template <typename CT>
+static int check_args(int64_t n, int sx, int sy, int sz, void *ws, size_t ws_bytes, const char *who) {
+  SPIRA_HIP_REQUIRE(n >= 0 && n < (int64_t(1) << 31), std::string(who) + ": n out of range");
+  SPIRA_HIP_REQUIRE(is_pow2(sx) && is_pow2(sy) && is_pow2(sz), std::string(who) + ": strides must be powers of two");
+  if (n > 0)
+    SPIRA_HIP_REQUIRE(ws != nullptr && ws_bytes >= ds_parts<CT>(n, nullptr).total,
+                      std::string(who) + ": workspace too small");
+  return kOk;
+}
+
+template <typename CT>
+static int plan_impl(const CT *keys, int64_t n, int sx, int sy, int sz, spira_hip_downsample_plan_t *plan_dev,
+                     void *ws, size_t ws_bytes, hipStream_t s) {
+  if (int rc = check_args<CT>(n, sx, sy, sz, ws, ws_bytes, "downsample_plan")) return rc;
+  SPIRA_HIP_REQUIRE(plan_dev != nullptr, "downsample_plan: plan must not be null");
+  SPIRA_HIP_REQUIRE(n > 0, "downsample_plan: no keys");
+  DsParts<CT> p = ds_parts<CT>(n, ws);
+  const CT mask = stride_mask<CT>(sx, sy, sz), xmask = x_keep_mask<CT>(mask);
+  const int64_t ntiles = div_up(n, kTile);
+  hipLaunchKernelGGL(ds_tiles_kernel<CT>, dim3(static_cast<unsigned>(ntiles)), dim3(256), 0, s, keys, n, mask,
+                     xmask, p.tile_starts, p.tile_vary, p.tile_flags);
+  SPIRA_HIP_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ds_starts_kernel<CT>, dim3(static_cast<unsigned>(ntiles)), dim3(256), 0, s, keys, n, xmask,
+                     ntiles, p.tile_starts, p.tile_vary, p.tile_flags, p.seg_start, plan_dev);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+template <typename CT, typename KT, int ITEMS>
+static void launch_segments(const CT *keys, CT mask, int lo, int nbits, const DsParts<CT> &p, int64_t nseg,
+                            hipStream_t s) {
+  hipLaunchKernelGGL((ds_segment_kernel<CT, KT, ITEMS>), dim3(static_cast<unsigned>(nseg)), dim3(kSegThreads), 0, s,
+                     keys, mask, lo, nbits, p.seg_start, p.tmp, p.seg_count);
+}
+
+// largest segment each (key type, items) variant holds: 1024 threads x ITEMS
+template <typename CT>
+static int execute_impl(const CT *keys, int64_t n, int sx, int sy, int sz, const spira_hip_downsample_plan_t *plan,
+                        CT *out, uint32_t *d_count, void *ws, size_t ws_bytes, hipStream_t s) {
+  if (int rc = check_args<CT>(n, sx, sy, sz, ws, ws_bytes, "downsample")) return rc;
+  SPIRA_HIP_REQUIRE(d_count != nullptr, "downsample: count must not be null");
+  if (n == 0) {
+    hipLaunchKernelGGL(zero_count_kernel, dim3(1), dim3(1), 0, s, d_count);
+    SPIRA_HIP_LAUNCH_CHECK();
+    return kOk;
+  }
+  SPIRA_HIP_REQUIRE(plan != nullptr, "downsample: plan must not be null");
+  DsParts<CT> p = ds_parts<CT>(n, ws);
+  const CT mask = stride_mask<CT>(sx, sy, sz);
+  const int64_t nseg = plan->num_segments;
+  const uint64_t low = plan->varying & ((uint64_t(1) << Layout<CT>::XS) - 1);
+  const int lo = low ? __builtin_ctzll(low) : 0;
+  const int nbits = low ? 64 - __builtin_clzll(low) - lo : 0;
+  const uint32_t ms = plan->max_segment;
+  bool fast = !plan->unsorted && nseg >= 1 && nseg <= n;
+  if (fast) {
+    if (nbits <= 32) {
+      if (ms <= 4 * kSegThreads)
+        launch_segments<CT, uint32_t, 4>(keys, mask, lo, nbits, p, nseg, s);
+      else if (ms <= 16 * kSegThreads)
+        launch_segments<CT, uint32_t, 16>(keys, mask, lo, nbits, p, nseg, s);
+      else if (ms <= 32 * kSegThreads)
+        launch_segments<CT, uint32_t, 32>(keys, mask, lo, nbits, p, nseg, s);
+      else
+        fast = false;
+    } else {
+      if (ms <= 4 * kSegThreads)
+        launch_segments<CT, uint64_t, 4>(keys, mask, lo, nbits, p, nseg, s);
+      else if (ms <= 16 * kSegThreads)
+        launch_segments<CT, uint64_t, 16>(keys, mask, lo, nbits, p, nseg, s);
+      else
+        fast = false;
+    }
+  }
+  if (fast) {
+    SPIRA_HIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(ds_offsets_kernel, dim3(1), dim3(1024), 0, s, p.seg_count, nseg, p.seg_off, d_count);
+    SPIRA_HIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(ds_copy_kernel<CT>, dim3(static_cast<unsigned>(nseg)), dim3(256), 0, s, p.tmp, p.seg_start,
+                       p.seg_count, p.seg_off, out);
+    SPIRA_HIP_LAUNCH_CHECK();
+    return kOk;
+  }
+  // general path
+  hipLaunchKernelGGL(mask_kernel<CT>, dim3(div_up(n, 256)), dim3(256), 0, s, n, keys, mask, p.masked);
+  SPIRA_HIP_LAUNCH_CHECK();
+  size_t b = p.temp_bytes;
+  SPIRA_HIP_TRY(rocprim::radix_sort_keys(p.temp, b, p.masked, p.sorted, static_cast<size_t>(n), 0, 8 * sizeof(CT), s));
+  b = p.temp_bytes;
+  SPIRA_HIP_TRY(rocprim::unique(p.temp, b, p.sorted, out, d_count, static_cast<size_t>(n), rocprim::equal_to<CT>(), s));
+  return kOk;
+}
+
+template <typename CT>
+static int downsample_impl(const CT *keys, int64_t n, int sx, int sy, int sz, CT *out, uint32_t *d_count, void *ws,
+                           size_t ws_bytes, hipStream_t s) {
+  if (int rc = check_args<CT>(n, sx, sy, sz, ws, ws_bytes, "downsample")) return rc;
+  if (n == 0) return execute_impl<CT>(keys, n, sx, sy, sz, nullptr, out, d_count, ws, ws_bytes, s);
+  DsParts<CT> p = ds_parts<CT>(n, ws);
+  if (int rc = plan_impl<CT>(keys, n, sx, sy, sz, p.plan, ws, ws_bytes, s)) return rc;
+  spira_hip_downsample_plan_t h{};
+  SPIRA_HIP_TRY(hipMemcpyAsync(&h, p.plan, sizeof(h), hipMemcpyDeviceToHost, s));
+  SPIRA_HIP_TRY(hipStreamSynchronize(s));
+  return execute_impl<CT>(keys, n, sx, sy, sz, &h, out, d_count, ws, ws_bytes, s);
+}
+
+}  // namespace spira_hip
+
+using namespace spira_hip;
+
+extern "C" {
+
+int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample: key_bits must be 32 or 64");
+  *bytes = n <= 0 ? 0 : (key_bits == 64 ? ds_parts<uint64_t>(n, nullptr).total : ds_parts<uint32_t>(n, nullptr).total);
+  return kOk;
+}
+
+int spira_hip_downsample(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz, void *out_keys,
+                         uint32_t *d_count, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample: key_bits must be 32 or 64");
+  if (key_bits == 64)
+    return downsample_impl<uint64_t>(static_cast<const uint64_t *>(keys), n, sx, sy, sz,
+                                     static_cast<uint64_t *>(out_keys), d_count, workspace, workspace_bytes, stream);
+  return downsample_impl<uint32_t>(static_cast<const uint32_t *>(keys), n, sx, sy, sz,
+                                   static_cast<uint32_t *>(out_keys), d_count, workspace, workspace_bytes, stream);
+}
+
+int spira_hip_downsample_plan(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz,
+                              spira_hip_downsample_plan_t *plan, void *workspace, size_t workspace_bytes,
+                              hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample_plan: key_bits must be 32 or 64");
+  if (key_bits == 64)
+    return plan_impl<uint64_t>(static_cast<const uint64_t *>(keys), n, sx, sy, sz, plan, workspace, workspace_bytes,
+                               stream);
+  return plan_impl<uint32_t>(static_cast<const uint32_t *>(keys), n, sx, sy, sz, plan, workspace, workspace_bytes,
+                             stream);
+}
+
+int spira_hip_downsample_execute(const void *keys, int64_t n, int key_bits, int sx, int sy, int sz,
+                                 const spira_hip_downsample_plan_t *plan, void *out_keys, uint32_t *d_count,
+                                 void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample: key_bits must be 32 or 64");
+  if (key_bits == 64)
+    return execute_impl<uint64_t>(static_cast<const uint64_t *>(keys), n, sx, sy, sz, plan,
+                                  static_cast<uint64_t *>(out_keys), d_count, workspace, workspace_bytes, stream);
+  return execute_impl<uint32_t>(static_cast<const uint32_t *>(keys), n, sx, sy, sz, plan,
+                                static_cast<uint32_t *>(out_keys), d_count, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

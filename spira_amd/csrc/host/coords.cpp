@@ -3,6 +3,8 @@
 // Reference: torch/cuda_arg_sort_coordinates.cu:11-208.
 #include "host_common.h"
 
+#include <cstring>
+
 namespace spira_host {
 
 // (coords [N,3] int32, is_double) -> (sorted keys [N] int64|int32, perm [N] int32)
@@ -62,36 +64,52 @@ torch::Tensor downsample(const torch::Tensor &keys, int sx, int sy, int sz) {
   return out.slice(0, 0, nu);
 }
 
-// One downsample per target stride, each on its own pool stream, one host
-// read of all counts at the end (reference: CUDAStreamedOutputGenerate, :107-200).
+// One downsample per target stride: every plan on the current stream, one
+// host read of all plans, then each execution on its own pool stream, and
+// one host read of all counts at the end (reference:
+// CUDAStreamedOutputGenerate, :107-200).
 std::vector<torch::Tensor> streamed_output_generate(const torch::Tensor &keys, const std::vector<Int3> &strides) {
   SPIRA_CHECK_ARG(keys.dim() == 1, "coordinates should be already flattened");
   require_device(keys, "keys");
-  key_bits_of(keys);
+  const int bits = key_bits_of(keys);
   const auto dev = keys.device();
+  const int64_t n = keys.size(0);
   const size_t B = strides.size();
   auto counts = torch::zeros({static_cast<int64_t>(std::max<size_t>(B, 1))},
                              torch::TensorOptions(dev).dtype(torch::kInt32));
-  std::vector<torch::Tensor> outs;
+  constexpr int64_t PB = sizeof(spira_hip_downsample_plan_t);
+  auto plans = torch::empty({static_cast<int64_t>(std::max<size_t>(B, 1)) * PB},
+                            torch::TensorOptions(dev).dtype(torch::kUInt8));
   // outputs and workspaces are allocated on the current stream before the
   // fan-out; the current stream waits for every side stream afterwards
-  std::vector<torch::Tensor> wss;
-  std::vector<size_t> ws_sizes;
+  std::vector<torch::Tensor> outs, wss;
+  size_t wsb = 0;
+  check_rc(spira_hip_downsample_workspace(n, bits, &wsb), "downsample");
   for (size_t i = 0; i < B; ++i) {
     outs.push_back(torch::empty_like(keys));
-    size_t b = 0;
-    check_rc(spira_hip_downsample_workspace(keys.size(0), key_bits_of(keys), &b), "downsample");
-    ws_sizes.push_back(b);
-    wss.push_back(workspace(b, dev));
+    wss.push_back(workspace(wsb, dev));
+  }
+  std::vector<spira_hip_downsample_plan_t> hplans(B);
+  if (n > 0 && B > 0) {
+    for (size_t i = 0; i < B; ++i) {
+      auto [sx, sy, sz] = strides[i];
+      check_rc(spira_hip_downsample_plan(
+                   keys.data_ptr(), n, bits, sx, sy, sz,
+                   reinterpret_cast<spira_hip_downsample_plan_t *>(plans.data_ptr<uint8_t>() + i * PB),
+                   wss[i].data_ptr(), wsb, current_stream()),
+               "streamed_output_generate");
+    }
+    auto h = plans.cpu();
+    std::memcpy(hplans.data(), h.data_ptr<uint8_t>(), B * PB);
   }
   {
     StreamFan fan(dev, B);
     for (size_t i = 0; i < B; ++i) {
       auto [sx, sy, sz] = strides[i];
-      check_rc(spira_hip_downsample(keys.data_ptr(), keys.size(0), key_bits_of(keys), sx, sy, sz,
-                                    outs[i].data_ptr(),
-                                    reinterpret_cast<uint32_t *>(counts.data_ptr<int32_t>() + i),
-                                    wss[i].data_ptr(), ws_sizes[i], fan[i]),
+      check_rc(spira_hip_downsample_execute(keys.data_ptr(), n, bits, sx, sy, sz, n > 0 ? &hplans[i] : nullptr,
+                                            outs[i].data_ptr(),
+                                            reinterpret_cast<uint32_t *>(counts.data_ptr<int32_t>() + i),
+                                            wsb ? wss[i].data_ptr() : nullptr, wsb, fan[i]),
                "streamed_output_generate");
     }
     fan.join();

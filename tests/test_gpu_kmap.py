@@ -64,6 +64,60 @@ def test_streamed_output_generate(dev, scene_small):
         assert np.array_equal(np_(o), orc.downsample(rk, s))
 
 
+def _grid(xs, ys, zs):
+    g = np.stack(np.meshgrid(np.asarray(xs), np.asarray(ys), np.asarray(zs), indexing="ij"), -1)
+    return g.reshape(-1, 3).astype(np.int32)
+
+
+def _ds_case(dev, keys_np, bits, strides):
+    tk = torch.from_numpy(keys_np).to(dev)
+    for s in strides:
+        assert np.array_equal(np_(F.downsample(tk, s)), orc.downsample(keys_np, s)), s
+    for o, s in zip(F.streamed_output_generate(tk, strides), strides):
+        assert np.array_equal(np_(o), orc.downsample(keys_np, s)), s
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+def test_downsample_paths(dev, bits):
+    """Each downsample path against the oracle, for single and streamed calls:
+    the segmented path with 32-bit sort keys (runs of equal masked x up to 4k
+    and up to 16k keys), the general path for unsorted keys and for a run
+    longer than 32768 keys (one dense x plane), sorted keys with duplicates,
+    and one or two keys."""
+    strides = [(2, 2, 2), (4, 4, 4), (1, 1, 2), (8, 8, 16), (1, 1, 1)]
+    rng = np.random.default_rng(21)
+    scattered = np.unique(rng.integers(0, 200, size=(30000, 3)), axis=0).astype(np.int32)
+    scattered[:, 2] %= 200 if bits == 64 else 250
+    plane = _grid([3], range(0, 200), range(0, 200 if bits == 64 else 250))  # 40k-50k keys in one x run
+    slab = _grid([4, 5], range(0, 85), range(0, 85))  # 14450 keys in one run at x stride 2
+    for c in (scattered, np.concatenate([scattered, slab]), np.concatenate([scattered, plane])):
+        rk, _ = orc.flatten_sort(c, bits == 64)
+        _ds_case(dev, rk, bits, strides)
+        _ds_case(dev, rng.permutation(rk), bits, strides)  # unsorted
+        _ds_case(dev, np.sort(np.concatenate([rk, rk[::3]])), bits, strides)  # duplicates
+    for c in (scattered[:1], scattered[:2]):
+        rk, _ = orc.flatten_sort(c, bits == 64)
+        _ds_case(dev, rk, bits, strides)
+
+
+def test_downsample_wide_sort_keys(dev):
+    """Negative y makes the varying bits below x wider than 32 (64-bit keys):
+    the segmented path with 64-bit sort keys (runs up to 4k and 16k keys)."""
+    rng = np.random.default_rng(22)
+    pts = np.unique(rng.integers(-300, 300, size=(40000, 3)), axis=0).astype(np.int32)
+    pts[:, 2] = np.abs(pts[:, 2])
+    slab = _grid([-2, -1], range(-40, 41), range(0, 91))  # 14742 keys in one x run at stride 2
+    for c in (pts, np.concatenate([pts, slab])):
+        rk, _ = orc.flatten_sort(np.unique(c, axis=0), True)
+        _ds_case(dev, rk, 64, [(2, 2, 2), (4, 4, 4), (1, 2, 1), (16, 16, 16)])
+
+
+def test_downsample_indoor_scene(dev):
+    """Config-4 scene: runs of up to ~16.5k keys (the 32k-key block tile)."""
+    rk, _ = orc.flatten_sort(scenes.indoor(), True)
+    _ds_case(dev, rk, 64, [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)])
+
+
 @pytest.mark.parametrize("bits", [32, 64])
 @pytest.mark.parametrize("dataflow", list(range(9)))
 def test_submanifold_all_dataflows(dev, scene_small, bits, dataflow):
