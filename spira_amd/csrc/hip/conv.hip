@@ -153,11 +153,8 @@ template <int N, class F> __device__ __forceinline__ void unroll(F &&f) {
   unroll_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-// 16 (or 4) bytes per lane from buffer `r` at byte offset `off` into
-// lds_wave_base + lane * 16 (or * 4); the LDS base must be wave-uniform.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, void *lds_wave_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_wave_base), 16, off, 0, 0, 0);
-}
+// 4 bytes per lane from buffer `r` at byte offset `off` into
+// lds_wave_base + lane * 4; the LDS base must be wave-uniform.
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t off, void *lds_wave_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_wave_base), 4, off, 0, 0, 0);
 }
@@ -205,59 +202,99 @@ template <class C> __device__ __forceinline__ ReadBase<C::NKS> read_base(const c
   return rb;
 }
 
+// Per-lane constants of a pipeline's loads, computed once per block so that
+// a step's issue is a few adds and selects per load (the step loop is bound
+// by instruction issue, not by the memory system).
+template <class C> struct IssueCtx {
+  uint32_t wlane[C::BVEC];  // byte offset of the lane's weight chunk in an (offset, kb = 0) block, or kOutOfRange
+  int c8[C::BVEC];          // first input channel of that chunk
+  uint32_t ldsw;            // LDS address of the wave's DMA slot in stage 0 (wave-uniform)
+  uint32_t kh16;            // byte offset of the lane's half of a 16-channel slice
+  int kh8;                  // its first channel
+};
+template <class C>
+__device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int n0, const Operands &op) {
+  IssueCtx<C> cx;
+  const int tid = threadIdx.x & 255;
+#pragma unroll
+  for (int i = 0; i < C::BVEC; ++i) {
+    const int v = i * 256 + tid;
+    const int n = v / C::CPR;
+    const int c8 = ((v % C::CPR) ^ C::swz(n)) * 8;
+    cx.wlane[i] = (n < C::BN && n0 + n < op.CoutP) ? static_cast<uint32_t>(((n0 + n) * op.CinP + c8) * 2)
+                                                     : kOutOfRange;
+    cx.c8[i] = c8;
+  }
+  cx.ldsw = __builtin_amdgcn_readfirstlane(lds_addr(ring) + wave * 64 * 16);
+  cx.kh8 = ((threadIdx.x & 63) >> 5) * 8;
+  cx.kh16 = static_cast<uint32_t>(cx.kh8 * 2);
+  return cx;
+}
+
 // Issue the loads of one step: A rows idx[m] (or -1) at channels
 // kb..kb+KC-1 into a[m][slice], weight row `wrow` into ring stage S.  When
 // !live every load is out of range, so each wave issues the same number of
-// loads in every step.
-template <class C, bool ALIGNED, int S>
-__device__ __forceinline__ void issue(char *ring, int wave, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
+// loads in every step.  CAT: the input is a channel concatenation [X | X2]
+// (each 16-channel slice lies wholly in one part, C1 % 16 == 0).  The
+// offsets use 32-bit arithmetic: every operand is below 2 GiB.
+template <class C, bool ALIGNED, bool CAT, int S>
+__device__ __forceinline__ void issue(const IssueCtx<C> &cx, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
                                       int kb, const Operands &op, __amdgpu_buffer_rsrc_t xr,
-                                      __amdgpu_buffer_rsrc_t xr2, __amdgpu_buffer_rsrc_t wr, int n0,
+                                      __amdgpu_buffer_rsrc_t xr2, __amdgpu_buffer_rsrc_t wr,
                                       half8 (&a)[C::BM / 128][C::NKS]) {
   constexpr int MT = C::BM / 128;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int kh = lane >> 5;
-  char *stage = ring + S * C::STAGE;
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
+    // branch-free selects: a divergent branch here would make both sides
+    // write the destination registers, and the second write would have to
+    // wait for every load in flight
+    const bool rv = live & (idx[m] >= 0);
+    if constexpr (!ALIGNED) {
+      // rows that are not 16-byte aligned: element loads (still one
+      // vector-memory op per k-half in the count, the first element's)
 #pragma unroll
-    for (int ks = 0; ks < C::NKS; ++ks) {
-      const int k = kb + ks * 16 + kh * 8;
-      // branch-free: a divergent branch here would make both sides write
-      // the destination registers, and the second write would have to
-      // wait for every load in flight
-      const bool ok = live & (idx[m] >= 0) & (k < op.Cin);
-      // the 16-channel slice lies wholly in X or in X2 (C1 % 16 == 0): a
-      // block-uniform choice of buffer
-      const bool second = kb + ks * 16 >= op.C1;
-      const uint32_t rowc = static_cast<uint32_t>(second ? op.Cin - op.C1 : op.C1);
-      const uint32_t at = (static_cast<uint32_t>(idx[m]) * rowc + (second ? k - op.C1 : k)) * 2u;
-      const uint32_t off = ok ? at : kOutOfRange;
-      if constexpr (!ALIGNED) {
-        // rows that are not 16-byte aligned: element loads (still one
-        // vector-memory op per k-half in the count, the first element's)
+      for (int ks = 0; ks < C::NKS; ++ks) {
+        const int k = kb + ks * 16 + cx.kh8;
+        const uint32_t off = (rv & (k < op.Cin)) ? (static_cast<uint32_t>(idx[m]) * op.Cin + k) * 2u : kOutOfRange;
         half8 v;
         v[0] = __builtin_bit_cast(_Float16, static_cast<unsigned short>(
                                                 __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0)));
 #pragma unroll
         for (int e = 1; e < 8; ++e)
-          v[e] = (live && idx[m] >= 0 && k + e < op.Cin) ? op.X[static_cast<int64_t>(idx[m]) * op.Cin + k + e]
-                                                        : static_cast<_Float16>(0.f);
+          v[e] = (rv && k + e < op.Cin) ? op.X[static_cast<int64_t>(idx[m]) * op.Cin + k + e]
+                                        : static_cast<_Float16>(0.f);
         a[m][ks] = v;
-      } else {
-        a[m][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, off, 0, 0));
+      }
+    } else {
+      const uint32_t rb1 = static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>(op.C1 * 2);
+      uint32_t rb2 = 0;
+      if constexpr (CAT) rb2 = static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>((op.Cin - op.C1) * 2);
+#pragma unroll
+      for (int ks = 0; ks < C::NKS; ++ks) {
+        const int k0 = kb + ks * 16;
+        const bool ok = rv & (cx.kh8 < op.Cin - k0);
+        if constexpr (CAT) {
+          const bool second = k0 >= op.C1;  // block-uniform
+          const uint32_t at = second ? rb2 + static_cast<uint32_t>((k0 - op.C1) * 2) : rb1 + static_cast<uint32_t>(k0 * 2);
+          a[m][ks] = __builtin_bit_cast(
+              half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, ok ? at + cx.kh16 : kOutOfRange, 0, 0));
+        } else {
+          a[m][ks] = __builtin_bit_cast(
+              half8, __builtin_amdgcn_raw_buffer_load_b128(
+                         xr, ok ? rb1 + static_cast<uint32_t>(k0 * 2) + cx.kh16 : kOutOfRange, 0, 0));
+        }
       }
     }
   }
+  // weights: chunk c8 of the lane's row is real while c8 < CinP - kb; an
+  // out-of-range lane offset stays out of range after adding the step's
+  // (wstep < wbytes < 2^31)
+  const uint32_t wstep = static_cast<uint32_t>((wrow * op.CoutP * op.CinP + kb) * 2);
+  const int wlim = live ? op.CinP - kb : 0;
 #pragma unroll
   for (int i = 0; i < C::BVEC; ++i) {
-    const int v = i * 256 + tid;
-    const int n = v / C::CPR, cp = v % C::CPR;
-    const int c = cp ^ C::swz(n);
-    const uint32_t off = (live && n < C::BN && n0 + n < op.CoutP && kb + c * 8 < op.CinP)
-                             ? ((static_cast<uint32_t>(wrow) * op.CoutP + n0 + n) * op.CinP + kb + c * 8) * 2u
-                             : kOutOfRange;
-    dma16(wr, off, stage + (i * 256 + wave * 64) * 16);
+    const uint32_t off = cx.c8[i] < wlim ? cx.wlane[i] + wstep : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void_t *)(cx.ldsw + S * C::STAGE + i * 4096), 16, off, 0, 0, 0);
   }
 }
 
@@ -302,7 +339,7 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32]
 // just read (each wave reads only its own slot).  Steps past nsteps (at most
 // NS-1) compute on all-zero stages, so the trip is uniform and the
 // accumulators stay in place.
-template <class C, bool ALIGNED, int PL, class Fetch, class Resolve>
+template <class C, bool ALIGNED, bool CAT, int PL, class Fetch, class Resolve>
 __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], int nsteps, Fetch fetch,
                                     Resolve resolve, const Operands &op, int n0, char *ring) {
   constexpr int MT = C::BM / 128, NS = C::NS;
@@ -311,6 +348,7 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
   const __amdgpu_buffer_rsrc_t xr2 = make_rsrc(op.X2 ? op.X2 : op.X, op.X2 ? op.x2bytes : 0u);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
   const ReadBase<C::NKS> rb = read_base<C>(ring);
+  const IssueCtx<C> cx = issue_ctx<C>(ring, wave, n0, op);
   half8 areg[NS][MT][C::NKS];  // gathered rows per stage
   auto put = [&](int u, auto St) {
     int32_t idx[MT];
@@ -322,8 +360,7 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
 #pragma unroll
       for (int m = 0; m < MT; ++m) idx[m] = -1;
     }
-    issue<C, ALIGNED, decltype(St)::value>(ring, wave, live, idx, wrow, kb, op, xr, xr2, wr, n0,
-                                           areg[decltype(St)::value]);
+    issue<C, ALIGNED, CAT, decltype(St)::value>(cx, live, idx, wrow, kb, op, xr, xr2, wr, areg[decltype(St)::value]);
   };
   unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
   unroll<NS - 1>([&](auto I) {
@@ -497,7 +534,7 @@ __device__ int64_t g_block_times[1 << 20];
 // logical row i is target order[i] and `map` holds the rows in logical order;
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
-template <int WN, int MODE, bool ALIGNED, int NKS>
+template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
@@ -632,7 +669,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     pit.step(nch);
     if (tiled) read_tile();
   };
-  ring::run<C, ALIGNED, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, CAT, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   SPIRA_STAMP(2);
 #ifdef SPIRA_BLOCK_TIMING
   if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = nact;
@@ -724,7 +761,7 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
     kb = u * C::KC;
   };
   const int nch = (op.CinP + C::KC - 1) / C::KC;
-  ring::run<C, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, false, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = dst[m];
@@ -775,7 +812,7 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operand
     kb = u * C::KC;
   };
   const int nch = (op.CinP + C::KC - 1) / C::KC;
-  ring::run<C, ALIGNED, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, false, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = src[m];
@@ -1050,12 +1087,12 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
     default: CALL(4); break;      \
   }
 
-template <int MODE, bool AL, int NKS>
+template <int MODE, bool AL, int NKS, bool CAT = false>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                       void *Y, const Epilogue &epi) {
 #define SPIRA_OS_CALL(W)                                                                                         \
-  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
                      jper, op, Y, epi)
   SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
 #undef SPIRA_OS_CALL
@@ -1075,8 +1112,15 @@ template <int MODE>
 static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                           const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                           void *Y, const Epilogue &epi) {
+  const bool cat = op.X2 != nullptr;
   if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-  else if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  else if (cat) {
+    // channel concatenations: storage-dtype outputs (split or not)
+    if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
+      if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+    }
+  } else if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
   else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
 }
 
@@ -1209,6 +1253,7 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
   SPIRA_HIP_REQUIRE(c_in2 == 0 || (sources2 && dtype == SPIRA_F16 && c_in % 16 == 0 && c_in2 % 8 == 0),
                     "conv_os_concat: fp16 only, the first part's channels a multiple of 16, the second's of 8");
   SPIRA_HIP_REQUIRE(out_mode >= SPIRA_OUT_STORE && out_mode <= SPIRA_OUT_ADD_F32, "conv_os: bad out_mode");
+  SPIRA_HIP_REQUIRE(c_in2 == 0 || out_mode == SPIRA_OUT_STORE, "conv_os_concat: storage-dtype outputs only");
   SPIRA_HIP_REQUIRE(c_in > 0 && c_out > 0 && num_offsets > 0, "conv_os: empty channel / offset dimension");
   SPIRA_HIP_REQUIRE(out_mode == SPIRA_OUT_STORE || (!scale && !shift && !residual && !relu),
                     "conv_os: the epilogue applies to the storage-dtype output only");
