@@ -128,9 +128,12 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
   static_assert((NS - 1) * STAGE + (WN - 1) * 32 * ROWB < 65536, "weight read offset exceeds 16 bits");
   static_assert((NS - 2) * LPS + (NS - 1) < 64, "vmcnt range");
-  // physical chunk of logical chunk c of weight row n: conflict-free 16-byte
-  // reads for 8 consecutive rows at one chunk, independent of n / 32
-  __host__ __device__ static constexpr int swz(int n) { return NKS == 2 ? (n >> 2) & 3 : n & 7; }
+  // physical chunk of logical chunk c of weight row n: a 16-byte LDS read
+  // serves 16 lanes (16 rows at one logical chunk) per cycle, and they are
+  // conflict-free when their byte addresses differ mod 256 (64 banks): rows
+  // of ROWB = 64 (128) bytes take 4 (2) positions from n, the swizzle the
+  // other 4 (8) from n >> 2 (n >> 1)
+  __host__ __device__ static constexpr int swz(int n) { return NKS == 2 ? (n >> 2) & 3 : (n >> 1) & 7; }
 };
 
 // Tile shape per column-tile width and step: one 32-row tile per wave (the
@@ -231,77 +234,92 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
   return cx;
 }
 
-// Issue the loads of one step: A rows idx[m] (or -1) at channels
-// kb..kb+KC-1 into a[m][slice], weight row `wrow` into ring stage S.  When
-// !live every load is out of range, so each wave issues the same number of
-// loads in every step.  CAT: the input is a channel concatenation [X | X2]
-// (each 16-channel slice lies wholly in one part, C1 % 16 == 0).  The
-// offsets use 32-bit arithmetic: every operand is below 2 GiB.
-template <class C, bool ALIGNED, bool CAT, int S>
-__device__ __forceinline__ void issue(const IssueCtx<C> &cx, bool live, const int32_t (&idx)[C::BM / 128], int wrow,
-                                      int kb, const Operands &op, __amdgpu_buffer_rsrc_t xr,
-                                      __amdgpu_buffer_rsrc_t xr2, __amdgpu_buffer_rsrc_t wr,
-                                      half8 (&a)[C::BM / 128][C::NKS]) {
+// The operands of one step: gathered rows idx[m] (or -1), weight row wrow,
+// first input channel kb; !live: a step past the end (every load out of
+// range, so that each wave issues the same number of loads in every step).
+template <int MT> struct StepIn {
+  bool live;
+  int32_t idx[MT];
+  int wrow, kb;
+};
+
+// Issue the loads of 16-channel slice KS of a step into ring stage S: the A
+// rows at channels kb + 16 KS .. + 15 into a[m][KS], and the weight DMAs
+// i = KS, KS + NKS, ... (a step's slices together issue every load of the
+// step, in slice order).  CAT: the input is a channel concatenation
+// [X | X2] (each 16-channel slice lies wholly in one part, C1 % 16 == 0).
+// The offsets use 32-bit arithmetic: every operand is below 2 GiB.
+template <class C, bool ALIGNED, bool CAT, int S, int KS>
+__device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn<C::BM / 128> &st, const Operands &op,
+                                            __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
+                                            __amdgpu_buffer_rsrc_t wr, half8 (&a)[C::BM / 128][C::NKS]) {
   constexpr int MT = C::BM / 128;
+  const int k0 = st.kb + KS * 16;
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     // branch-free selects: a divergent branch here would make both sides
     // write the destination registers, and the second write would have to
     // wait for every load in flight
-    const bool rv = live & (idx[m] >= 0);
+    const bool rv = st.live & (st.idx[m] >= 0);
     if constexpr (!ALIGNED) {
       // rows that are not 16-byte aligned: element loads (still one
       // vector-memory op per k-half in the count, the first element's)
+      const int k = k0 + cx.kh8;
+      const uint32_t off = (rv & (k < op.Cin)) ? (static_cast<uint32_t>(st.idx[m]) * op.Cin + k) * 2u : kOutOfRange;
+      half8 v;
+      v[0] = __builtin_bit_cast(_Float16, static_cast<unsigned short>(
+                                              __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0)));
 #pragma unroll
-      for (int ks = 0; ks < C::NKS; ++ks) {
-        const int k = kb + ks * 16 + cx.kh8;
-        const uint32_t off = (rv & (k < op.Cin)) ? (static_cast<uint32_t>(idx[m]) * op.Cin + k) * 2u : kOutOfRange;
-        half8 v;
-        v[0] = __builtin_bit_cast(_Float16, static_cast<unsigned short>(
-                                                __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0)));
-#pragma unroll
-        for (int e = 1; e < 8; ++e)
-          v[e] = (rv && k + e < op.Cin) ? op.X[static_cast<int64_t>(idx[m]) * op.Cin + k + e]
-                                        : static_cast<_Float16>(0.f);
-        a[m][ks] = v;
-      }
+      for (int e = 1; e < 8; ++e)
+        v[e] = (rv && k + e < op.Cin) ? op.X[static_cast<int64_t>(st.idx[m]) * op.Cin + k + e]
+                                      : static_cast<_Float16>(0.f);
+      a[m][KS] = v;
     } else {
-      const uint32_t rb1 = static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>(op.C1 * 2);
-      uint32_t rb2 = 0;
-      if constexpr (CAT) rb2 = static_cast<uint32_t>(idx[m]) * static_cast<uint32_t>((op.Cin - op.C1) * 2);
-#pragma unroll
-      for (int ks = 0; ks < C::NKS; ++ks) {
-        const int k0 = kb + ks * 16;
-        const bool ok = rv & (cx.kh8 < op.Cin - k0);
-        if constexpr (CAT) {
-          const bool second = k0 >= op.C1;  // block-uniform
-          const uint32_t at = second ? rb2 + static_cast<uint32_t>((k0 - op.C1) * 2) : rb1 + static_cast<uint32_t>(k0 * 2);
-          a[m][ks] = __builtin_bit_cast(
-              half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, ok ? at + cx.kh16 : kOutOfRange, 0, 0));
-        } else {
-          a[m][ks] = __builtin_bit_cast(
-              half8, __builtin_amdgcn_raw_buffer_load_b128(
-                         xr, ok ? rb1 + static_cast<uint32_t>(k0 * 2) + cx.kh16 : kOutOfRange, 0, 0));
-        }
+      const bool ok = rv & (cx.kh8 < op.Cin - k0);
+      if constexpr (CAT) {
+        const bool second = k0 >= op.C1;  // block-uniform
+        const uint32_t at = second ? static_cast<uint32_t>(st.idx[m]) * static_cast<uint32_t>((op.Cin - op.C1) * 2) +
+                                         static_cast<uint32_t>((k0 - op.C1) * 2)
+                                   : static_cast<uint32_t>(st.idx[m]) * static_cast<uint32_t>(op.C1 * 2) +
+                                         static_cast<uint32_t>(k0 * 2);
+        a[m][KS] = __builtin_bit_cast(
+            half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, ok ? at + cx.kh16 : kOutOfRange, 0, 0));
+      } else {
+        const uint32_t rb1 = static_cast<uint32_t>(st.idx[m]) * static_cast<uint32_t>(op.C1 * 2);
+        a[m][KS] = __builtin_bit_cast(
+            half8, __builtin_amdgcn_raw_buffer_load_b128(
+                       xr, ok ? rb1 + static_cast<uint32_t>(k0 * 2) + cx.kh16 : kOutOfRange, 0, 0));
       }
     }
   }
   // weights: chunk c8 of the lane's row is real while c8 < CinP - kb; an
   // out-of-range lane offset stays out of range after adding the step's
   // (wstep < wbytes < 2^31)
-  const uint32_t wstep = static_cast<uint32_t>((wrow * op.CoutP * op.CinP + kb) * 2);
-  const int wlim = live ? op.CinP - kb : 0;
+  const uint32_t wstep = static_cast<uint32_t>((st.wrow * op.CoutP * op.CinP + st.kb) * 2);
+  const int wlim = st.live ? op.CinP - st.kb : 0;
 #pragma unroll
-  for (int i = 0; i < C::BVEC; ++i) {
+  for (int i = KS; i < C::BVEC; i += C::NKS) {
     const uint32_t off = cx.c8[i] < wlim ? cx.wlane[i] + wstep : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void_t *)(cx.ldsw + S * C::STAGE + i * 4096), 16, off, 0, 0, 0);
   }
 }
 
-// MFMAs of stage S (rows without a neighbour hold zeros)
-template <class C, int S>
+// Every load of a step, slice after slice (the prologue's steps).
+template <class C, bool ALIGNED, bool CAT, int S>
+__device__ __forceinline__ void issue(const IssueCtx<C> &cx, const StepIn<C::BM / 128> &st, const Operands &op,
+                                      __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
+                                      __amdgpu_buffer_rsrc_t wr, half8 (&a)[C::BM / 128][C::NKS]) {
+  unroll<C::NKS>([&](auto KS) { issue_slice<C, ALIGNED, CAT, S, decltype(KS)::value>(cx, st, op, xr, xr2, wr, a); });
+}
+
+// MFMAs of stage S (rows without a neighbour hold zeros).  between(KS) runs
+// after slice KS's weight reads are issued and before their wait: the next
+// step's loads issued there overlap the LDS latency and the MFMAs of the
+// previous slice, instead of all waves of the block issuing them in one
+// burst after the barrier.
+template <class C, int S, class Between>
 __device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase<C::NKS> &rb,
-                                        const half8 (&a)[C::BM / 128][C::NKS]) {
+                                        const half8 (&a)[C::BM / 128][C::NKS], Between between) {
   constexpr int MT = C::BM / 128, WN = C::BN / 32;
   unroll<C::NKS>([&](auto KS) {
     constexpr int ks = decltype(KS)::value;
@@ -310,6 +328,7 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32]
       constexpr int wn = decltype(W)::value;
       b[wn] = rd16<S * C::STAGE + wn * 32 * C::ROWB>(rb.b[ks]);
     });
+    between(KS);
     lds_wait();
 #pragma unroll
     for (int wn = 0; wn < WN; ++wn) pin(b[wn]);
@@ -350,17 +369,21 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
   const ReadBase<C::NKS> rb = read_base<C>(ring);
   const IssueCtx<C> cx = issue_ctx<C>(ring, wave, n0, op);
   half8 areg[NS][MT][C::NKS];  // gathered rows per stage
-  auto put = [&](int u, auto St) {
-    int32_t idx[MT];
-    int wrow = 0;
-    int kb = 0;
-    const bool live = u < nsteps;
-    if (live) resolve(u, St, idx, wrow, kb);
+  auto prepare = [&](int u, auto St) {
+    StepIn<MT> st;
+    st.wrow = 0;
+    st.kb = 0;
+    st.live = u < nsteps;
+    if (st.live) resolve(u, St, st.idx, st.wrow, st.kb);
     else {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) idx[m] = -1;
+      for (int m = 0; m < MT; ++m) st.idx[m] = -1;
     }
-    issue<C, ALIGNED, CAT, decltype(St)::value>(cx, live, idx, wrow, kb, op, xr, xr2, wr, areg[decltype(St)::value]);
+    return st;
+  };
+  auto put = [&](int u, auto St) {
+    const StepIn<MT> st = prepare(u, St);
+    issue<C, ALIGNED, CAT, decltype(St)::value>(cx, st, op, xr, xr2, wr, areg[decltype(St)::value]);
   };
   unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
   unroll<NS - 1>([&](auto I) {
@@ -378,10 +401,12 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
       SPIRA_STEP_STAMP(s + i, 1);
       __builtin_amdgcn_s_barrier();
       SPIRA_STEP_STAMP(s + i, 2);
-      put(s + i + NS - 1, std::integral_constant<int, slot>{});
-      fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
+      const StepIn<MT> nx = prepare(s + i + NS - 1, std::integral_constant<int, slot>{});
       SPIRA_STEP_STAMP(s + i, 3);
-      compute<C, i>(acc, rb, areg[i]);
+      compute<C, i>(acc, rb, areg[i], [&](auto KS) {
+        issue_slice<C, ALIGNED, CAT, slot, decltype(KS)::value>(cx, nx, op, xr, xr2, wr, areg[slot]);
+      });
+      fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
     });
   }
   wait_vm<0>();
