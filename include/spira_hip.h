@@ -236,8 +236,8 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
 
 /* spira_hip_conv_os over the channel concatenation [sources | sources2] of two
  * fp16 feature arrays ([num_sources, c_in] and [num_sources, c_in2]; c_in a
- * multiple of 16, c_in2 of 8) without materialising it: the gather picks
- * each 16-channel slice from the part that holds it.  `prepared` holds the
+ * multiple of 32, c_in2 of 8) without materialising it: the gather picks
+ * each 32-channel block from the part that holds it.  `prepared` holds the
  * weights of the whole [K, c_in + c_in2, c_out] layer; every other argument
  * is as in spira_hip_conv_os.  (Replaces the skip-connection torch.cat in
  * front of a decoder layer, source/spira/operators.py:11-13; no counterpart

@@ -72,7 +72,7 @@ struct Operands {
   uint32_t xbytes;
   const _Float16 *X2;  // [rows, Cin - C1]: channels C1 .. Cin-1 (a channel concatenation), or null
   uint32_t x2bytes;
-  int C1;  // channels held by X (Cin without X2; a multiple of 16 with it)
+  int C1;  // channels held by X (Cin without X2; a multiple of 32 with it)
   int Cin, CinP;
   const _Float16 *WT;  // prepared weights [K, CoutP, CinP]
   uint32_t wbytes;
@@ -125,6 +125,7 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int LDS = RING + MAP_TILE > OUT_STAGE ? RING + MAP_TILE : OUT_STAGE;
   static constexpr int LPS = MT * NKS + BVEC;  // vector-memory loads per wave and step
   static_assert(NKS == 2 || NKS == 4, "a step is 32 or 64 channels");
+  static_assert(MT == 1, "a wave owns 32 rows: two 16-row MFMA tiles");
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
   static_assert((NS - 1) * STAGE + (WN - 1) * 32 * ROWB < 65536, "weight read offset exceeds 16 bits");
   static_assert((NS - 2) * LPS + (NS - 1) < 64, "vmcnt range");
@@ -191,17 +192,19 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 // ties a value read by rd16 / rd4 to a point after lds_wait()
 template <class V> __device__ __forceinline__ void pin(V &v) { asm volatile("" : "+v"(v)); }
 
-// per-lane LDS read bases of the ring: weights of 16-channel slice ks,
-// + s * STAGE + wn * 32 * ROWB
+// per-lane LDS read bases of the ring: the weight fragment of 32-channel
+// block kq (v_mfma_f32_16x16x32_f16 B layout: lane l holds column l % 16,
+// channels 8 (l / 16) .. + 7 of the block), + s * STAGE + nb * 16 * ROWB for
+// stage s and 16-column tile nb (the swizzle depends on l % 16 only)
 template <int NKS> struct ReadBase {
-  uint32_t b[NKS];
+  uint32_t b[NKS / 2];
 };
 template <class C> __device__ __forceinline__ ReadBase<C::NKS> read_base(const char *ring) {
-  const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, lq = lane >> 4;
   const uint32_t base = lds_addr(ring);
   ReadBase<C::NKS> rb;
 #pragma unroll
-  for (int ks = 0; ks < C::NKS; ++ks) rb.b[ks] = base + (r * C::CPR + ((2 * ks + kh) ^ C::swz(r))) * 16;
+  for (int kq = 0; kq < C::NKS / 2; ++kq) rb.b[kq] = base + (l16 * C::CPR + ((4 * kq + lq) ^ C::swz(l16))) * 16;
   return rb;
 }
 
@@ -212,7 +215,7 @@ template <class C> struct IssueCtx {
   uint32_t wlane[C::BVEC];  // byte offset of the lane's weight chunk in an (offset, kb = 0) block, or kOutOfRange
   int c8[C::BVEC];          // first input channel of that chunk
   uint32_t ldsw;            // LDS address of the wave's DMA slot in stage 0 (wave-uniform)
-  uint32_t kh16;            // byte offset of the lane's half of a 16-channel slice
+  uint32_t kh16;            // byte offset of the lane's quarter of a 32-channel block
   int kh8;                  // its first channel
 };
 template <class C>
@@ -229,63 +232,69 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
     cx.c8[i] = c8;
   }
   cx.ldsw = __builtin_amdgcn_readfirstlane(lds_addr(ring) + wave * 64 * 16);
-  cx.kh8 = ((threadIdx.x & 63) >> 5) * 8;
+  cx.kh8 = ((threadIdx.x & 63) >> 4) * 8;
   cx.kh16 = static_cast<uint32_t>(cx.kh8 * 2);
   return cx;
 }
 
-// The operands of one step: gathered rows idx[m] (or -1), weight row wrow,
-// first input channel kb; !live: a step past the end (every load out of
-// range, so that each wave issues the same number of loads in every step).
-template <int MT> struct StepIn {
+// The operands of one step: the gathered row of the lane in each of the
+// wave's two 16-row tiles, idx[rt] (source row of tile row l % 16, or -1),
+// weight row wrow, first input channel kb; !live: a step past the end (every
+// load out of range, so that each wave issues the same number of loads in
+// every step).
+struct StepIn {
   bool live;
-  int32_t idx[MT];
+  int32_t idx[2];
   int wrow, kb;
 };
 
-// Issue the loads of 16-channel slice KS of a step into ring stage S: the A
-// rows at channels kb + 16 KS .. + 15 into a[m][KS], and the weight DMAs
-// i = KS, KS + NKS, ... (a step's slices together issue every load of the
-// step, in slice order).  CAT: the input is a channel concatenation
-// [X | X2] (each 16-channel slice lies wholly in one part, C1 % 16 == 0).
-// The offsets use 32-bit arithmetic: every operand is below 2 GiB.
+// Issue the loads of slice KS of a step into ring stage S: the A fragment
+// of row tile rt = KS % 2 and 32-channel block kq = KS / 2 (lane l: its row
+// idx[rt], channels kb + 32 kq + 8 (l / 16) .. + 7, the
+// v_mfma_f32_16x16x32_f16 A layout: one instruction reads 16 rows x 64
+// bytes) into a[0][KS], and the weight DMAs i = KS, KS + NKS, ... (a step's
+// slices together issue every load of the step, in slice order).  CAT: the
+// input is a channel concatenation [X | X2] (each 32-channel block lies
+// wholly in one part, C1 % 32 == 0).  The offsets use 32-bit arithmetic:
+// every operand is below 2 GiB.
 template <class C, bool ALIGNED, bool CAT, int S, int KS>
-__device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn<C::BM / 128> &st, const Operands &op,
+__device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
                                             __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
-                                            __amdgpu_buffer_rsrc_t wr, half8 (&a)[C::BM / 128][C::NKS]) {
-  constexpr int MT = C::BM / 128;
-  const int k0 = st.kb + KS * 16;
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
+                                            __amdgpu_buffer_rsrc_t wr, half8 (&a)[1][C::NKS]) {
+  constexpr int rt = KS & 1;
+  const int k0 = st.kb + (KS >> 1) * 32;
+  {
+    constexpr int m = 0;
     // branch-free selects: a divergent branch here would make both sides
     // write the destination registers, and the second write would have to
     // wait for every load in flight
-    const bool rv = st.live & (st.idx[m] >= 0);
+    const int32_t ix = st.idx[rt];
+    const bool rv = st.live & (ix >= 0);
     if constexpr (!ALIGNED) {
       // rows that are not 16-byte aligned: element loads (still one
       // vector-memory op per k-half in the count, the first element's)
       const int k = k0 + cx.kh8;
-      const uint32_t off = (rv & (k < op.Cin)) ? (static_cast<uint32_t>(st.idx[m]) * op.Cin + k) * 2u : kOutOfRange;
+      const uint32_t off = (rv & (k < op.Cin)) ? (static_cast<uint32_t>(ix) * op.Cin + k) * 2u : kOutOfRange;
       half8 v;
       v[0] = __builtin_bit_cast(_Float16, static_cast<unsigned short>(
                                               __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0)));
 #pragma unroll
       for (int e = 1; e < 8; ++e)
-        v[e] = (rv && k + e < op.Cin) ? op.X[static_cast<int64_t>(st.idx[m]) * op.Cin + k + e]
+        v[e] = (rv && k + e < op.Cin) ? op.X[static_cast<int64_t>(ix) * op.Cin + k + e]
                                       : static_cast<_Float16>(0.f);
       a[m][KS] = v;
     } else {
       const bool ok = rv & (cx.kh8 < op.Cin - k0);
       if constexpr (CAT) {
         const bool second = k0 >= op.C1;  // block-uniform
-        const uint32_t at = second ? static_cast<uint32_t>(st.idx[m]) * static_cast<uint32_t>((op.Cin - op.C1) * 2) +
+        const uint32_t at = second ? static_cast<uint32_t>(ix) * static_cast<uint32_t>((op.Cin - op.C1) * 2) +
                                          static_cast<uint32_t>((k0 - op.C1) * 2)
-                                   : static_cast<uint32_t>(st.idx[m]) * static_cast<uint32_t>(op.C1 * 2) +
+                                   : static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.C1 * 2) +
                                          static_cast<uint32_t>(k0 * 2);
         a[m][KS] = __builtin_bit_cast(
             half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, ok ? at + cx.kh16 : kOutOfRange, 0, 0));
       } else {
-        const uint32_t rb1 = static_cast<uint32_t>(st.idx[m]) * static_cast<uint32_t>(op.C1 * 2);
+        const uint32_t rb1 = static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.C1 * 2);
         a[m][KS] = __builtin_bit_cast(
             half8, __builtin_amdgcn_raw_buffer_load_b128(
                        xr, ok ? rb1 + static_cast<uint32_t>(k0 * 2) + cx.kh16 : kOutOfRange, 0, 0));
@@ -306,37 +315,48 @@ __device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn<
 
 // Every load of a step, slice after slice (the prologue's steps).
 template <class C, bool ALIGNED, bool CAT, int S>
-__device__ __forceinline__ void issue(const IssueCtx<C> &cx, const StepIn<C::BM / 128> &st, const Operands &op,
+__device__ __forceinline__ void issue(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
                                       __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
-                                      __amdgpu_buffer_rsrc_t wr, half8 (&a)[C::BM / 128][C::NKS]) {
+                                      __amdgpu_buffer_rsrc_t wr, half8 (&a)[1][C::NKS]) {
   unroll<C::NKS>([&](auto KS) { issue_slice<C, ALIGNED, CAT, S, decltype(KS)::value>(cx, st, op, xr, xr2, wr, a); });
 }
 
-// MFMAs of stage S (rows without a neighbour hold zeros).  between(KS) runs
-// after slice KS's weight reads are issued and before their wait: the next
-// step's loads issued there overlap the LDS latency and the MFMAs of the
-// previous slice, instead of all waves of the block issuing them in one
-// burst after the barrier.
+// MFMAs of stage S (rows without a neighbour hold zeros): per 32-channel
+// block kq, the weight fragments of the BN / 16 column tiles, then
+// v_mfma_f32_16x16x32_f16 for both row tiles.  between(KQ) runs after block
+// kq's weight reads are issued and before their wait: the next step's loads
+// issued there overlap the LDS latency and the previous block's MFMAs,
+// instead of all waves of the block issuing them in one burst after the
+// barrier.  acc[rt][nb]: lane l holds rows 4 (l / 16) + i (i < 4) of row tile
+// rt, column l % 16 of column tile nb.
 template <class C, int S, class Between>
-__device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32], const ReadBase<C::NKS> &rb,
-                                        const half8 (&a)[C::BM / 128][C::NKS], Between between) {
-  constexpr int MT = C::BM / 128, WN = C::BN / 32;
-  unroll<C::NKS>([&](auto KS) {
-    constexpr int ks = decltype(KS)::value;
-    half8 b[WN];
-    unroll<WN>([&](auto W) {
-      constexpr int wn = decltype(W)::value;
-      b[wn] = rd16<S * C::STAGE + wn * 32 * C::ROWB>(rb.b[ks]);
+__device__ __forceinline__ void compute(floatx4 (&acc)[2][C::BN / 16], const ReadBase<C::NKS> &rb,
+                                        const half8 (&a)[1][C::NKS], Between between) {
+  constexpr int NB = C::BN / 16;
+  // wide tiles read their weight fragments in two halves (fewer live
+  // registers); the second half's reads overlap the first half's MFMAs
+  constexpr int NH = NB > 4 ? 2 : 1, NBH = NB / NH;
+  static_assert(NB % NH == 0, "column tiles split evenly");
+  unroll<C::NKS / 2>([&](auto KQ) {
+    constexpr int kq = decltype(KQ)::value;
+    unroll<NH>([&](auto H) {
+      constexpr int h = decltype(H)::value;
+      half8 b[NBH];
+      unroll<NBH>([&](auto B) {
+        constexpr int nb = decltype(B)::value;
+        b[nb] = rd16<S * C::STAGE + (h * NBH + nb) * 16 * C::ROWB>(rb.b[kq]);
+      });
+      if constexpr (h == 0) between(KQ);
+      lds_wait();
+#pragma unroll
+      for (int nb = 0; nb < NBH; ++nb) pin(b[nb]);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int nb = 0; nb < NBH; ++nb)
+          acc[rt][h * NBH + nb] =
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][2 * kq + rt], b[nb], acc[rt][h * NBH + nb], 0, 0, 0);
     });
-    between(KS);
-    lds_wait();
-#pragma unroll
-    for (int wn = 0; wn < WN; ++wn) pin(b[wn]);
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int wn = 0; wn < WN; ++wn)
-        acc[m][wn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m][ks], b[wn], acc[m][wn], 0, 0, 0);
   });
 }
 
@@ -346,8 +366,8 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32]
 //  * fetch(u, S) issues exactly PL LDS-DMA loads per wave that bring step
 //    u's row indices into the caller's index slot S (also for u >= nsteps,
 //    so that the vmcnt arithmetic is the same in every wave);
-//  * resolve(u, S, idx, wrow, kb) turns them into the gathered rows idx[m]
-//    (or -1), the weight row and the first input channel of step u.
+//  * resolve(u, S, idx, wrow, kb) turns them into the lane's gathered rows
+//    idx[rt] (or -1), the weight row and the first input channel of step u.
 // Both are called with u = 0, 1, 2, ... in order (fetch NS steps ahead of
 // resolve).  Issue order: F(0..NS-1), then per step u: D(u) F(u+NS)
 // (D = the LPS LDS-DMA loads of a step, F = a fetch).  Before step s
@@ -359,7 +379,7 @@ __device__ __forceinline__ void compute(floatx16 (&acc)[C::BM / 128][C::BN / 32]
 // NS-1) compute on all-zero stages, so the trip is uniform and the
 // accumulators stay in place.
 template <class C, bool ALIGNED, bool CAT, int PL, class Fetch, class Resolve>
-__device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], int nsteps, Fetch fetch,
+__device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, Fetch fetch,
                                     Resolve resolve, const Operands &op, int n0, char *ring) {
   constexpr int MT = C::BM / 128, NS = C::NS;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -370,19 +390,19 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
   const IssueCtx<C> cx = issue_ctx<C>(ring, wave, n0, op);
   half8 areg[NS][MT][C::NKS];  // gathered rows per stage
   auto prepare = [&](int u, auto St) {
-    StepIn<MT> st;
+    StepIn st;
     st.wrow = 0;
     st.kb = 0;
     st.live = u < nsteps;
     if (st.live) resolve(u, St, st.idx, st.wrow, st.kb);
     else {
-#pragma unroll
-      for (int m = 0; m < MT; ++m) st.idx[m] = -1;
+      st.idx[0] = -1;
+      st.idx[1] = -1;
     }
     return st;
   };
   auto put = [&](int u, auto St) {
-    const StepIn<MT> st = prepare(u, St);
+    const StepIn st = prepare(u, St);
     issue<C, ALIGNED, CAT, decltype(St)::value>(cx, st, op, xr, xr2, wr, areg[decltype(St)::value]);
   };
   unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
@@ -401,10 +421,11 @@ __device__ __forceinline__ void run(floatx16 (&acc)[C::BM / 128][C::BN / 32], in
       SPIRA_STEP_STAMP(s + i, 1);
       __builtin_amdgcn_s_barrier();
       SPIRA_STEP_STAMP(s + i, 2);
-      const StepIn<MT> nx = prepare(s + i + NS - 1, std::integral_constant<int, slot>{});
+      const StepIn nx = prepare(s + i + NS - 1, std::integral_constant<int, slot>{});
       SPIRA_STEP_STAMP(s + i, 3);
-      compute<C, i>(acc, rb, areg[i], [&](auto KS) {
-        issue_slice<C, ALIGNED, CAT, slot, decltype(KS)::value>(cx, nx, op, xr, xr2, wr, areg[slot]);
+      compute<C, i>(acc, rb, areg[i], [&](auto KQ) {
+        issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value>(cx, nx, op, xr, xr2, wr, areg[slot]);
+        issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value + 1>(cx, nx, op, xr, xr2, wr, areg[slot]);
       });
       fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
     });
@@ -443,22 +464,26 @@ struct StepIter {
 
 }  // namespace ring
 
-template <int WN, int MT> __device__ __forceinline__ void zero_acc(floatx16 (&acc)[MT][WN]) {
+// A wave's accumulators: 32 rows x 32 WN columns as 2 x 2 WN tiles of
+// 16 x 16 (v_mfma_f32_16x16x32_f16 layout: acc[rt][nb][i] of lane l is row
+// 16 rt + 4 (l / 16) + i, column 16 nb + l % 16).
+template <int WN> __device__ __forceinline__ void zero_acc(floatx4 (&acc)[2][2 * WN]) {
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int wn = 0; wn < WN; ++wn)
+    for (int nb = 0; nb < 2 * WN; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[m][wn][i] = 0.f;
+      for (int i = 0; i < 4; ++i) acc[rt][nb][i] = 0.f;
 }
 
-// Write one 32-row MFMA tile; orow[row] is the output row or -1.
+// Write a wave's 32-row tile; orow[row] is the output row or -1.
 template <int WN, int MODE>
-__device__ __forceinline__ void store_tile(const floatx16 (&acc)[WN], const int32_t *orow, int n0, int Cout, int r,
-                                           int kh, void *Yv, const Epilogue &epi) {
+__device__ __forceinline__ void store_tile(const floatx4 (&acc)[2][2 * WN], const int32_t *orow, int n0, int Cout,
+                                           void *Yv, const Epilogue &epi) {
+  const int lane = threadIdx.x & 63, l16 = lane & 15, lq = lane >> 4;
 #pragma unroll
-  for (int wn = 0; wn < WN; ++wn) {
-    const int col = n0 + wn * 32 + r;
+  for (int nb = 0; nb < 2 * WN; ++nb) {
+    const int col = n0 + nb * 16 + l16;
     if (col >= Cout) continue;
     float sc = 1.f, sh = 0.f;
     if constexpr (MODE == kStoreNative) {
@@ -466,53 +491,54 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[WN], const int3
       if (epi.shift) sh = epi.shift[col];
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = (i / 4) * 8 + kh * 4 + (i % 4);
-      const int32_t o = orow[row];
-      if (o < 0) continue;
-      float v = acc[wn][i];
-      const int64_t at = static_cast<int64_t>(o) * Cout + col;
-      if constexpr (MODE == kStoreNative) {
-        v = v * sc + sh;
-        if (epi.residual) v += static_cast<float>(static_cast<const _Float16 *>(epi.residual)[at]);
-        if (epi.relu) v = v > 0.f ? v : 0.f;
-        static_cast<_Float16 *>(Yv)[at] = static_cast<_Float16>(v);
-      } else if constexpr (MODE == kStoreF32) {
-        static_cast<float *>(Yv)[at] = v;
-      } else if constexpr (MODE == kAddF32) {
-        static_cast<float *>(Yv)[at] += v;
-      } else {
-        atomicAdd(static_cast<float *>(Yv) + at, v);
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int32_t o = orow[rt * 16 + lq * 4 + i];
+        if (o < 0) continue;
+        float v = acc[rt][nb][i];
+        const int64_t at = static_cast<int64_t>(o) * Cout + col;
+        if constexpr (MODE == kStoreNative) {
+          v = v * sc + sh;
+          if (epi.residual) v += static_cast<float>(static_cast<const _Float16 *>(epi.residual)[at]);
+          if (epi.relu) v = v > 0.f ? v : 0.f;
+          static_cast<_Float16 *>(Yv)[at] = static_cast<_Float16>(v);
+        } else if constexpr (MODE == kStoreF32) {
+          static_cast<float *>(Yv)[at] = v;
+        } else if constexpr (MODE == kAddF32) {
+          static_cast<float *>(Yv)[at] += v;
+        } else {
+          atomicAdd(static_cast<float *>(Yv) + at, v);
+        }
       }
-    }
   }
 }
 
-// Storage-dtype output of a wave's 32*MT x BN tile through LDS: the
+// Storage-dtype output of a wave's 32 x BN tile through LDS: the
 // accumulators (times scale, plus shift) are staged as fp16 rows, then every
 // lane writes 16-byte chunks of output rows (adding the residual and
 // applying ReLU), so that the output rows are written with full-width
 // vector stores.  Needs Cout % 8 == 0 (16-byte aligned rows) and a staging
-// area of 32*MT x (BN + 8) halves per wave.
-template <int WN, int MT>
-__device__ __forceinline__ void store_tile_vec(const floatx16 (&acc)[MT][WN], const int32_t *orow, int n0, int Cout,
+// area of 32 x (BN + 8) halves per wave.
+template <int WN>
+__device__ __forceinline__ void store_tile_vec(const floatx4 (&acc)[2][2 * WN], const int32_t *orow, int n0, int Cout,
                                                _Float16 *stage, void *Yv, const Epilogue &epi) {
-  constexpr int BN = 32 * WN, BNP = BN + 8, ROWS = 32 * MT;
-  const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
+  constexpr int BN = 32 * WN, BNP = BN + 8, ROWS = 32;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, lq = lane >> 4;
 #pragma unroll
-  for (int wn = 0; wn < WN; ++wn) {
-    const int col = n0 + wn * 32 + r;
+  for (int nb = 0; nb < 2 * WN; ++nb) {
+    const int col = n0 + nb * 16 + l16;
     float sc = 1.f, sh = 0.f;
     if (col < Cout) {
       if (epi.scale) sc = epi.scale[col];
       if (epi.shift) sh = epi.shift[col];
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = m * 32 + (i / 4) * 8 + kh * 4 + (i % 4);
-        stage[row * BNP + wn * 32 + r] = static_cast<_Float16>(acc[m][wn][i] * sc + sh);
+      for (int i = 0; i < 4; ++i) {
+        const int row = rt * 16 + lq * 4 + i;
+        stage[row * BNP + nb * 16 + l16] = static_cast<_Float16>(acc[rt][nb][i] * sc + sh);
       }
   }
   // the staging rows are private to the wave: LDS keeps its accesses in order
@@ -604,11 +630,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const int nsteps = nact * nch;
   SPIRA_STAMP(1);
 
-  floatx16 acc[MT][WN];
-  zero_acc<WN, MT>(acc);
-  bool mvalid[MT];
+  floatx4 acc[2][2 * WN];
+  zero_acc<WN>(acc);
+  // the lane's rows in the wave's two 16-row tiles: 32 wave + 16 rt + l % 16
+  const int l16 = lane & 15;
+  bool mvalid[2];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) mvalid[m] = row0 + wave * 32 * MT + m * 32 + r < T;
+  for (int rt = 0; rt < 2; ++rt) mvalid[rt] = row0 + wave * 32 + rt * 16 + l16 < T;
   // Map entries.  Kernels of at most 27 offsets: the block's BM map rows are
   // copied into LDS once (row stride KP = Kc | 1 words, odd, so that the
   // per-row reads of one column are conflict-free) and every step reads its
@@ -625,7 +653,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const uint32_t fbase = (flr < T && !ident) ? static_cast<uint32_t>(flr * Kc + j0) * 4u : kOutOfRange;
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(map, static_cast<uint32_t>(T * Kc * 4));
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + r) * 4;
+  const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + l16) * 4;
   ring::StepIter fit, pit;  // fetch side (runs NS steps ahead) and issue side
   fit.init(ulo, uhi);
   pit = fit;
@@ -651,7 +679,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     ring::wait_vm<0>();
     __syncthreads();
   }
-  const uint32_t tbase = ring::lds_addr(tile) + ((wave * 32 * MT + r) * KP + j0) * 4;
+  const uint32_t tbase = ring::lds_addr(tile) + ((wave * 32 + l16) * KP + j0) * 4;
   auto fetch = [&](int u, auto St) {
     (void)u;
     // (tiled: an out-of-range fetch that only keeps the vmcnt arithmetic)
@@ -664,30 +692,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   // after a step's are resolved, so their LDS latency hides behind the
   // following compute (whose B-read wait also covers them); only the
   // prologue's steps (no compute in between) wait for their own read.
-  int32_t pre[MT];
+  int32_t pre[2];
   auto read_tile = [&]() {
     const uint32_t col = static_cast<uint32_t>(pit.j) * 4u;
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-      asm volatile("ds_read_b32 %0, %1" : "=v"(pre[m]) : "v"(tbase + m * 32 * KP * 4 + col) : "memory");
+    for (int rt = 0; rt < 2; ++rt)
+      asm volatile("ds_read_b32 %0, %1" : "=v"(pre[rt]) : "v"(tbase + rt * 16 * KP * 4 + col) : "memory");
   };
   if (tiled) read_tile();
-  auto resolve = [&](int u, auto St, int32_t (&idx)[MT], int &wrow, int &kb) {
+  auto resolve = [&](int u, auto St, int32_t (&idx)[2], int &wrow, int &kb) {
     if (tiled) {
       if (u < NS) ring::lds_wait();  // prologue puts: no compute since the read
-#pragma unroll
-      for (int m = 0; m < MT; ++m) idx[m] = pre[m];
+      idx[0] = pre[0];
+      idx[1] = pre[1];
     } else {
-      ring::unroll<MT>([&](auto M) {
-        idx[decltype(M)::value] = ring::rd4<decltype(St)::value * 1024 + decltype(M)::value * 128>(ibase);
-      });
+      idx[0] = ring::rd4<decltype(St)::value * 1024>(ibase);
+      idx[1] = ring::rd4<decltype(St)::value * 1024 + 64>(ibase);
       ring::lds_wait();
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      ring::pin(idx[m]);
-      if (ident) idx[m] = static_cast<int32_t>(row0 + wave * 32 * MT + m * 32 + r);
-      if (!mvalid[m]) idx[m] = -1;
+    for (int rt = 0; rt < 2; ++rt) {
+      ring::pin(idx[rt]);
+      if (ident) idx[rt] = static_cast<int32_t>(row0 + wave * 32 + rt * 16 + l16);
+      if (!mvalid[rt]) idx[rt] = -1;
     }
     wrow = j0 + pit.j;
     kb = pit.chunk * C::KC;
@@ -709,13 +736,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   __syncthreads();  // every wave is done with the ring: it becomes the staging area
   if constexpr (MODE == kStoreNative) {
     if (op.Cout % 8 == 0) {
-      store_tile_vec<WN, MT>(acc, orow_s[wave], n0, op.Cout,
-                             reinterpret_cast<_Float16 *>(ring_lds) + wave * 32 * MT * (C::BN + 8), Y, epi);
+      store_tile_vec<WN>(acc, orow_s[wave], n0, op.Cout,
+                         reinterpret_cast<_Float16 *>(ring_lds) + wave * 32 * (C::BN + 8), Y, epi);
       return;
     }
   }
-#pragma unroll
-  for (int m = 0; m < MT; ++m) store_tile<WN, MODE>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Y, epi);
+  store_tile<WN, MODE>(acc, orow_s[wave], n0, op.Cout, Y, epi);
 }
 
 // Fused weight-stationary pass.  Rows of the pair list are tiled per
@@ -765,36 +791,32 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
   const int row = lo;
   if (tile >= tstart[R] || (mir && 2 * row + 1 == Kw)) return;  // block-uniform
   const int64_t nrow = naddrs[row + 1] - naddrs[row];
-  int32_t src[MT], dst[MT];
+  // the lane's source rows in the wave's two 16-row tiles (MFMA A layout)
+  // and the destination of wave row r (epilogue)
+  const int64_t base = (tile - tstart[row]) * C::BM + wave * 32;
+  int32_t src[2], dst = -1;
 #pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const int64_t local = (tile - tstart[row]) * C::BM + wave * 32 * MT + m * 32 + r;
-    const bool valid = local < nrow;
-    const int64_t p = naddrs[row] + local;
-    src[m] = valid ? (mir ? out_idx[p] : in_idx[p]) : -1;
-    dst[m] = valid ? (mir ? in_idx[p] : out_idx[p]) : -1;
+  for (int rt = 0; rt < 2; ++rt) {
+    const int64_t local = base + rt * 16 + (lane & 15);
+    src[rt] = local < nrow ? (mir ? out_idx[naddrs[row] + local] : in_idx[naddrs[row] + local]) : -1;
   }
+  if (base + r < nrow) dst = mir ? in_idx[naddrs[row] + base + r] : out_idx[naddrs[row] + base + r];
   const int wrow0 = woffset + (mir ? Kw - 1 - row : row);
   const int n0 = blockIdx.y * C::BN;
-  floatx16 acc[MT][WN];
-  zero_acc<WN, MT>(acc);
+  floatx4 acc[2][2 * WN];
+  zero_acc<WN>(acc);
   auto fetch = [](int, auto) {};
-  auto resolve = [&](int u, auto, int32_t (&idx)[MT], int &wrow, int &kb) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) idx[m] = src[m];
+  auto resolve = [&](int u, auto, int32_t (&idx)[2], int &wrow, int &kb) {
+    idx[0] = src[0];
+    idx[1] = src[1];
     wrow = wrow0;
     kb = u * C::KC;
   };
   const int nch = (op.CinP + C::KC - 1) / C::KC;
   ring::run<C, ALIGNED, false, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
-  if (kh == 0) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = dst[m];
-  }
+  if (kh == 0) orow_s[wave][r] = dst;
   __syncthreads();
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-    store_tile<WN, kAtomicF32>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Yacc, Epilogue{});
+  store_tile<WN, kAtomicF32>(acc, orow_s[wave], n0, op.Cout, Yacc, Epilogue{});
 }
 
 struct GroupTable {
@@ -820,32 +842,26 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operand
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, kh = lane >> 5;
-  int32_t src[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const int64_t local = (tile - gt.tile_start[g]) * C::BM + wave * 32 * MT + m * 32 + r;
-    src[m] = local < gt.rows[g] ? static_cast<int32_t>(gt.row_off[g] + local) : -1;
-  }
+  const int64_t base = (tile - gt.tile_start[g]) * C::BM + wave * 32;
+  auto row_of = [&](int64_t local) {
+    return local < gt.rows[g] ? static_cast<int32_t>(gt.row_off[g] + local) : -1;
+  };
+  const int32_t src[2] = {row_of(base + (lane & 15)), row_of(base + 16 + (lane & 15))};
   const int n0 = blockIdx.y * C::BN;
-  floatx16 acc[MT][WN];
-  zero_acc<WN, MT>(acc);
+  floatx4 acc[2][2 * WN];
+  zero_acc<WN>(acc);
   auto fetch = [](int, auto) {};
-  auto resolve = [&](int u, auto, int32_t (&idx)[MT], int &wrow, int &kb) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) idx[m] = src[m];
+  auto resolve = [&](int u, auto, int32_t (&idx)[2], int &wrow, int &kb) {
+    idx[0] = src[0];
+    idx[1] = src[1];
     wrow = g;
     kb = u * C::KC;
   };
   const int nch = (op.CinP + C::KC - 1) / C::KC;
   ring::run<C, ALIGNED, false, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
-  if (kh == 0) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) orow_s[wave][m * 32 + r] = src[m];
-  }
+  if (kh == 0) orow_s[wave][r] = row_of(base + r);
   __syncthreads();
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-    store_tile<WN, kStoreF32>(acc[m], orow_s[wave] + m * 32, n0, op.Cout, r, kh, Yb, Epilogue{});
+  store_tile<WN, kStoreF32>(acc, orow_s[wave], n0, op.Cout, Yb, Epilogue{});
 }
 
 // ---------------------------------------------------------------------------
@@ -1267,7 +1283,7 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
 }  // extern "C"
 
 // conv_os over sources (c_in channels) or over the channel concatenation
-// [sources | sources2] (c_in + c_in2 channels; fp16, c_in % 16 == 0,
+// [sources | sources2] (c_in + c_in2 channels; fp16, c_in % 32 == 0,
 // c_in2 % 8 == 0)
 static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out_in_map, const int32_t *row_order,
                         const uint64_t *group_masks, const void *sources, const void *sources2, int64_t num_sources,
@@ -1275,8 +1291,8 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
                         void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
                         int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_os: dtype must be fp16 or fp32");
-  SPIRA_HIP_REQUIRE(c_in2 == 0 || (sources2 && dtype == SPIRA_F16 && c_in % 16 == 0 && c_in2 % 8 == 0),
-                    "conv_os_concat: fp16 only, the first part's channels a multiple of 16, the second's of 8");
+  SPIRA_HIP_REQUIRE(c_in2 == 0 || (sources2 && dtype == SPIRA_F16 && c_in % 32 == 0 && c_in2 % 8 == 0),
+                    "conv_os_concat: fp16 only, the first part's channels a multiple of 32, the second's of 8");
   SPIRA_HIP_REQUIRE(out_mode >= SPIRA_OUT_STORE && out_mode <= SPIRA_OUT_ADD_F32, "conv_os: bad out_mode");
   SPIRA_HIP_REQUIRE(c_in2 == 0 || out_mode == SPIRA_OUT_STORE, "conv_os_concat: storage-dtype outputs only");
   SPIRA_HIP_REQUIRE(c_in > 0 && c_out > 0 && num_offsets > 0, "conv_os: empty channel / offset dimension");

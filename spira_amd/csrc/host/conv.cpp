@@ -233,7 +233,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   const int dtype = dtype_of(X0);
   // a channel concatenation [X0 | X2] is gathered from its two parts when
   // the split falls on a 16-channel slice (fp16), else materialised here
-  const bool split = X2 && dtype == SPIRA_F16 && X0.size(1) % 16 == 0 && X2->size(1) % 8 == 0;
+  const bool split = X2 && dtype == SPIRA_F16 && X0.size(1) % 32 == 0 && X2->size(1) % 8 == 0;
   const torch::Tensor X = (X2 && !split) ? torch::cat({X0, *X2}, 1) : X0;
   const int32_t *mp = nullptr;
   if (map) {

@@ -160,11 +160,11 @@ def test_dense_forward(dev, dtype, cin, cout):
     assert rel_err(np_(y.float()), _ref(ref_conv, scale, shift, res, True)) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("c1,c2", [(96, 32), (32, 32), (256, 128), (48, 24), (40, 24), (64, 3)])
+@pytest.mark.parametrize("c1,c2", [(96, 32), (32, 32), (256, 128), (48, 24), (16, 16), (40, 24), (64, 3)])
 def test_concat_input_without_copy(dev, keys, c1, c2):
     """A layer whose input is the channel concatenation [A | B] (a decoder's
     skip connection) gathers from the two parts when the split falls on a
-    16-channel slice, and materialises the concatenation otherwise; both
+    32-channel block, and materialises the concatenation otherwise; both
     match the oracle on the concatenated features, with the epilogue."""
     S = T = len(keys)
     g = torch.Generator().manual_seed(c1 + c2)
@@ -195,9 +195,9 @@ def test_lazy_cat_materialises_on_access(dev):
     assert c._parts is not None
     assert torch.equal(c.features, torch.cat([a.features, b.features], 1))
     assert c._parts is None
-    # splits off a 16-channel slice and fp32 parts are concatenated right away
-    e = spira_amd.SparseTensor(coordinates=a.coordinates, features=torch.randn(10, 24, device=dev).half())
+    # splits off a 32-channel block and fp32 parts are concatenated right away
+    e = spira_amd.SparseTensor(coordinates=a.coordinates, features=torch.randn(10, 48, device=dev).half())
     d = spira_amd.cat([e, b])
-    assert d._parts is None and d.features.shape == (10, 40)
+    assert d._parts is None and d.features.shape == (10, 64)
     f = spira_amd.SparseTensor(coordinates=a.coordinates, features=torch.randn(10, 32, device=dev))
     assert spira_amd.cat([f, f])._parts is None
