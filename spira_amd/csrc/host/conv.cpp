@@ -112,6 +112,17 @@ static int64_t row_order_min_targets() {
   }();
   return v;
 }
+// Maps of fewer offsets than this (SPIRA_OS_ROW_ORDER_MIN_K, default 27)
+// skip the row order: a k = 2 down / up-sampling map serves a single layer,
+// and its sort costs more than that layer saves (config-4 network: 3.28 ->
+// 3.07 ms per step without the order of its two k = 2 maps)
+static int64_t row_order_min_offsets() {
+  static const int64_t v = [] {
+    const char *e = std::getenv("SPIRA_OS_ROW_ORDER_MIN_K");
+    return e ? std::atoll(e) : int64_t(27);
+  }();
+  return v;
+}
 void set_row_order(bool on) { row_order_flag() = on; }
 
 static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
@@ -254,7 +265,8 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128) {
+  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128 &&
+      K >= row_order_min_offsets()) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
