@@ -124,6 +124,11 @@ static int64_t row_order_min_offsets() {
   return v;
 }
 void set_row_order(bool on) { row_order_flag() = on; }
+// whether the fp16 output-stationary kernel walks a map of T targets and K
+// offsets in row order
+static bool row_order_applies(int64_t T, int64_t K) {
+  return row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128 && K >= row_order_min_offsets();
+}
 
 static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
   auto &cache = order_cache();
@@ -155,6 +160,25 @@ static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
                                     e.ordered_map.data_ptr<int32_t>(), ws.data_ptr(), wsb, current_stream()),
            "row_order");
   return cache.emplace(key, std::move(e)).first->second;
+}
+
+// Queue the row order of an output-stationary map now, on the current
+// stream, if the fp16 kernel would use one for it (same rule as run_os), so
+// that it is computed before the first layer needs it.  Returns its tensors
+// (order, group masks, ordered map; for a caller that made them on another
+// stream than the one that will read them), or nothing if the kernel uses
+// no row order for this map.  No reference counterpart (the row order is
+// this build's own).
+std::vector<torch::Tensor> prepare_row_order(const torch::Tensor &map, int64_t T) {
+  SPIRA_CHECK_ARG(map.dim() == 2 && map.scalar_type() == torch::kInt32, "out_in_map must be 2-D int32");
+  require_device(map, "out_in_map");
+  SPIRA_CHECK_ARG(map.size(0) >= T, "out_in_map has fewer rows than targets");
+  const int64_t K = map.size(1);
+  if (!row_order_applies(T, K)) return {};
+  const OrderEntry &e = row_order_of(map, T);
+  std::vector<torch::Tensor> out{e.order, e.ordered_map};
+  if (e.masks.defined()) out.push_back(e.masks);
+  return out;
 }
 
 // The row order of an output-stationary map as the fp16 kernel uses it:
@@ -265,8 +289,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128 &&
-      K >= row_order_min_offsets()) {
+  if (map && dtype == SPIRA_F16 && row_order_applies(T, K)) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
@@ -640,6 +663,7 @@ void register_conv(pybind11::module_ &m) {
   m.def("cuda_reset_error", &reset_error);
   m.def("set_os_row_order", &set_row_order);
   m.def("kmap_row_order", &kmap_row_order);
+  m.def("prepare_row_order", &prepare_row_order);
 }
 
 }  // namespace spira_host

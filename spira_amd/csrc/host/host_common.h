@@ -7,6 +7,8 @@
 #include <ATen/hip/HIPContext.h>
 #include <c10/hip/HIPStream.h>
 
+#include <map>
+#include <mutex>
 #include <optional>
 #include <sstream>
 #include <string>
@@ -65,24 +67,21 @@ inline torch::Tensor workspace(size_t bytes, const torch::Device &dev) {
 class StreamFan {
  public:
   StreamFan(const torch::Device &dev, size_t n) : main_(current_stream()) {
-    hipEvent_t e;
-    check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    if (n == 0) return;
+    hipEvent_t e = event(0);
     check_hip(hipEventRecord(e, main_));
     for (size_t i = 0; i < n; ++i) {
       side_.push_back(c10::hip::getStreamFromPool(false, dev.index()));
       check_hip(hipStreamWaitEvent(side_.back().stream(), e, 0));
     }
-    check_hip(hipEventDestroy(e));
   }
   hipStream_t operator[](size_t i) const { return side_[i].stream(); }
   size_t size() const { return side_.size(); }
   void join() {
-    for (auto &s : side_) {
-      hipEvent_t e;
-      check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-      check_hip(hipEventRecord(e, s.stream()));
+    for (size_t i = 0; i < side_.size(); ++i) {
+      hipEvent_t e = event(i + 1);
+      check_hip(hipEventRecord(e, side_[i].stream()));
       check_hip(hipStreamWaitEvent(main_, e, 0));
-      check_hip(hipEventDestroy(e));
     }
     side_.clear();
   }
@@ -95,6 +94,20 @@ class StreamFan {
  private:
   static void check_hip(hipError_t e) {
     if (e != hipSuccess) fail("HIP error: ", hipGetErrorString(e));
+  }
+  // Timing-free events, created once per (device, slot) and reused: an
+  // event may be recorded again once the waits on its previous record are
+  // enqueued (each wait captures the record it follows), and creating and
+  // destroying events costs more host time than the fan-out's launches.
+  static hipEvent_t event(size_t slot) {
+    int dev = 0;
+    check_hip(hipGetDevice(&dev));
+    static std::mutex mu;
+    static std::map<std::pair<int, size_t>, hipEvent_t> pool;
+    std::lock_guard<std::mutex> lock(mu);
+    auto &e = pool[{dev, slot}];
+    if (!e) check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    return e;
   }
   hipStream_t main_;
   std::vector<c10::hip::HIPStream> side_;

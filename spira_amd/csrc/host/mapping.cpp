@@ -174,26 +174,37 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
   auto sizes_host = torch::empty({static_cast<int64_t>(std::max<size_t>(2 * n, 2))},
                                  torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
   std::vector<KmapTuple> out;
-  StreamFan fan(dev, n);
+  // Output-stationary maps are one search kernel each: they go on the
+  // current stream back to back (a stream fan-out costs more host time per
+  // map than the kernel takes; measured end to end, either way gives the
+  // same step time).  The other dataflows run several kernels and
+  // a size read-back per map: one pool stream each.
+  std::vector<size_t> side_of(n, 0);
+  size_t nside = 0;
+  for (size_t i = 0; i < n; ++i)
+    if (dataflow[i] != 0) side_of[i] = nside++;
+  StreamFan fan(dev, nside);
+  const hipStream_t cur = current_stream();
+  auto stream_of = [&](size_t i) { return dataflow[i] == 0 ? cur : fan[side_of[i]]; };
   for (size_t i = 0; i < n; ++i) {
     // half maps: dataflow 2 uses the position in the list (mapping.cu:1129),
     // the other dataflows compare the set sizes (mapping.cu:955)
     const int half = (dataflow[i] == 2) ? (i % 2 == 0 ? 1 : 0) : -1;
     pending[i] = stage_map(voxels[i / 2], voxels[(i + 1) / 2], kernel_sizes[i], source_strides[i], dataflow[i],
-                           half, fan[i]);
+                           half, stream_of(i));
     if (dataflow[i] % 2 == 1) {
       SPIRA_CHECK_ARG(hipMemcpyAsync(sizes_host.data_ptr<int32_t>() + 2 * i, pending[i].sizes.data_ptr<int32_t>(),
-                                     2 * sizeof(int32_t), hipMemcpyDeviceToHost, fan[i]) == hipSuccess,
+                                     2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream_of(i)) == hipSuccess,
                       "size read-back failed");
     }
   }
   for (size_t i = 0; i < n; ++i)
     if (dataflow[i] % 2 == 1)
-      SPIRA_CHECK_ARG(hipStreamSynchronize(fan[i]) == hipSuccess, "stream synchronisation failed");
+      SPIRA_CHECK_ARG(hipStreamSynchronize(stream_of(i)) == hipSuccess, "stream synchronisation failed");
   for (size_t i = 0; i < n; ++i) {
     const int32_t *h = sizes_host.data_ptr<int32_t>() + 2 * i;
     out.push_back(finish_map(pending[i], dataflow[i] % 2 == 1 ? h[0] : 0, dataflow[i] % 2 == 1 ? h[1] : 0,
-                             fan[i]));
+                             stream_of(i)));
   }
   fan.join();
   return out;

@@ -34,6 +34,11 @@ class KernelMapCache:
     """Coordinates per tensor stride and kernel maps per
     ``(source stride, target stride, kernel size)``."""
 
+    #: queue the row orders of the large output-stationary maps with the
+    #: network-wide map build (only the fp16 convolution kernel uses them; a
+    #: network run in fp32 can turn this off to skip that work)
+    prepare_row_orders = True
+
     def __init__(self):
         self._kernel_maps_cache: Dict[tuple, list] = {}
         self._coordinates_cache: Dict[tuple, torch.Tensor] = {}
@@ -101,6 +106,10 @@ class KernelMapCache:
         for i, ts in enumerate(target_strides):
             self._coordinates_cache[as_tuple(ts, size=3)] = voxels[i + 1]
         kmaps = F.build_kmap_streamed(voxels, kernel_sizes, list(source_strides)[:-1], dataflow)
+        if self.prepare_row_orders:
+            for i, d in enumerate(dataflow):
+                if d == 0:
+                    F.prepare_row_order(kmaps[i][2], kmaps[i][1])
         for i in range(len(kernel_sizes)):
             t_stride = as_tuple(source_strides[i + 1], size=3)
             self._kernel_maps_cache[(s_stride, t_stride, as_tuple(kernel_sizes[i], size=3))] = [False, *kmaps[i]]

@@ -17,6 +17,7 @@ from ._native import _C
 __all__ = [
     "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os",
     "build_kmap_streamed", "streamed_output_generate", "build_kmap_no_small_z", "sparse_quantize",
+    "prepare_row_order",
 ]
 
 
@@ -64,6 +65,16 @@ def build_kmap_streamed(voxels: List[torch.Tensor], kernel_sizes: List[ScalarOrT
     if not (len(kernel_sizes) == len(source_strides) == len(dataflow)):
         raise ValueError("All argument lists must have the same length in build_kmap_streamed")
     return _C.cuda_binary_search_streamed(voxels, kernel_sizes, source_strides, list(dataflow))
+
+
+def prepare_row_order(kmap: torch.Tensor, num_targets: int) -> List[torch.Tensor]:
+    """Queue the row order of an output-stationary map on the current stream
+    if the fp16 convolution kernel will walk it in row order (large maps of
+    27 or more offsets), so that it is computed with the maps instead of at
+    the first layer that uses it.  Returns the row order's tensors (empty if
+    the map gets none)."""
+    _require_gpu(kmap)
+    return list(_C.prepare_row_order(kmap, int(num_targets)))
 
 
 def downsample(coordinates: torch.Tensor, target_stride: Tuple[int, int, int]) -> torch.Tensor:

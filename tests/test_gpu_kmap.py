@@ -238,3 +238,40 @@ def test_streamed_build_matches_single(dev, scene_small):
             half = (i % 2 == 0) if dfs[i] == 2 else None
             ref = orc.build_kmap(src, tgt, ks[i], ss[i], dfs[i], half=half)
             assert_tuple_equal(m, ref, f"streamed map {i} dataflow {dfs[i]}")
+
+
+@pytest.mark.parametrize("prepare", [True, False])
+@pytest.mark.parametrize("df", [0, 1, 2])
+def test_network_wide_cache_build(dev, prepare, df):
+    """KernelMapCache.add_all_kernel_maps (output-stationary maps on the
+    current stream, the other dataflows on one pool stream each, row orders
+    queued with the build) caches, for every layer, the map the oracle builds
+    for that layer's voxel sets; a row order queued at build time is the one
+    a layer would compute itself."""
+    import spira_amd
+    from spira_amd.networks import kmap_schedule
+    from spira_amd.nn.functional import _native
+    coords = scenes.indoor(target=120_000, seed=3)
+    rk, _ = orc.flatten_sort(coords, True)
+    cache = spira_amd.nn.KernelMapCache()
+    cache.prepare_row_orders = prepare
+    x = spira_amd.SparseTensor(coordinates=torch.from_numpy(coords).to(dev),
+                               features=torch.zeros(len(coords), 3, device=dev).half(), double=True)
+    x.order()
+    ts, ks, ss = kmap_schedule("UNet")
+    cache.add_all_kernel_maps(x._coordinates, ks, ss, ts, (1, 1, 1), [df] * len(ks))
+    vox = {(1, 1, 1): rk}
+    for t in ts:
+        vox[t] = orc.downsample(rk, t)
+        assert np.array_equal(np_(cache._coordinates_cache[t]), vox[t]), f"coordinates at stride {t}"
+    for i, k in enumerate(ks):
+        s_src, s_tgt = ss[i], ss[i + 1]
+        entry = cache._kernel_maps_cache[(s_src, s_tgt, k)]
+        half = (i % 2 == 0) if df == 2 else None
+        ref = orc.build_kmap(vox[s_src], vox[s_tgt], k, s_src, df, half=half)
+        assert_tuple_equal(tuple(entry[1:]), ref, f"cached map {i} dataflow {df}")
+        if df == 0 and entry[2] >= 100_000 and int(np.prod(k)) >= 27:
+            m, T = entry[3], entry[2]
+            order, masks, omap = _native._C.kmap_row_order(m, T)
+            o2, m2, om2 = _native._C.kmap_row_order(m.clone(), T)  # computed afresh
+            assert torch.equal(order, o2) and torch.equal(masks, m2) and torch.equal(omap, om2)
