@@ -124,7 +124,7 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int MAP_TILE = BM * MAP_TILE_K * 4;  // the block's map rows, after the ring
   static constexpr int LDS = RING + MAP_TILE > OUT_STAGE ? RING + MAP_TILE : OUT_STAGE;
   static constexpr int LPS = MT * NKS + BVEC;  // vector-memory loads per wave and step
-  static_assert(NKS == 2 || NKS == 4, "a step is 32 or 64 channels");
+  static_assert(NKS == 2 || NKS == 4 || NKS == 8, "a step is 32, 64 or 128 channels");
   static_assert(MT == 1, "a wave owns 32 rows: two 16-row MFMA tiles");
   // every LDS read offset of a stage is an instruction immediate (< 64 KiB)
   static_assert((NS - 1) * STAGE + (WN - 1) * 32 * ROWB < 65536, "weight read offset exceeds 16 bits");
@@ -134,7 +134,9 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   // conflict-free when their byte addresses differ mod 256 (64 banks): rows
   // of ROWB = 64 (128) bytes take 4 (2) positions from n, the swizzle the
   // other 4 (8) from n >> 2 (n >> 1)
-  __host__ __device__ static constexpr int swz(int n) { return NKS == 2 ? (n >> 2) & 3 : (n >> 1) & 7; }
+  __host__ __device__ static constexpr int swz(int n) {
+    return NKS == 2 ? (n >> 2) & 3 : (NKS == 4 ? (n >> 1) & 7 : n & 15);
+  }
 };
 
 // Tile shape per column-tile width and step: one 32-row tile per wave (the
@@ -143,7 +145,7 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
 // up to 96 columns (<= 128 VGPRs, four 40 KiB blocks per CU), 3 for 128.
 template <int WN, int NKS = 2> struct TileOf {
   static constexpr int MT = 1;
-  static constexpr int NS = NKS == 2 ? (WN >= 3 ? 3 : 4) : (WN >= 3 ? 2 : 3);
+  static constexpr int NS = NKS == 2 ? (WN >= 3 ? 3 : 4) : (NKS == 8 || WN >= 3 ? 2 : 3);
   static constexpr int WAVES = WN <= 3 ? 4 : 3;
   using C = Cfg<WN, MT, NS, NKS>;
 };
@@ -1142,10 +1144,22 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
 // 16-channel slices per step of the output-stationary kernel: 64-channel
 // steps once the (padded) input has 64 channels or more, else 32.
 // SPIRA_OS_KC=32 / 64 overrides (measurements).
-static int os_nks(int CinP) {
+// 128-channel steps (one step per offset for 96 and 128 channels) when the
+// padded input is 96 or a multiple of 128 channels (no half-empty step), and
+// either the column tile is at most 96 wide or the grid has at most 1.5
+// blocks per CU: the widest tile's 128-channel weight stages hold a block at
+// 80 KiB of LDS, which costs more occupancy than the halved steps save on
+// larger grids.  (Measured on the config-4 layers: 96 -> 96 at 200k voxels
+// 52.3 -> 46.6 us, 256 -> 256 at stride 8 111.6 -> 101.7 us; 128 -> 128 at
+// stride 4, 529 blocks of the widest tile, 79.7 -> 92.7 us, so it keeps
+// 64-channel steps.)  SPIRA_OS_KC=32 / 64 / 128 overrides (measurements).
+static int os_nks(int CinP, int wn, int64_t blocks, int cus) {
   static const int kc = env_int("SPIRA_OS_KC", 0);
   if (kc == 32) return 2;
-  if (kc == 64) return 4;
+  if (kc == 64) return CinP >= 64 ? 4 : 2;
+  if (kc == 128) return CinP >= 96 ? 8 : (CinP >= 64 ? 4 : 2);
+  if ((CinP == 96 || CinP % 128 == 0) && CinP >= 96 && (wn <= 3 || 2 * blocks <= 3 * static_cast<int64_t>(cus)))
+    return 8;
   return CinP >= 64 ? 4 : 2;
 }
 
@@ -1153,15 +1167,18 @@ template <int MODE>
 static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                           const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                           void *Y, const Epilogue &epi) {
+  const int nks = os_nks(op.CinP, wn, static_cast<int64_t>(grid.x) * grid.y * grid.z, device_cu_count());
   const bool cat = op.X2 != nullptr;
   if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
   else if (cat) {
     // channel concatenations: storage-dtype outputs (split or not)
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
-      if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
       else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
     }
-  } else if (os_nks(op.CinP) == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  } else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
   else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
 }
 
