@@ -1271,16 +1271,20 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
 }
 
 // Column-tile width of the output-stationary kernel: the widest tile, made
-// narrower (more column blocks, each re-gathering its rows) while the grid
-// has fewer than SPIRA_OS_MIN_BLOCKS (default 1) blocks per CU.  (Measured
-// on the end-to-end network: more than one block per CU this way, or by
-// more offset splits, costs more in re-gathered rows / atomics than the
-// added occupancy returns.)
+// narrower once (more column blocks, each re-gathering its rows) when the
+// grid has fewer than SPIRA_OS_MIN_BLOCKS (default 1) blocks per CU; a grid
+// still short of the CUs then splits its offsets (choose_jper).  (Measured
+// on the config-4 layers: s8 128 -> 128, 134 row blocks, is fastest with
+// one halving (42.9 us, 46.7 us without); s16 256 -> 256, 32 row blocks,
+// took 53.0 us narrowed down to 32-column tiles against 34.8 us without,
+// as every narrowing multiplies the gathered rows.  More than one block per
+// CU this way, or by more offset splits, costs more in re-gathered rows /
+// atomics than the added occupancy returns.)
 static int os_wn(int64_t num_targets, int c_out, int cus) {
   static const int mult = env_int("SPIRA_OS_MIN_BLOCKS", 1);
   int wn = wn_for(c_out);
   const int64_t bx = div_up(num_targets, bm_for(1));
-  while (wn > 1 && bx * div_up(pad_out(c_out), 32 * wn) < static_cast<int64_t>(mult) * cus) wn = wn == 3 ? 1 : wn / 2;
+  if (wn > 1 && bx * div_up(pad_out(c_out), 32 * wn) < static_cast<int64_t>(mult) * cus) wn = wn == 3 ? 1 : wn / 2;
   return wn;
 }
 
