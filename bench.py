@@ -9,6 +9,9 @@ inside one event-timed region.  Also reported on the same run:
   * kmap_build_us: one kernel-map search (config 2, ~100k LiDAR voxels,
     k=3, 64-bit keys, output-stationary layout) as in mapping_experiment.py;
   * layer_ms: one output-stationary fp16 layer (config 3, C=64);
+  * config5_ms: the large-kernel network of config 5 (SparseResNetLarge, k=5,
+    fp16) end to end on the ~300k-voxel LiDAR-plus-blobs scene, timed like
+    the headline (10 steps after 5 warm-ups);
   * roofline: the dominant kernel (output-stationary MFMA conv) against its
     binding roofline -- HBM for the full-resolution 96->96 layer, whose
     algorithmic bytes take longer at peak bandwidth than its flops at peak
@@ -50,7 +53,7 @@ def parse():
     p.add_argument("--dataflow", type=int, default=0, help="map dataflow used by every layer")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-fuse", action="store_true", help="run batch norm / ReLU / residual adds unfused")
-    p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer (calib: a plain 256 MiB "
+    p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer,config5 (calib: a plain 256 MiB "
                                               "device copy, the reference point of the HBM byte counters)")
     return p.parse_args()
 
@@ -77,12 +80,18 @@ class Timer:
         return float(np.mean(times)), float(np.min(times))
 
 
-def e2e_leg(torch, args, coords_np):
+def e2e_leg(torch, args, coords_np, net="UNet", steps=None, warmup=None):
+    """End-to-end step of `net` (UNet: SparseResUNet42, config 4; ResNetLarge:
+    the k = 5 SparseResNetLarge, config 5): map cache reset, order(), the
+    network-wide map build and the forward pass, event-timed."""
     import spira_amd
-    from spira_amd.networks import SparseResUNet42, kmap_schedule
+    from spira_amd.networks import SparseResNetLarge, SparseResUNet42, kmap_schedule
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    model = SparseResUNet42(in_channels=3).to(dev).half().eval()
+    cin = 3 if net == "UNet" else 4
+    model = (SparseResUNet42 if net == "UNet" else SparseResNetLarge)(in_channels=cin).to(dev).half().eval()
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     if not args.no_fuse:
         spira_amd.nn.fuse_epilogues(model)
     cache = spira_amd.nn.KernelMapCache()
@@ -90,9 +99,9 @@ def e2e_leg(torch, args, coords_np):
     for m in model.modules():
         if isinstance(m, spira_amd.nn.SparseConv):
             m._tunable_config["map_dataflow"] = args.dataflow
-    ts, ks, ss = kmap_schedule("UNet")
+    ts, ks, ss = kmap_schedule(net)
     coords = torch.from_numpy(coords_np).to(dev)
-    feats = torch.randn(coords.shape[0], 3, device=dev, dtype=torch.float16)
+    feats = torch.randn(coords.shape[0], cin, device=dev, dtype=torch.float16)
 
     def step():
         cache.reset()
@@ -102,18 +111,18 @@ def e2e_leg(torch, args, coords_np):
         return model(x)
 
     with torch.no_grad():
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             step()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         s.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             out = step()
         e.record()
         torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) * 1e3 / args.steps
-        ms = s.elapsed_time(e) / args.steps
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        ms = s.elapsed_time(e) / steps
     return ms, wall, model, [o._features for o in out]
 
 
@@ -197,70 +206,10 @@ def calib_leg(torch, mib=256, reps=5):
 # CPU baseline: the same end-to-end pipeline on the host through the oracle
 # ---------------------------------------------------------------------------
 def cpu_e2e(model, coords_np, feats_np):
-    import torch
-    from oracle import oracle as orc
-    from spira_amd import nn as spnn
-    from spira_amd.networks import SparseResBlock
-
-    keys, perm = orc.flatten_sort(coords_np, True)
-    x = np.ascontiguousarray(feats_np[perm], dtype=np.float32)
-    vox = {(1, 1, 1): keys}
-    maps = {}
-
-    def coords_of(stride):
-        if stride not in vox:
-            vox[stride] = orc.downsample(keys, stride)
-        return vox[stride]
-
-    def conv(layer, feats, stride):
-        W = layer.kernel.detach().float().cpu().numpy()
-        if layer.is_trivial:
-            return feats @ W[0], stride
-        if layer.transposed:
-            out_stride = tuple(a // b for a, b in zip(stride, layer.stride))
-            key = (out_stride, stride, layer.kernel_size)
-            if key not in maps:
-                maps[key] = orc.search(coords_of(out_stride), coords_of(stride), layer.kernel_size, out_stride, orc.OS)
-            tmap = orc.convert_transposed_os(maps[key], len(coords_of(out_stride)))
-            return orc.conv_os_f32(tmap, len(coords_of(out_stride)), feats, W), out_stride
-        out_stride = tuple(a * b for a, b in zip(stride, layer.stride))
-        key = (stride, out_stride, layer.kernel_size)
-        if key not in maps:
-            maps[key] = orc.search(coords_of(stride), coords_of(out_stride), layer.kernel_size, stride, orc.OS)
-        return orc.conv_os_f32(maps[key], len(coords_of(out_stride)), feats, W), out_stride
-
-    def run(mod, feats, stride):
-        if isinstance(mod, spnn.SparseConv):
-            return conv(mod, feats, stride)
-        if isinstance(mod, spnn.BatchNorm):
-            rm, rv = mod.running_mean.float().cpu().numpy(), mod.running_var.float().cpu().numpy()
-            g, b = mod.weight.detach().float().cpu().numpy(), mod.bias.detach().float().cpu().numpy()
-            return (feats - rm) / np.sqrt(rv + mod.eps) * g + b, stride
-        if isinstance(mod, (spnn.ReLU,)):
-            return np.maximum(feats, 0), stride
-        if isinstance(mod, torch.nn.Identity):
-            return feats, stride
-        if isinstance(mod, SparseResBlock):
-            a, s1 = run(mod.main, feats, stride)
-            b, _ = run(mod.shortcut, feats, stride)
-            return np.maximum(a + b, 0), s1
-        if isinstance(mod, torch.nn.Sequential):
-            for sub in mod:
-                feats, stride = run(sub, feats, stride)
-            return feats, stride
-        raise TypeError(type(mod))
-
-    def level(feats, stride, encoders, decoders):
-        if len(encoders) == 0:
-            return [(feats, stride)]
-        f2, s2 = run(encoders[0], feats, stride)
-        outs = level(f2, s2, encoders[1:], decoders[:-1])
-        up, su = run(decoders[-1]["upsample"], *outs[-1])
-        y, sy = run(decoders[-1]["fuse"], np.concatenate([up, feats], axis=1), su)
-        return [(feats, stride)] + outs + [(y, sy)]
-
-    f, s = run(model.stem, x, (1, 1, 1))
-    return level(f, s, list(model.encoders), list(model.decoders))
+    """The same network end to end on the host through the oracle (fp32,
+    OpenMP C restatement of the maps and convolutions)."""
+    from oracle.network import network_forward
+    return network_forward(model, coords_np, feats_np)
 
 
 def main():
@@ -272,7 +221,7 @@ def main():
     import torch
     from spira_amd import scenes
 
-    legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer"}
+    legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer", "config5"}
     with open(os.path.join(ROOT, "BASELINE.json")) as f:
         baseline = json.load(f)
 
@@ -289,6 +238,13 @@ def main():
         res["value"] = ms
         res["ms_per_step"] = ms
         res["wall_ms_per_step"] = wall
+    if "config5" in legs:
+        # config 5: the large-kernel (k = 5) SparseResNetLarge on the ~300k-voxel
+        # scene of merged LiDAR rings and Gaussian blobs, timed like config 4
+        blobs = scenes.lidar_blobs()
+        c5, _, _, _ = e2e_leg(torch, args, blobs, net="ResNetLarge", steps=10, warmup=5)
+        res["config5_ms"] = c5
+        cfg["config5_voxels"] = int(blobs.shape[0])
     lidar = scenes.lidar()
     from oracle import oracle as orc
     lkeys, _ = orc.flatten_sort(lidar, True)

@@ -433,8 +433,20 @@ __global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict
                                                        KT *__restrict__ keys, int32_t *__restrict__ iota) {
   extern __shared__ int32_t rows_lds[];
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RB;
-  const int64_t nr = (T - row0) < RB ? (T - row0) : RB;
-  for (int64_t e = threadIdx.x; e < nr * K; e += 256) rows_lds[e] = map[row0 * K + e];
+  const int nr = static_cast<int>((T - row0) < RB ? (T - row0) : RB);
+  // the block's rows are one contiguous run of nr * K words: 16-byte loads
+  // where the run is 16-byte aligned, several in flight per thread
+  const int32_t *src = map + row0 * K;
+  const int n = nr * K;
+  int head = 0;
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    const int n4 = n / 4;
+#pragma unroll 4
+    for (int e = threadIdx.x; e < n4; e += 256)
+      reinterpret_cast<int4 *>(rows_lds)[e] = reinterpret_cast<const int4 *>(src)[e];
+    head = n4 * 4;
+  }
+  for (int e = head + static_cast<int>(threadIdx.x); e < n; e += 256) rows_lds[e] = src[e];
   __syncthreads();
   if (threadIdx.x >= nr) return;
   const int32_t *row = rows_lds + threadIdx.x * K;
@@ -577,15 +589,26 @@ __global__ __launch_bounds__(256) void order_rows_kernel(const int32_t *__restri
   const int64_t n = rows * K;
   uint64_t m[2][2] = {{0, 0}, {0, 0}};
   if (ordered || reduce) {
-    for (int64_t e = threadIdx.x; e < n; e += 256) {
-      const int64_t r = e / K;
-      const int c = static_cast<int>(e - r * K);
+    // element e = r * K + c of the block's rows (e < 256 K: 32-bit), walked
+    // with an incremental (r, c) instead of a division per element
+    const int ni = static_cast<int>(n);
+    const int dr = 256 / K, dc = 256 - dr * K;
+    int r = static_cast<int>(threadIdx.x) / K, c = static_cast<int>(threadIdx.x) - r * K;
+    int32_t *dst = ordered ? ordered + row0 * K : nullptr;
+#pragma unroll 4
+    for (int e = threadIdx.x; e < ni; e += 256) {
       const int32_t v = map[static_cast<int64_t>(src_s[r]) * K + c];
-      if (ordered) ordered[row0 * K + e] = v;
+      if (ordered) dst[e] = v;
       if (reduce && v >= 0 && c < 128) {
         const int gi = r >= 128 ? 1 : 0;
         if (c < 64) m[gi][0] |= uint64_t(1) << c;
         else m[gi][1] |= uint64_t(1) << (c - 64);
+      }
+      r += dr;
+      c += dc;
+      if (c >= K) {
+        c -= K;
+        ++r;
       }
     }
   }
