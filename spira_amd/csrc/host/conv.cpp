@@ -124,10 +124,24 @@ static int64_t row_order_min_offsets() {
   return v;
 }
 void set_row_order(bool on) { row_order_flag() = on; }
+// Maps of more offsets than this (SPIRA_OS_ROW_ORDER_MAX_K, default 57) skip
+// the row order: above 57 columns the sort keys cannot hold the column mask,
+// the order takes 64-bit keys and a second pass over the map, and for the
+// 125-offset maps of config 5 it cost more than it saved (SparseResNetLarge
+// on the 300k-voxel scene: 6.61 ms per step with it, 5.87 ms without).
+static int64_t row_order_max_offsets() {
+  static const int64_t v = [] {
+    const char *e = std::getenv("SPIRA_OS_ROW_ORDER_MAX_K");
+    return e ? std::atoll(e) : int64_t(57);
+  }();
+  return v;
+}
+
 // whether the fp16 output-stationary kernel walks a map of T targets and K
 // offsets in row order
 static bool row_order_applies(int64_t T, int64_t K) {
-  return row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128 && K >= row_order_min_offsets();
+  return row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128 && K >= row_order_min_offsets() &&
+         K <= row_order_max_offsets();
 }
 
 static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
