@@ -8,22 +8,23 @@
 //  * gather -> grouped GEMM -> scatter over per-offset masks
 //    (padded_gather/scatter_warp_optimized.cuh, sparse_convolution.cu:488-1124).
 //
-// MI355X design (fp16 storage, fp32 accumulation on v_mfma_f32_32x32x16_f16).
+// MI355X design (fp16 storage, fp32 accumulation on v_mfma_f32_16x16x32_f16).
 // All three dataflows share one MMA core:
-//  * a block is 4 waves; a wave owns a tile of 32 rows x 32*WN columns (WN
-//    accumulators of 16 floats); WN = 1, 2, 3 or 4 (wider layers take
-//    several 128-column tiles), so that 96-channel layers do not pad to a
-//    power of two.  The tiles are small on purpose: the kernels are bound by
-//    latency, not by any one unit, and small tiles let 3-4 waves share each
-//    SIMD;
-//  * the K dimension is walked in steps of 32 or 64 input channels of one
-//    kernel offset.  The offset's weight chunk (shared by the four waves)
-//    lands in a 2-4 stage LDS ring through global_load_lds_dwordx4 (direct
-//    HBM/L2 -> LDS)
-//    with an XOR swizzle that makes the B reads conflict-free; the gathered
-//    rows (private to a wave) are loaded straight into the registers of the
-//    MFMA A operand (lane L fetches exactly the 16 bytes its A slot needs).
-//    Loads run two steps ahead of the MFMAs; a step costs one workgroup
+//  * a block is 4 waves; a wave owns a tile of 32 rows (two 16-row MFMA
+//    tiles) x 32*WN columns; WN = 1, 2, 3 or 4 (wider layers take several
+//    128-column tiles), so that 96-channel layers do not pad to a power of
+//    two.  The tiles are small on purpose: the kernels are bound by the
+//    latency of their gathers, not by any one unit, and small tiles let 2-4
+//    waves share each SIMD;
+//  * the K dimension is walked in steps of 32, 64 or 128 input channels of
+//    one kernel offset.  The offset's weight chunk (shared by the four waves)
+//    lands in a 2-4 stage LDS ring through buffer_load ... lds (direct
+//    HBM/L2 -> LDS) with an XOR swizzle that makes the B reads
+//    conflict-free; the gathered rows (private to a wave) are loaded straight
+//    into the registers of the MFMA A operand (lane L fetches exactly the 16
+//    bytes its A slot needs: one load covers 16 rows x 64 bytes).  Loads run
+//    NS - 1 steps ahead of the MFMAs and are issued slice by slice between
+//    the current step's weight reads and MFMAs; a step costs one workgroup
 //    barrier and one vmcnt wait, and rows without a neighbour read a 16-byte
 //    zero block instead of branching;
 //  * weights are prepared once per weight tensor into [K, CoutP, CinP]
@@ -102,11 +103,11 @@ namespace ring {
 // Ring layout: stage s at byte s * STAGE holds the step's weight chunk
 // (BN rows x ROWB = KC * 2 bytes, 16-byte chunks XOR-swizzled per row),
 // shared by the block's four waves.  The gathered rows are private to a wave
-// and go straight into registers (one 16-byte buffer load per lane, tile and
-// 16-channel slice: the MFMA A layout), so they cost no LDS bandwidth.  A
-// step covers KC = 16 * NKS input channels of one kernel offset: NKS = 2
-// (32 channels) or 4 (64 channels, fewer steps and so less per-step
-// synchronisation for wide layers).
+// and go straight into registers (one 16-byte buffer load per lane, 16-row
+// tile and 32-channel block: the MFMA A layout), so they cost no LDS
+// bandwidth.  A step covers KC = 16 * NKS input channels of one kernel
+// offset: NKS = 2, 4 or 8 (32, 64 or 128 channels: fewer steps and so less
+// per-step synchronisation for wide layers).
 template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int NS = NS_;  // ring depth: NS - 1 steps load while one computes
   static constexpr int NKS = NKS_;
@@ -580,8 +581,8 @@ __device__ int64_t g_block_times[1 << 20];
 #define SPIRA_STAMP(slot)
 #endif
 
-// Output-stationary implicit GEMM.  A block owns BM = 128*MT logical rows
-// (wave w: rows [w*32*MT, (w+1)*32*MT) as MT tiles of 32) and BN = 32*WN
+// Output-stationary implicit GEMM.  A block owns BM = 128 logical rows
+// (wave w: rows [32 w, 32 w + 32) as two 16-row MFMA tiles) and BN = 32*WN
 // output channels; grid = (row blocks, column blocks, offset splits), split z
 // covering offsets [z*jper, min(Kc, (z+1)*jper)), jper <= 128.  With `order`,
 // logical row i is target order[i] and `map` holds the rows in logical order;
@@ -643,8 +644,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   // copied into LDS once (row stride KP = Kc | 1 words, odd, so that the
   // per-row reads of one column are conflict-free) and every step reads its
   // column there.  Larger kernels: lane L of a wave fetches the entry of row
-  // L (MT = 2) or L % 32 (MT = 1) of the wave's rows for step u into the
-  // stage's index slot, NS steps ahead.  Rows past T read nothing (out of
+  // L % 32 of the wave's rows for step u into the stage's index slot, NS
+  // steps ahead (lane l then reads the entries of rows l % 16 and 16 + l % 16).  Rows past T read nothing (out of
   // range) and are masked when resolved.  No map: the identity (logical row
   // i reads source i); the fetches then load nothing (out of range) but keep
   // the vmcnt arithmetic.
@@ -1142,8 +1143,7 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
 }
 
 // 16-channel slices per step of the output-stationary kernel: 64-channel
-// steps once the (padded) input has 64 channels or more, else 32.
-// SPIRA_OS_KC=32 / 64 overrides (measurements).
+// steps once the (padded) input has 64 channels or more, else 32; and
 // 128-channel steps (one step per offset for 96 and 128 channels) when the
 // padded input is 96 or a multiple of 128 channels (no half-empty step), and
 // either the column tile is at most 96 wide or the grid has at most 1.5
