@@ -216,12 +216,14 @@ template <class C> __device__ __forceinline__ ReadBase<C::NKS> read_base(const c
 // by instruction issue, not by the memory system).
 template <class C> struct IssueCtx {
   uint32_t wlane[C::BVEC];  // byte offset of the lane's weight chunk in an (offset, kb = 0) block, or kOutOfRange
-  int c8[C::BVEC];          // first input channel of that chunk
+  int c8[C::BVEC];          // first input channel of that chunk (OP = 2: 0 / 1, the step's offset it belongs to)
   uint32_t ldsw;            // LDS address of the wave's DMA slot in stage 0 (wave-uniform)
   uint32_t kh16;            // byte offset of the lane's quarter of a 32-channel block
   int kh8;                  // its first channel
 };
-template <class C>
+// OP = 2 (two kernel offsets per step, KC = 2 CinP): channel c of a step is
+// channel c % CinP of the step's offset c / CinP.
+template <class C, int OP = 1>
 __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int n0, const Operands &op) {
   IssueCtx<C> cx;
   const int tid = threadIdx.x & 255;
@@ -230,9 +232,11 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
     const int v = i * 256 + tid;
     const int n = v / C::CPR;
     const int c8 = ((v % C::CPR) ^ C::swz(n)) * 8;
-    cx.wlane[i] = (n < C::BN && n0 + n < op.CoutP) ? static_cast<uint32_t>(((n0 + n) * op.CinP + c8) * 2)
+    const int part = OP == 2 ? c8 / op.CinP : 0;
+    const int ch = c8 - part * op.CinP;
+    cx.wlane[i] = (n < C::BN && n0 + n < op.CoutP) ? static_cast<uint32_t>(((n0 + n) * op.CinP + ch) * 2)
                                                      : kOutOfRange;
-    cx.c8[i] = c8;
+    cx.c8[i] = OP == 2 ? part : c8;
   }
   cx.ldsw = __builtin_amdgcn_readfirstlane(lds_addr(ring) + wave * 64 * 16);
   cx.kh8 = ((threadIdx.x & 63) >> 4) * 8;
@@ -245,10 +249,11 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
 // weight row wrow, first input channel kb; !live: a step past the end (every
 // load out of range, so that each wave issues the same number of loads in
 // every step).
+// OP = 2: idx2 / wrow2 / live2 describe the step's second offset.
 struct StepIn {
-  bool live;
-  int32_t idx[2];
-  int wrow, kb;
+  bool live, live2;
+  int32_t idx[2], idx2[2];
+  int wrow, wrow2, kb;
 };
 
 // Issue the loads of slice KS of a step into ring stage S: the A fragment
@@ -260,12 +265,37 @@ struct StepIn {
 // input is a channel concatenation [X | X2] (each 32-channel block lies
 // wholly in one part, C1 % 32 == 0).  The offsets use 32-bit arithmetic:
 // every operand is below 2 GiB.
-template <class C, bool ALIGNED, bool CAT, int S, int KS>
+//
+// OP = 2 (offset packing for 16- and 32-channel inputs, KC = 2 CinP): the
+// step's channels [0, CinP) belong to offset 1 (idx, wrow), [CinP, 2 CinP)
+// to offset 2 (idx2, wrow2); the lane picks its row and weight row by the
+// part its channels fall in.
+template <class C, bool ALIGNED, bool CAT, int S, int KS, int OP = 1>
 __device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
                                             __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
                                             __amdgpu_buffer_rsrc_t wr, half8 (&a)[1][C::NKS]) {
   constexpr int rt = KS & 1;
   const int k0 = st.kb + (KS >> 1) * 32;
+  if constexpr (OP == 2) {
+    static_assert(ALIGNED && !CAT, "offset packing: aligned rows of one source");
+    const int k = k0 + cx.kh8;  // the lane's channel within the step
+    const bool part = k >= op.CinP;
+    const int ch = part ? k - op.CinP : k;
+    const int32_t ix = part ? st.idx2[rt] : st.idx[rt];
+    const bool ok = (part ? st.live2 : st.live) & (ix >= 0) & (ch < op.Cin);
+    const uint32_t at = static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.Cin * 2) + static_cast<uint32_t>(ch * 2);
+    a[0][KS] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at : kOutOfRange, 0, 0));
+    const uint32_t ws1 = static_cast<uint32_t>(st.wrow * op.CoutP * op.CinP * 2);
+    const uint32_t ws2 = static_cast<uint32_t>(st.wrow2 * op.CoutP * op.CinP * 2);
+#pragma unroll
+    for (int i = KS; i < C::BVEC; i += C::NKS) {
+      const bool p2 = cx.c8[i] != 0;
+      const uint32_t off = (p2 ? st.live2 : st.live) ? cx.wlane[i] + (p2 ? ws2 : ws1) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void_t *)(cx.ldsw + S * C::STAGE + i * 4096), 16, off, 0, 0,
+                                               0);
+    }
+    return;
+  }
   {
     constexpr int m = 0;
     // branch-free selects: a divergent branch here would make both sides
@@ -317,11 +347,12 @@ __device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn 
 }
 
 // Every load of a step, slice after slice (the prologue's steps).
-template <class C, bool ALIGNED, bool CAT, int S>
+template <class C, bool ALIGNED, bool CAT, int S, int OP = 1>
 __device__ __forceinline__ void issue(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
                                       __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
                                       __amdgpu_buffer_rsrc_t wr, half8 (&a)[1][C::NKS]) {
-  unroll<C::NKS>([&](auto KS) { issue_slice<C, ALIGNED, CAT, S, decltype(KS)::value>(cx, st, op, xr, xr2, wr, a); });
+  unroll<C::NKS>(
+      [&](auto KS) { issue_slice<C, ALIGNED, CAT, S, decltype(KS)::value, OP>(cx, st, op, xr, xr2, wr, a); });
 }
 
 // MFMAs of stage S (rows without a neighbour hold zeros): per 32-channel
@@ -369,8 +400,9 @@ __device__ __forceinline__ void compute(floatx4 (&acc)[2][C::BN / 16], const Rea
 //  * fetch(u, S) issues exactly PL LDS-DMA loads per wave that bring step
 //    u's row indices into the caller's index slot S (also for u >= nsteps,
 //    so that the vmcnt arithmetic is the same in every wave);
-//  * resolve(u, S, idx, wrow, kb) turns them into the lane's gathered rows
-//    idx[rt] (or -1), the weight row and the first input channel of step u.
+//  * resolve(u, S, st) turns them into step u's operands st (the lane's
+//    gathered rows idx[rt] (or -1), the weight row and the first input
+//    channel; OP = 2 also the second offset's).
 // Both are called with u = 0, 1, 2, ... in order (fetch NS steps ahead of
 // resolve).  Issue order: F(0..NS-1), then per step u: D(u) F(u+NS)
 // (D = the LPS LDS-DMA loads of a step, F = a fetch).  Before step s
@@ -381,7 +413,7 @@ __device__ __forceinline__ void compute(floatx4 (&acc)[2][C::BN / 16], const Rea
 // just read (each wave reads only its own slot).  Steps past nsteps (at most
 // NS-1) compute on all-zero stages, so the trip is uniform and the
 // accumulators stay in place.
-template <class C, bool ALIGNED, bool CAT, int PL, class Fetch, class Resolve>
+template <class C, bool ALIGNED, bool CAT, int PL, int OP = 1, class Fetch, class Resolve>
 __device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, Fetch fetch,
                                     Resolve resolve, const Operands &op, int n0, char *ring) {
   constexpr int MT = C::BM / 128, NS = C::NS;
@@ -390,23 +422,22 @@ __device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, F
   const __amdgpu_buffer_rsrc_t xr2 = make_rsrc(op.X2 ? op.X2 : op.X, op.X2 ? op.x2bytes : 0u);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
   const ReadBase<C::NKS> rb = read_base<C>(ring);
-  const IssueCtx<C> cx = issue_ctx<C>(ring, wave, n0, op);
+  const IssueCtx<C> cx = issue_ctx<C, OP>(ring, wave, n0, op);
   half8 areg[NS][MT][C::NKS];  // gathered rows per stage
   auto prepare = [&](int u, auto St) {
     StepIn st;
     st.wrow = 0;
+    st.wrow2 = 0;
     st.kb = 0;
     st.live = u < nsteps;
-    if (st.live) resolve(u, St, st.idx, st.wrow, st.kb);
-    else {
-      st.idx[0] = -1;
-      st.idx[1] = -1;
-    }
+    st.live2 = false;
+    st.idx[0] = st.idx[1] = st.idx2[0] = st.idx2[1] = -1;
+    if (st.live) resolve(u, St, st);
     return st;
   };
   auto put = [&](int u, auto St) {
     const StepIn st = prepare(u, St);
-    issue<C, ALIGNED, CAT, decltype(St)::value>(cx, st, op, xr, xr2, wr, areg[decltype(St)::value]);
+    issue<C, ALIGNED, CAT, decltype(St)::value, OP>(cx, st, op, xr, xr2, wr, areg[decltype(St)::value]);
   };
   unroll<NS>([&](auto I) { fetch(decltype(I)::value, I); });
   unroll<NS - 1>([&](auto I) {
@@ -427,8 +458,8 @@ __device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, F
       const StepIn nx = prepare(s + i + NS - 1, std::integral_constant<int, slot>{});
       SPIRA_STEP_STAMP(s + i, 3);
       compute<C, i>(acc, rb, areg[i], [&](auto KQ) {
-        issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value>(cx, nx, op, xr, xr2, wr, areg[slot]);
-        issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value + 1>(cx, nx, op, xr, xr2, wr, areg[slot]);
+        issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value, OP>(cx, nx, op, xr, xr2, wr, areg[slot]);
+        issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value + 1, OP>(cx, nx, op, xr, xr2, wr, areg[slot]);
       });
       fetch(s + i + 2 * NS - 1, std::integral_constant<int, slot>{});
     });
@@ -462,6 +493,33 @@ struct StepIter {
       j = first(lo, hi);
       drop();
     }
+  }
+};
+
+// Two offsets per step (offset packing, one channel chunk per offset): j
+// and j2 (-1 when the set has run out).
+struct PairIter {
+  uint64_t lo, hi;
+  int j, j2;
+  static constexpr int chunk = 0;
+  __device__ __forceinline__ void take(int &x) {
+    if (!(lo | hi)) {
+      x = -1;
+      return;
+    }
+    x = StepIter::first(lo, hi);
+    if (x < 64) lo &= ~(uint64_t(1) << x);
+    else hi &= ~(uint64_t(1) << (x - 64));
+  }
+  __device__ __forceinline__ void init(uint64_t l, uint64_t h) {
+    lo = l;
+    hi = h;
+    take(j);
+    take(j2);
+  }
+  __device__ __forceinline__ void step(int) {
+    take(j);
+    take(j2);
   }
 };
 
@@ -588,7 +646,7 @@ __device__ int64_t g_block_times[1 << 20];
 // logical row i is target order[i] and `map` holds the rows in logical order;
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
-template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT>
+template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
@@ -596,9 +654,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   using C = typename ring::TileOf<WN, NKS>::C;
   constexpr int MT = C::BM / 128, NS = C::NS;
   __shared__ __align__(1024) char ring_lds[C::LDS];
-  // map entries of a later step, per stage (untiled maps; the map tile's place)
+  // map entries of a later step, per stage and packed offset (untiled maps;
+  // the map tile's place)
   int32_t(*idx_lds)[256] = reinterpret_cast<int32_t(*)[256]>(ring_lds + C::RING);
-  static_assert(NS * 256 * 4 <= C::MAP_TILE, "index slots exceed the map tile");
+  static_assert(NS * OP * 256 * 4 <= C::MAP_TILE, "index slots exceed the map tile");
+  static_assert(OP == 1 || (OP == 2 && ALIGNED && !CAT && MODE == kStoreNative), "offset packing: plain stores");
   // output row per tile row (epilogue); 64 per wave so that during the
   // step loop a wave's dummy map fetches (tiled maps) can land here
   __shared__ int32_t orow_s[4][64];
@@ -630,7 +690,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   }
   const int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
   const int nch = (op.CinP + C::KC - 1) / C::KC;
-  const int nsteps = nact * nch;
+  // OP = 2: two offsets per step (one channel chunk each)
+  const int nsteps = OP == 2 ? (nact + 1) / 2 : nact * nch;
   SPIRA_STAMP(1);
 
   floatx4 acc[2][2 * WN];
@@ -657,7 +718,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(map, static_cast<uint32_t>(T * Kc * 4));
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + l16) * 4;
-  ring::StepIter fit, pit;  // fetch side (runs NS steps ahead) and issue side
+  using Iter = std::conditional_t<OP == 2, ring::PairIter, ring::StepIter>;
+  Iter fit, pit;  // fetch side (runs NS steps ahead) and issue side
   fit.init(ulo, uhi);
   pit = fit;
   int fu = 0;
@@ -685,9 +747,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const uint32_t tbase = ring::lds_addr(tile) + ((wave * 32 + l16) * KP + j0) * 4;
   auto fetch = [&](int u, auto St) {
     (void)u;
-    // (tiled: an out-of-range fetch that only keeps the vmcnt arithmetic)
-    const uint32_t off = (tiled || fbase == kOutOfRange || fu >= nsteps) ? kOutOfRange : fbase + fit.j * 4u;
-    ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value][uwave * 64]);
+    // (tiled: out-of-range fetches that only keep the vmcnt arithmetic)
+    const bool none = tiled || fbase == kOutOfRange || fu >= nsteps;
+    const uint32_t off = none ? kOutOfRange : fbase + fit.j * 4u;
+    ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP][uwave * 64]);
+    if constexpr (OP == 2) {
+      const uint32_t off2 = (none || fit.j2 < 0) ? kOutOfRange : fbase + fit.j2 * 4u;
+      ring::dma4(mr, off2, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP + 1][uwave * 64]);
+    }
     ++fu;
     fit.step(nch);
   };
@@ -695,22 +762,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   // after a step's are resolved, so their LDS latency hides behind the
   // following compute (whose B-read wait also covers them); only the
   // prologue's steps (no compute in between) wait for their own read.
-  int32_t pre[2];
+  int32_t pre[2], pre2[2];
   auto read_tile = [&]() {
-    const uint32_t col = static_cast<uint32_t>(pit.j) * 4u;
+    // (past the last offset (OP = 2: j = -1) column 0 is read, unused)
+    const uint32_t col = static_cast<uint32_t>(pit.j < 0 ? 0 : pit.j) * 4u;
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
       asm volatile("ds_read_b32 %0, %1" : "=v"(pre[rt]) : "v"(tbase + rt * 16 * KP * 4 + col) : "memory");
+    if constexpr (OP == 2) {
+      // (no second offset: column 0 is read and discarded when resolved)
+      const uint32_t col2 = static_cast<uint32_t>(pit.j2 < 0 ? 0 : pit.j2) * 4u;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        asm volatile("ds_read_b32 %0, %1" : "=v"(pre2[rt]) : "v"(tbase + rt * 16 * KP * 4 + col2) : "memory");
+    }
   };
   if (tiled) read_tile();
-  auto resolve = [&](int u, auto St, int32_t (&idx)[2], int &wrow, int &kb) {
+  auto resolve = [&](int u, auto St, ring::StepIn &st) {
+    int32_t(&idx)[2] = st.idx;
     if (tiled) {
       if (u < NS) ring::lds_wait();  // prologue puts: no compute since the read
       idx[0] = pre[0];
       idx[1] = pre[1];
+      if constexpr (OP == 2) {
+        st.idx2[0] = pre2[0];
+        st.idx2[1] = pre2[1];
+      }
     } else {
-      idx[0] = ring::rd4<decltype(St)::value * 1024>(ibase);
-      idx[1] = ring::rd4<decltype(St)::value * 1024 + 64>(ibase);
+      idx[0] = ring::rd4<decltype(St)::value * OP * 1024>(ibase);
+      idx[1] = ring::rd4<decltype(St)::value * OP * 1024 + 64>(ibase);
+      if constexpr (OP == 2) {
+        st.idx2[0] = ring::rd4<(decltype(St)::value * OP + 1) * 1024>(ibase);
+        st.idx2[1] = ring::rd4<(decltype(St)::value * OP + 1) * 1024 + 64>(ibase);
+      }
       ring::lds_wait();
     }
 #pragma unroll
@@ -718,13 +802,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
       ring::pin(idx[rt]);
       if (ident) idx[rt] = static_cast<int32_t>(row0 + wave * 32 + rt * 16 + l16);
       if (!mvalid[rt]) idx[rt] = -1;
+      if constexpr (OP == 2) {
+        ring::pin(st.idx2[rt]);
+        if (!mvalid[rt]) st.idx2[rt] = -1;
+      }
     }
-    wrow = j0 + pit.j;
-    kb = pit.chunk * C::KC;
+    st.wrow = j0 + pit.j;
+    st.kb = pit.chunk * C::KC;
+    if constexpr (OP == 2) {
+      st.live2 = pit.j2 >= 0;
+      st.wrow2 = j0 + (pit.j2 < 0 ? 0 : pit.j2);
+    }
     pit.step(nch);
     if (tiled) read_tile();
   };
-  ring::run<C, ALIGNED, CAT, 1>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   SPIRA_STAMP(2);
 #ifdef SPIRA_BLOCK_TIMING
   if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = nact;
@@ -809,11 +901,11 @@ __global__ __launch_bounds__(256, 2) void ws_kernel(const int32_t *__restrict__ 
   floatx4 acc[2][2 * WN];
   zero_acc<WN>(acc);
   auto fetch = [](int, auto) {};
-  auto resolve = [&](int u, auto, int32_t (&idx)[2], int &wrow, int &kb) {
-    idx[0] = src[0];
-    idx[1] = src[1];
-    wrow = wrow0;
-    kb = u * C::KC;
+  auto resolve = [&](int u, auto, ring::StepIn &st) {
+    st.idx[0] = src[0];
+    st.idx[1] = src[1];
+    st.wrow = wrow0;
+    st.kb = u * C::KC;
   };
   const int nch = (op.CinP + C::KC - 1) / C::KC;
   ring::run<C, ALIGNED, false, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
@@ -854,11 +946,11 @@ __global__ __launch_bounds__(256, 2) void gg_kernel(const GroupTable gt, Operand
   floatx4 acc[2][2 * WN];
   zero_acc<WN>(acc);
   auto fetch = [](int, auto) {};
-  auto resolve = [&](int u, auto, int32_t (&idx)[2], int &wrow, int &kb) {
-    idx[0] = src[0];
-    idx[1] = src[1];
-    wrow = g;
-    kb = u * C::KC;
+  auto resolve = [&](int u, auto, ring::StepIn &st) {
+    st.idx[0] = src[0];
+    st.idx[1] = src[1];
+    st.wrow = g;
+    st.kb = u * C::KC;
   };
   const int nch = (op.CinP + C::KC - 1) / C::KC;
   ring::run<C, ALIGNED, false, 0>(acc, nch, fetch, resolve, op, n0, ring_lds);
@@ -1131,12 +1223,12 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
     default: CALL(4); break;      \
   }
 
-template <int MODE, bool AL, int NKS, bool CAT = false>
+template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                       void *Y, const Epilogue &epi) {
-#define SPIRA_OS_CALL(W)                                                                                         \
-  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
+#define SPIRA_OS_CALL(W)                                                                                             \
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
                      jper, op, Y, epi)
   SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
 #undef SPIRA_OS_CALL
@@ -1169,6 +1261,16 @@ static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, 
                           void *Y, const Epilogue &epi) {
   const int nks = os_nks(op.CinP, wn, static_cast<int64_t>(grid.x) * grid.y * grid.z, device_cu_count());
   const bool cat = op.X2 != nullptr;
+  // offset packing: 16- and 32-channel inputs run two offsets per step
+  // (KC = 2 CinP) instead of a half-empty or one-block step per offset
+  static const bool pack = env_int("SPIRA_OS_PACK", 1) != 0;
+  if constexpr (MODE == kStoreNative) {
+    if (pack && map && !cat && op.Cin % 8 == 0 && (op.CinP == 16 || op.CinP == 32) && jper >= Kc) {
+      if (op.CinP == 16) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      else launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      return;
+    }
+  }
   if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
   else if (cat) {
     // channel concatenations: storage-dtype outputs (split or not)

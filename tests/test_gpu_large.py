@@ -117,3 +117,29 @@ def test_row_order_k5(dev):
     m = orc.build_kmap(k, k, (5, 5, 5), (1, 1, 1), 0)[2]
     order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(m).to(dev), T))
     _check_row_order(m, T, order, masks, omap)
+
+
+@pytest.fixture(scope="module")
+def scene_k5():
+    c = scenes.spheres_planes(n=60000, grid=96, seed=9)
+    k, _ = orc.flatten_sort(c, True)
+    return k, orc.build_kmap(k, k, (5, 5, 5), (1, 1, 1), 0)[2]
+
+
+@pytest.mark.parametrize("ks,cin,cout", [(3, 16, 32), (3, 24, 40), (3, 32, 64), (3, 8, 16),
+                                         (5, 16, 16), (5, 32, 32), (5, 24, 96)])
+def test_offset_packing(dev, indoor, scene_k5, ks, cin, cout):
+    """16- and 32-channel (padded) inputs run two kernel offsets per step;
+    an odd offset count leaves the last step half empty, and rows without a
+    neighbour at one of the pair's offsets must read zeros there.  k = 3 on
+    the 200k scene (row-ordered, map tile in LDS), k = 5 (125 offsets, map
+    entries fetched per step)."""
+    k, m = indoor if ks == 3 else scene_k5
+    S = T = len(k)
+    X = _case(S, cin, cout, dev, seed=ks * 100 + cin)[0]
+    g = torch.Generator().manual_seed(cin + cout)
+    W = (torch.randn(m.shape[1], cin, cout, generator=g) / np.sqrt(m.shape[1] * cin)).half()
+    md = torch.from_numpy(m).to(dev)
+    y = np_(F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev)).float())
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(y, ref) <= 1e-2
