@@ -99,12 +99,31 @@ def _check_row_order(m, T, order, masks, omap):
     for g in range(G):
         c = cnt[g * 128:(g + 1) * 128]
         assert np.all(np.diff(c) <= 0)
+    if K <= 57:
+        # each group is one run of 128 rows of the stable ascending sort of
+        # the row keys ((K - count) << K | column mask), in that order
+        keys = ((K - valid.sum(1)).astype(np.uint64) << np.uint64(K)) | (
+            valid.astype(np.uint64) << np.arange(K, dtype=np.uint64)).sum(1, dtype=np.uint64)
+        srt = np.argsort(keys, kind="stable")
+        runs = {int(srt[i]): srt[i:i + 128] for i in range(0, T, 128)}
+        for g in range(G):
+            grp = order[g * 128:(g + 1) * 128]
+            assert np.array_equal(grp, runs[int(grp[0])])
 
 
 def test_row_order_k3(dev, indoor):
     from spira_amd.nn.functional._native import _C
     k, m = indoor
     T = len(k)
+    order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(m).to(dev), T))
+    _check_row_order(m, T, order, masks, omap)
+
+
+@pytest.mark.parametrize("T", [1, 130, 2048, 3001])
+def test_row_order_small(dev, indoor, T):
+    """Sort tiles of 2048 rows: one partial tile, exactly one, and a partial second."""
+    from spira_amd.nn.functional._native import _C
+    m = np.ascontiguousarray(indoor[1][:T])
     order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(m).to(dev), T))
     _check_row_order(m, T, order, masks, omap)
 
