@@ -108,6 +108,7 @@ namespace ring {
 // bandwidth.  A step covers KC = 16 * NKS input channels of one kernel
 // offset: NKS = 2, 4 or 8 (32, 64 or 128 channels: fewer steps and so less
 // per-step synchronisation for wide layers).
+constexpr int kMapTileK = 27;  // map columns held in LDS (kernels of <= 27 offsets)
 template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int NS = NS_;  // ring depth: NS - 1 steps load while one computes
   static constexpr int NKS = NKS_;
@@ -121,7 +122,7 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
   static constexpr int STAGE = B_BYTES;
   static constexpr int RING = NS * STAGE;
   static constexpr int OUT_STAGE = BM * (BN + 8) * 2;  // fp16 output tile staged by the epilogue
-  static constexpr int MAP_TILE_K = 27;                 // map columns held in LDS (kernels of <= 27 offsets)
+  static constexpr int MAP_TILE_K = kMapTileK;
   static constexpr int MAP_TILE = BM * MAP_TILE_K * 4;  // the block's map rows, after the ring
   static constexpr int LDS = RING + MAP_TILE > OUT_STAGE ? RING + MAP_TILE : OUT_STAGE;
   static constexpr int LPS = MT * NKS + BVEC;  // vector-memory loads per wave and step
@@ -216,12 +217,12 @@ template <class C> __device__ __forceinline__ ReadBase<C::NKS> read_base(const c
 // by instruction issue, not by the memory system).
 template <class C> struct IssueCtx {
   uint32_t wlane[C::BVEC];  // byte offset of the lane's weight chunk in an (offset, kb = 0) block, or kOutOfRange
-  int c8[C::BVEC];          // first input channel of that chunk (OP = 2: 0 / 1, the step's offset it belongs to)
+  int c8[C::BVEC];          // first input channel of that chunk (OP > 1: the step's offset part it belongs to)
   uint32_t ldsw;            // LDS address of the wave's DMA slot in stage 0 (wave-uniform)
   uint32_t kh16;            // byte offset of the lane's quarter of a 32-channel block
   int kh8;                  // its first channel
 };
-// OP = 2 (two kernel offsets per step, KC = 2 CinP): channel c of a step is
+// OP > 1 (OP kernel offsets per step, KC = OP CinP): channel c of a step is
 // channel c % CinP of the step's offset c / CinP.
 template <class C, int OP = 1>
 __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int n0, const Operands &op) {
@@ -232,11 +233,11 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
     const int v = i * 256 + tid;
     const int n = v / C::CPR;
     const int c8 = ((v % C::CPR) ^ C::swz(n)) * 8;
-    const int part = OP == 2 ? c8 / op.CinP : 0;
+    const int part = OP > 1 ? c8 / op.CinP : 0;
     const int ch = c8 - part * op.CinP;
     cx.wlane[i] = (n < C::BN && n0 + n < op.CoutP) ? static_cast<uint32_t>(((n0 + n) * op.CinP + ch) * 2)
                                                      : kOutOfRange;
-    cx.c8[i] = OP == 2 ? part : c8;
+    cx.c8[i] = OP > 1 ? part : c8;
   }
   cx.ldsw = __builtin_amdgcn_readfirstlane(lds_addr(ring) + wave * 64 * 16);
   cx.kh8 = ((threadIdx.x & 63) >> 4) * 8;
@@ -249,12 +250,22 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
 // weight row wrow, first input channel kb; !live: a step past the end (every
 // load out of range, so that each wave issues the same number of loads in
 // every step).
-// OP = 2: idx2 / wrow2 / live2 describe the step's second offset.
+// OP > 1 (offset packing): idxp / wrowp / livep[p - 1] describe the step's
+// offset p = 1 .. OP - 1.
 struct StepIn {
-  bool live, live2;
-  int32_t idx[2], idx2[2];
-  int wrow, wrow2, kb;
+  bool live;
+  int32_t idx[2];
+  int wrow, kb;
+  bool livep[3];
+  int32_t idxp[3][2];
+  int wrowp[3];
 };
+
+// The value of offset part p of a packed step (OP = 2 or 4).
+template <int OP, class T> __device__ __forceinline__ T part_sel(int p, T v0, T v1, T v2, T v3) {
+  if constexpr (OP == 2) return p ? v1 : v0;
+  else return p < 2 ? (p ? v1 : v0) : (p == 2 ? v2 : v3);
+}
 
 // Issue the loads of slice KS of a step into ring stage S: the A fragment
 // of row tile rt = KS % 2 and 32-channel block kq = KS / 2 (lane l: its row
@@ -266,31 +277,37 @@ struct StepIn {
 // wholly in one part, C1 % 32 == 0).  The offsets use 32-bit arithmetic:
 // every operand is below 2 GiB.
 //
-// OP = 2 (offset packing for 16- and 32-channel inputs, KC = 2 CinP): the
-// step's channels [0, CinP) belong to offset 1 (idx, wrow), [CinP, 2 CinP)
-// to offset 2 (idx2, wrow2); the lane picks its row and weight row by the
-// part its channels fall in.
+// OP = 2 or 4 (offset packing for 16- and 32-channel inputs, KC = OP CinP,
+// one channel chunk per offset): channels [p CinP, (p + 1) CinP) of the step
+// belong to its offset p; the lane picks its row and each weight DMA its
+// weight row by the part its channels fall in.
 template <class C, bool ALIGNED, bool CAT, int S, int KS, int OP = 1>
 __device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
                                             __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
                                             __amdgpu_buffer_rsrc_t wr, half8 (&a)[1][C::NKS]) {
   constexpr int rt = KS & 1;
   const int k0 = st.kb + (KS >> 1) * 32;
-  if constexpr (OP == 2) {
+  if constexpr (OP > 1) {
     static_assert(ALIGNED && !CAT, "offset packing: aligned rows of one source");
-    const int k = k0 + cx.kh8;  // the lane's channel within the step
-    const bool part = k >= op.CinP;
-    const int ch = part ? k - op.CinP : k;
-    const int32_t ix = part ? st.idx2[rt] : st.idx[rt];
-    const bool ok = (part ? st.live2 : st.live) & (ix >= 0) & (ch < op.Cin);
+    constexpr int CP = C::KC / OP;          // channels per offset (16 or 32)
+    const int k = (KS >> 1) * 32 + cx.kh8;  // the lane's channel within the step
+    const int part = k / CP;
+    const int ch = k - part * CP;
+    const int32_t ix = part_sel<OP>(part, st.idx[rt], st.idxp[0][rt], st.idxp[1][rt], st.idxp[2][rt]);
+    const bool lv = part_sel<OP>(part, st.live, st.livep[0], st.livep[1], st.livep[2]);
+    const bool ok = lv & (ix >= 0) & (ch < op.Cin);
     const uint32_t at = static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.Cin * 2) + static_cast<uint32_t>(ch * 2);
     a[0][KS] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? at : kOutOfRange, 0, 0));
-    const uint32_t ws1 = static_cast<uint32_t>(st.wrow * op.CoutP * op.CinP * 2);
-    const uint32_t ws2 = static_cast<uint32_t>(st.wrow2 * op.CoutP * op.CinP * 2);
+    const uint32_t wb = static_cast<uint32_t>(op.CoutP * op.CinP * 2);
+    // (a part past the step's last offset: out of range)
+    const uint32_t w0 = st.live ? static_cast<uint32_t>(st.wrow) * wb : kOutOfRange;
+    uint32_t wp[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) wp[q] = st.livep[q] ? static_cast<uint32_t>(st.wrowp[q]) * wb : kOutOfRange;
 #pragma unroll
     for (int i = KS; i < C::BVEC; i += C::NKS) {
-      const bool p2 = cx.c8[i] != 0;
-      const uint32_t off = (p2 ? st.live2 : st.live) ? cx.wlane[i] + (p2 ? ws2 : ws1) : kOutOfRange;
+      const uint32_t ws = part_sel<OP>(cx.c8[i], w0, wp[0], wp[1], wp[2]);
+      const uint32_t off = (ws == kOutOfRange || cx.wlane[i] == kOutOfRange) ? kOutOfRange : cx.wlane[i] + ws;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void_t *)(cx.ldsw + S * C::STAGE + i * 4096), 16, off, 0, 0,
                                                0);
     }
@@ -427,11 +444,15 @@ __device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, F
   auto prepare = [&](int u, auto St) {
     StepIn st;
     st.wrow = 0;
-    st.wrow2 = 0;
     st.kb = 0;
     st.live = u < nsteps;
-    st.live2 = false;
-    st.idx[0] = st.idx[1] = st.idx2[0] = st.idx2[1] = -1;
+    st.idx[0] = st.idx[1] = -1;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      st.livep[q] = false;
+      st.wrowp[q] = 0;
+      st.idxp[q][0] = st.idxp[q][1] = -1;
+    }
     if (st.live) resolve(u, St, st);
     return st;
   };
@@ -496,11 +517,11 @@ struct StepIter {
   }
 };
 
-// Two offsets per step (offset packing, one channel chunk per offset): j
-// and j2 (-1 when the set has run out).
-struct PairIter {
+// OP offsets per step (offset packing, one channel chunk per offset): j,
+// jp[0 .. OP - 2] (-1 when the set has run out).
+template <int OP> struct GroupIter {
   uint64_t lo, hi;
-  int j, j2;
+  int j, jp[OP - 1];
   static constexpr int chunk = 0;
   __device__ __forceinline__ void take(int &x) {
     if (!(lo | hi)) {
@@ -511,15 +532,15 @@ struct PairIter {
     if (x < 64) lo &= ~(uint64_t(1) << x);
     else hi &= ~(uint64_t(1) << (x - 64));
   }
+  __device__ __forceinline__ void step(int) {
+    take(j);
+#pragma unroll
+    for (int q = 0; q < OP - 1; ++q) take(jp[q]);
+  }
   __device__ __forceinline__ void init(uint64_t l, uint64_t h) {
     lo = l;
     hi = h;
-    take(j);
-    take(j2);
-  }
-  __device__ __forceinline__ void step(int) {
-    take(j);
-    take(j2);
+    step(1);
   }
 };
 
@@ -658,7 +679,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   // the map tile's place)
   int32_t(*idx_lds)[256] = reinterpret_cast<int32_t(*)[256]>(ring_lds + C::RING);
   static_assert(NS * OP * 256 * 4 <= C::MAP_TILE, "index slots exceed the map tile");
-  static_assert(OP == 1 || (OP == 2 && ALIGNED && !CAT && MODE == kStoreNative), "offset packing: plain stores");
+  static_assert(OP == 1 || ((OP == 2 || OP == 4) && ALIGNED && !CAT && MODE == kStoreNative),
+                "offset packing: plain stores");
   // output row per tile row (epilogue); 64 per wave so that during the
   // step loop a wave's dummy map fetches (tiled maps) can land here
   __shared__ int32_t orow_s[4][64];
@@ -690,8 +712,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   }
   const int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
   const int nch = (op.CinP + C::KC - 1) / C::KC;
-  // OP = 2: two offsets per step (one channel chunk each)
-  const int nsteps = OP == 2 ? (nact + 1) / 2 : nact * nch;
+  // OP > 1: OP offsets per step (one channel chunk each)
+  const int nsteps = OP > 1 ? (nact + OP - 1) / OP : nact * nch;
   SPIRA_STAMP(1);
 
   floatx4 acc[2][2 * WN];
@@ -718,7 +740,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(map, static_cast<uint32_t>(T * Kc * 4));
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t ibase = ring::lds_addr(&idx_lds[0][0]) + (wave * 64 + l16) * 4;
-  using Iter = std::conditional_t<OP == 2, ring::PairIter, ring::StepIter>;
+  using Iter = std::conditional_t<(OP > 1), ring::GroupIter<(OP > 1 ? OP : 2)>, ring::StepIter>;
   Iter fit, pit;  // fetch side (runs NS steps ahead) and issue side
   fit.init(ulo, uhi);
   pit = fit;
@@ -751,9 +773,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     const bool none = tiled || fbase == kOutOfRange || fu >= nsteps;
     const uint32_t off = none ? kOutOfRange : fbase + fit.j * 4u;
     ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP][uwave * 64]);
-    if constexpr (OP == 2) {
-      const uint32_t off2 = (none || fit.j2 < 0) ? kOutOfRange : fbase + fit.j2 * 4u;
-      ring::dma4(mr, off2, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP + 1][uwave * 64]);
+    if constexpr (OP > 1) {
+#pragma unroll
+      for (int q = 0; q < OP - 1; ++q) {
+        const uint32_t offq = (none || fit.jp[q] < 0) ? kOutOfRange : fbase + fit.jp[q] * 4u;
+        ring::dma4(mr, offq, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP + 1 + q][uwave * 64]);
+      }
     }
     ++fu;
     fit.step(nch);
@@ -762,19 +787,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   // after a step's are resolved, so their LDS latency hides behind the
   // following compute (whose B-read wait also covers them); only the
   // prologue's steps (no compute in between) wait for their own read.
-  int32_t pre[2], pre2[2];
+  int32_t pre[2], prep[3][2];
   auto read_tile = [&]() {
     // (past the last offset (OP = 2: j = -1) column 0 is read, unused)
     const uint32_t col = static_cast<uint32_t>(pit.j < 0 ? 0 : pit.j) * 4u;
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
       asm volatile("ds_read_b32 %0, %1" : "=v"(pre[rt]) : "v"(tbase + rt * 16 * KP * 4 + col) : "memory");
-    if constexpr (OP == 2) {
-      // (no second offset: column 0 is read and discarded when resolved)
-      const uint32_t col2 = static_cast<uint32_t>(pit.j2 < 0 ? 0 : pit.j2) * 4u;
+    if constexpr (OP > 1) {
+      // (a part past the last offset: column 0 is read and discarded when resolved)
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        asm volatile("ds_read_b32 %0, %1" : "=v"(pre2[rt]) : "v"(tbase + rt * 16 * KP * 4 + col2) : "memory");
+      for (int q = 0; q < OP - 1; ++q) {
+        const uint32_t colq = static_cast<uint32_t>(pit.jp[q] < 0 ? 0 : pit.jp[q]) * 4u;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          asm volatile("ds_read_b32 %0, %1" : "=v"(prep[q][rt]) : "v"(tbase + rt * 16 * KP * 4 + colq) : "memory");
+      }
     }
   };
   if (tiled) read_tile();
@@ -784,16 +812,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
       if (u < NS) ring::lds_wait();  // prologue puts: no compute since the read
       idx[0] = pre[0];
       idx[1] = pre[1];
-      if constexpr (OP == 2) {
-        st.idx2[0] = pre2[0];
-        st.idx2[1] = pre2[1];
+      if constexpr (OP > 1) {
+#pragma unroll
+        for (int q = 0; q < OP - 1; ++q) {
+          st.idxp[q][0] = prep[q][0];
+          st.idxp[q][1] = prep[q][1];
+        }
       }
     } else {
       idx[0] = ring::rd4<decltype(St)::value * OP * 1024>(ibase);
       idx[1] = ring::rd4<decltype(St)::value * OP * 1024 + 64>(ibase);
-      if constexpr (OP == 2) {
-        st.idx2[0] = ring::rd4<(decltype(St)::value * OP + 1) * 1024>(ibase);
-        st.idx2[1] = ring::rd4<(decltype(St)::value * OP + 1) * 1024 + 64>(ibase);
+      if constexpr (OP > 1) {
+        ring::unroll<OP - 1>([&](auto Q) {
+          constexpr int q = decltype(Q)::value;
+          st.idxp[q][0] = ring::rd4<(decltype(St)::value * OP + 1 + q) * 1024>(ibase);
+          st.idxp[q][1] = ring::rd4<(decltype(St)::value * OP + 1 + q) * 1024 + 64>(ibase);
+        });
       }
       ring::lds_wait();
     }
@@ -802,16 +836,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
       ring::pin(idx[rt]);
       if (ident) idx[rt] = static_cast<int32_t>(row0 + wave * 32 + rt * 16 + l16);
       if (!mvalid[rt]) idx[rt] = -1;
-      if constexpr (OP == 2) {
-        ring::pin(st.idx2[rt]);
-        if (!mvalid[rt]) st.idx2[rt] = -1;
+      if constexpr (OP > 1) {
+#pragma unroll
+        for (int q = 0; q < OP - 1; ++q) {
+          ring::pin(st.idxp[q][rt]);
+          if (!mvalid[rt]) st.idxp[q][rt] = -1;
+        }
       }
     }
     st.wrow = j0 + pit.j;
     st.kb = pit.chunk * C::KC;
-    if constexpr (OP == 2) {
-      st.live2 = pit.j2 >= 0;
-      st.wrow2 = j0 + (pit.j2 < 0 ? 0 : pit.j2);
+    if constexpr (OP > 1) {
+#pragma unroll
+      for (int q = 0; q < OP - 1; ++q) {
+        st.livep[q] = pit.jp[q] >= 0;
+        st.wrowp[q] = j0 + (pit.jp[q] < 0 ? 0 : pit.jp[q]);
+      }
     }
     pit.step(nch);
     if (tiled) read_tile();
@@ -1261,13 +1301,25 @@ static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, 
                           void *Y, const Epilogue &epi) {
   const int nks = os_nks(op.CinP, wn, static_cast<int64_t>(grid.x) * grid.y * grid.z, device_cu_count());
   const bool cat = op.X2 != nullptr;
-  // offset packing: 16- and 32-channel inputs run two offsets per step
-  // (KC = 2 CinP) instead of a half-empty or one-block step per offset
-  static const bool pack = env_int("SPIRA_OS_PACK", 1) != 0;
+  // offset packing: 16- and 32-channel inputs of kernels with more than 27
+  // offsets (map entries fetched per step) run four offsets per step (64-
+  // or 128-channel steps) instead of a step per offset.  (Measured, kernel
+  // only, 300k voxels, 125 offsets: 16 -> 16 262 -> 182 us, 32 -> 32 273 ->
+  // 213 us, 32 -> 64 299 -> 256 us; with 27 offsets (map tile in LDS) it was
+  // slower: 17.5 -> 18.3-20.9 us at 200k voxels.)  SPIRA_OS_PACK=0 switches
+  // it off, =2 packs pairs of offsets (measurements).
+  static const int pack = env_int("SPIRA_OS_PACK", 4);
   if constexpr (MODE == kStoreNative) {
-    if (pack && map && !cat && op.Cin % 8 == 0 && (op.CinP == 16 || op.CinP == 32) && jper >= Kc) {
-      if (op.CinP == 16) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      else launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+    if (pack && map && !cat && op.Cin % 8 == 0 && (op.CinP == 16 || op.CinP == 32) && jper >= Kc &&
+        Kc > ring::kMapTileK) {
+      if (pack == 2) {
+        if (op.CinP == 16) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+        else launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      } else if (op.CinP == 16) {
+        launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      } else {
+        launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      }
       return;
     }
   }

@@ -148,11 +148,11 @@ def scene_k5():
 @pytest.mark.parametrize("ks,cin,cout", [(3, 16, 32), (3, 24, 40), (3, 32, 64), (3, 8, 16),
                                          (5, 16, 16), (5, 32, 32), (5, 24, 96)])
 def test_offset_packing(dev, indoor, scene_k5, ks, cin, cout):
-    """16- and 32-channel (padded) inputs run two kernel offsets per step;
-    an odd offset count leaves the last step half empty, and rows without a
-    neighbour at one of the pair's offsets must read zeros there.  k = 3 on
-    the 200k scene (row-ordered, map tile in LDS), k = 5 (125 offsets, map
-    entries fetched per step)."""
+    """16- and 32-channel (padded) inputs of kernels with more than 27
+    offsets run four kernel offsets per step: 125 offsets leave the last step
+    with one, and rows without a neighbour at one of a step's offsets must
+    read zeros there.  k = 3 on the 200k scene (map tile in LDS, one offset
+    per step) for comparison."""
     k, m = indoor if ks == 3 else scene_k5
     S = T = len(k)
     X = _case(S, cin, cout, dev, seed=ks * 100 + cin)[0]
@@ -162,3 +162,46 @@ def test_offset_packing(dev, indoor, scene_k5, ks, cin, cout):
     y = np_(F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev)).float())
     ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
     assert rel_err(y, ref) <= 1e-2
+
+
+_PACK_CHILD = """
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, "tests")
+from oracle import oracle as orc
+from spira_amd import scenes
+from spira_amd.nn import functional as F
+from helpers import rel_err
+c = scenes.spheres_planes(n=60000, grid=96, seed=9)
+k, _ = orc.flatten_sort(c, True)
+T = len(k)
+g = torch.Generator().manual_seed(1)
+worst = 0.0
+for ks in (3, 5):
+    m = orc.build_kmap(k, k, (ks, ks, ks), (1, 1, 1), 0)[2]
+    K = m.shape[1]
+    for cin, cout in [(16, 32), (32, 32), (24, 64)]:
+        X = torch.randn(T, cin, generator=g).half()
+        W = (torch.randn(K, cin, cout, generator=g) / np.sqrt(K * cin)).half()
+        y = F.sparse_convolution_forward_os(T, T, torch.from_numpy(m).cuda(), X.cuda(), W.cuda())
+        ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+        worst = max(worst, rel_err(y.float().cpu().numpy(), ref))
+print("WORST", worst)
+"""
+
+
+@pytest.mark.parametrize("pack", ["2", "0"])
+def test_offset_packing_variants(dev, pack):
+    """Pairs of offsets per step (SPIRA_OS_PACK=2) and no packing (=0), k = 3
+    and 5, each in a child process since the library reads SPIRA_OS_PACK
+    once."""
+    import os
+    import subprocess
+    import sys
+    env = dict(os.environ, SPIRA_OS_PACK=pack)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _PACK_CHILD], env=env, cwd=root, capture_output=True, text=True,
+                       timeout=150)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert float(r.stdout.split("WORST")[-1]) <= 1e-2
