@@ -1322,6 +1322,16 @@ static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, 
       }
       return;
     }
+    // 64-channel inputs: two offsets per 128-channel step when the column
+    // tile is at most 64 wide (300k voxels, 125 offsets: 64 -> 64 420 ->
+    // 390 us; 64 -> 128 594 -> 601 us, so wider tiles keep one offset per
+    // step).  SPIRA_OS_PACK64=0 switches it off (measurements).
+    static const int pack64 = env_int("SPIRA_OS_PACK64", 1);
+    if (pack && pack64 && map && !cat && op.Cin % 8 == 0 && op.CinP == 64 && jper >= Kc && Kc > ring::kMapTileK &&
+        wn <= 2) {
+      launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      return;
+    }
   }
   if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
   else if (cat) {

@@ -146,7 +146,7 @@ def scene_k5():
 
 
 @pytest.mark.parametrize("ks,cin,cout", [(3, 16, 32), (3, 24, 40), (3, 32, 64), (3, 8, 16),
-                                         (5, 16, 16), (5, 32, 32), (5, 24, 96)])
+                                         (5, 16, 16), (5, 32, 32), (5, 24, 96), (5, 64, 64), (5, 56, 32)])
 def test_offset_packing(dev, indoor, scene_k5, ks, cin, cout):
     """16- and 32-channel (padded) inputs of kernels with more than 27
     offsets run four kernel offsets per step: 125 offsets leave the last step
@@ -181,7 +181,7 @@ worst = 0.0
 for ks in (3, 5):
     m = orc.build_kmap(k, k, (ks, ks, ks), (1, 1, 1), 0)[2]
     K = m.shape[1]
-    for cin, cout in [(16, 32), (32, 32), (24, 64)]:
+    for cin, cout in [(16, 32), (32, 32), (24, 64), (64, 64)]:
         X = torch.randn(T, cin, generator=g).half()
         W = (torch.randn(K, cin, cout, generator=g) / np.sqrt(K * cin)).half()
         y = F.sparse_convolution_forward_os(T, T, torch.from_numpy(m).cuda(), X.cuda(), W.cuda())
