@@ -37,12 +37,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the dominant kernel (os_kernel<3,0,true,8,false>, 200k
+# HBM bytes per launch of the dominant kernel (os_kernel<3,0,true,8,false,1>, 200k
 # voxels, 96 -> 96): rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE over
 # `bench.py --no-cpu --only layer,calib`, each scaled by what the counter
 # reads for the calibration leg's 256 MiB copy (FETCH_SIZE x 2.000,
-# WRITE_SIZE x 1.000): 68075 KiB fetched, 37579 KiB written.
-DOMINANT_TRAFFIC_BYTES = 68075 * 1024 * 2.0 + 37579 * 1024 * 1.0
+# WRITE_SIZE x 1.000): 68049 KiB fetched, 37578 KiB written.
+DOMINANT_TRAFFIC_BYTES = 68049 * 1024 * 2.0 + 37578 * 1024 * 1.0
 
 
 def parse():
@@ -283,7 +283,7 @@ def main():
                            "algorithmic_bytes": dm["bytes"],
                            "traffic": DOMINANT_TRAFFIC_BYTES,
                            "traffic_gbs": DOMINANT_TRAFFIC_BYTES / (dm["ms"] * 1e-3) / 1e9,
-                           "kernel": "os_kernel<3,0,true,8,false> (config 4 full resolution, 200k voxels, k=3, 96->96, "
+                           "kernel": "os_kernel<3,0,true,8,false,1> (config 4 full resolution, 200k voxels, k=3, 96->96, "
                                      "fp16, 128-channel steps)",
                            "ms": dm["ms"], "algorithmic_flops": dm["flops"], "valid_pairs": dm["pairs"]}
     if "calib" in legs:
