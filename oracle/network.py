@@ -23,19 +23,32 @@ from . import oracle as orc
 Stride = Tuple[int, int, int]
 
 
-def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray) -> List[Tuple[np.ndarray, Stride]]:
+def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray,
+                    dataflow: int = 0) -> List[Tuple[np.ndarray, Stride]]:
     """Outputs of ``model`` (SparseResUNet42-style: ``stem`` / ``encoders`` /
     ``decoders``; or a SparseResNet-style ModuleList of stages) as
     (features in sorted-key order, tensor stride) pairs, like the GPU
-    forward's SparseTensors after ``order()``."""
+    forward's SparseTensors after ``order()``.
+
+    ``dataflow`` is the map dataflow every layer runs on, with that
+    dataflow's semantics: 0 -- the output-stationary map and z-major weight
+    rows (convert_weights.py:19-28); 1 -- the compacted pair lists with the
+    mirrored half map of submanifold layers (weight_stat.cuh semantics,
+    sparse_convolution.cu:1267-1295); 2 -- the gather / scatter masks with
+    their half map (sparse_convolution.cu:1002-1124).  Dataflows 1 and 2 use
+    canonical weight rows.  The half maps differ from the full map where the
+    reference's z walk wraps (voxels at x = y = 0), so each dataflow is
+    evaluated with its own maps."""
     import torch
     from spira_amd import nn as spnn
     from spira_amd.networks import SparseResBlock
 
+    if dataflow not in (0, 1, 2):
+        raise ValueError(f"dataflow must be 0, 1 or 2, not {dataflow}")
     keys, perm = orc.flatten_sort(coords_np, True)
     x = np.ascontiguousarray(feats_np[perm], dtype=np.float32)
     vox: Dict[Stride, np.ndarray] = {(1, 1, 1): keys}
-    maps: Dict[tuple, np.ndarray] = {}
+    maps: Dict[tuple, tuple] = {}
 
     def coords_of(stride):
         if stride not in vox:
@@ -49,15 +62,22 @@ def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray) -> List[
         if layer.transposed:
             out_stride = tuple(a // b for a, b in zip(stride, layer.stride))
             key = (out_stride, stride, layer.kernel_size)
-            if key not in maps:
-                maps[key] = orc.search(coords_of(out_stride), coords_of(stride), layer.kernel_size, out_stride, orc.OS)
-            tmap = orc.convert_transposed_os(maps[key], len(coords_of(out_stride)))
-            return orc.conv_os_f32(tmap, len(coords_of(out_stride)), feats, W), out_stride
-        out_stride = tuple(a * b for a, b in zip(stride, layer.stride))
-        key = (stride, out_stride, layer.kernel_size)
+        else:
+            out_stride = tuple(a * b for a, b in zip(stride, layer.stride))
+            key = (stride, out_stride, layer.kernel_size)
         if key not in maps:
-            maps[key] = orc.search(coords_of(stride), coords_of(out_stride), layer.kernel_size, stride, orc.OS)
-        return orc.conv_os_f32(maps[key], len(coords_of(out_stride)), feats, W), out_stride
+            maps[key] = orc.build_kmap(coords_of(key[0]), coords_of(key[1]), layer.kernel_size, key[0], dataflow)
+        m = maps[key]
+        S, T = (m[1], m[0]) if layer.transposed else (m[0], m[1])
+        if dataflow == 0:
+            omap = orc.convert_transposed_os(m[2], m[0]) if layer.transposed else m[2]
+            return orc.conv_os_f32(omap, T, feats, W), out_stride
+        if dataflow == 1:
+            y = orc.conv_ws_merged(S, T, feats, W, m[5], m[3], transpose=layer.transposed)
+        else:
+            sm, tm = (m[4], m[3]) if layer.transposed else (m[3], m[4])
+            y = orc.conv_ws_gs(S, T, feats, W, sm, tm)
+        return y.astype(np.float32), out_stride
 
     def run(mod, feats, stride):
         if isinstance(mod, spnn.SparseConv):

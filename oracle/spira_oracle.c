@@ -310,16 +310,39 @@ void orc_conv_os(const int32_t *map, int64_t T, int Kc, const double *X, int Cin
  * Y is accumulated into (not cleared).  Serial over pairs, so exact order. */
 void orc_conv_pairs(int64_t P, const int32_t *in_idx, const int32_t *out_idx, const int32_t *widx,
                     const double *X, int Cin, const double *W, int Cout, double *Y) {
-  for (int64_t p = 0; p < P; ++p) {
-    const double *x = X + (int64_t)in_idx[p] * Cin;
-    const double *w = W + (int64_t)widx[p] * Cin * Cout;
-    double *y = Y + (int64_t)out_idx[p] * Cout;
-    for (int ci = 0; ci < Cin; ++ci) {
-      double xv = x[ci];
-      const double *wr = w + (int64_t)ci * Cout;
-      for (int c = 0; c < Cout; ++c) y[c] += xv * wr[c];
+  /* Y[out[p]] += X[in[p]] @ W[widx[p]].  The pairs are bucketed by output
+   * row (a stable counting sort, so each row still sums its pairs in list
+   * order) and the rows are summed in parallel. */
+  if (P <= 0) return;
+  int64_t nout = 0;
+  for (int64_t p = 0; p < P; ++p)
+    if (out_idx[p] + 1 > nout) nout = out_idx[p] + 1;
+  int64_t *start = (int64_t *)calloc((size_t)nout + 1, sizeof(int64_t));
+  int64_t *order = (int64_t *)malloc((size_t)P * sizeof(int64_t));
+  for (int64_t p = 0; p < P; ++p) start[out_idx[p] + 1]++;
+  for (int64_t t = 0; t < nout; ++t) start[t + 1] += start[t];
+  {
+    int64_t *fill = (int64_t *)malloc((size_t)nout * sizeof(int64_t));
+    for (int64_t t = 0; t < nout; ++t) fill[t] = start[t];
+    for (int64_t p = 0; p < P; ++p) order[fill[out_idx[p]]++] = p;
+    free(fill);
+  }
+#pragma omp parallel for schedule(dynamic, 64)
+  for (int64_t t = 0; t < nout; ++t) {
+    double *y = Y + t * Cout;
+    for (int64_t q = start[t]; q < start[t + 1]; ++q) {
+      const int64_t p = order[q];
+      const double *x = X + (int64_t)in_idx[p] * Cin;
+      const double *w = W + (int64_t)widx[p] * Cin * Cout;
+      for (int ci = 0; ci < Cin; ++ci) {
+        double xv = x[ci];
+        const double *wr = w + (int64_t)ci * Cout;
+        for (int c = 0; c < Cout; ++c) y[c] += xv * wr[c];
+      }
     }
   }
+  free(start);
+  free(order);
 }
 
 /* float32-accumulating output-stationary sum: the CPU baseline's compute leg

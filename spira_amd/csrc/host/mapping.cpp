@@ -35,6 +35,12 @@ struct PendingMap {
   int K = 0, dataflow = 0, dense = 0, R = 0, row0 = 0;
   bool half = false;
   torch::Tensor map, counts, tile_offsets, nbsizes, naddrs, qnaddrs, sizes, smask, tmask;
+  // scratch of the pair/mask scan.  Held here (not freed when stage_map
+  // returns) because the scan may run on a side stream: the caching
+  // allocator would hand a freed block straight to the next map's scan on
+  // another stream, and two decoupled look-back scans sharing one flag array
+  // can wait on each other forever.
+  torch::Tensor scan_ws;
 };
 
 static void check_keys(const torch::Tensor &src, const torch::Tensor &tgt) {
@@ -105,7 +111,8 @@ static PendingMap stage_map(const torch::Tensor &src, const torch::Tensor &tgt, 
   }
   size_t ws_bytes = 0;
   check_rc(spira_hip_kmap_scan_workspace(ncounts, &ws_bytes), "binary_search");
-  auto ws = workspace(ws_bytes, dev);
+  pm.scan_ws = workspace(ws_bytes, dev);
+  auto &ws = pm.scan_ws;
   check_rc(spira_hip_kmap_scan(pm.counts.data_ptr<int32_t>() + static_cast<int64_t>(pm.row0) * pm.ntiles, pm.R,
                                pm.ntiles, 128, pm.tile_offsets.data_ptr<int32_t>(), pm.nbsizes.data_ptr<int32_t>(),
                                pairs ? pm.naddrs.data_ptr<int32_t>() : nullptr,
@@ -198,8 +205,11 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
                       "size read-back failed");
     }
   }
+  // Odd dataflows need their pair counts on the host; hybrid dataflows above
+  // 4 transpose their dense part on the current stream in finish_map, so the
+  // side stream that wrote the map must be complete first.
   for (size_t i = 0; i < n; ++i)
-    if (dataflow[i] % 2 == 1)
+    if (dataflow[i] % 2 == 1 || dataflow[i] > 4)
       SPIRA_CHECK_ARG(hipStreamSynchronize(stream_of(i)) == hipSuccess, "stream synchronisation failed");
   for (size_t i = 0; i < n; ++i) {
     const int32_t *h = sizes_host.data_ptr<int32_t>() + 2 * i;
