@@ -48,6 +48,16 @@ int spira_hip_flatten_sort_workspace(int64_t n, int key_bits, size_t *bytes);
 int spira_hip_flatten_sort(const int32_t *coords, int64_t n, int key_bits, void *keys_out, int32_t *perm_out,
                            void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* spira_hip_flatten_sort without any allocation: the workspace is a fixed
+ * 32 MiB device array inside the library (one per GPU, held until the
+ * process ends), so n is limited to 1048576 points; larger n is rejected.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Calls that overlap on one GPU share the
+ * array and race; serialise them (one stream, or events). */
+int spira_hip_flatten_sort_noalloc(const int32_t *coords, int64_t n, int key_bits, void *keys_out, int32_t *perm_out,
+                                   hipStream_t stream);
+
 /* Workspace bytes for spira_hip_downsample, _plan and _execute. */
 int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes);
 

@@ -102,6 +102,41 @@ static int flatten_sort_impl(const int32_t *coords, int64_t n, CT *keys_out, int
   return kOk;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free flatten_sort: its workspace lives in a fixed device array.
+// Every GPU holds its own copy of `scratch` (for the life of the process);
+// host code must use the address hipGetSymbolAddress returns for the current
+// device, never the array's name (a host-side stand-in).
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocMaxPoints = int64_t(1) << 20;
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once
+// per device; nullptr (with the error set) on failure.
+static void *noalloc_scratch() {
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("flatten_sort_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error(std::string("flatten_sort_noalloc: hipGetSymbolAddress failed: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace spira_hip
 
 using namespace spira_hip;
@@ -150,6 +185,22 @@ int spira_hip_flatten_sort(const int32_t *coords, int64_t n, int key_bits, void 
                                        workspace_bytes, stream);
   return flatten_sort_impl<uint32_t>(coords, n, static_cast<uint32_t *>(keys_out), perm_out, workspace,
                                      workspace_bytes, stream);
+}
+
+int spira_hip_flatten_sort_noalloc(const int32_t *coords, int64_t n, int key_bits, void *keys_out, int32_t *perm_out,
+                                   hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "flatten_sort_noalloc: key_bits must be 32 or 64");
+  SPIRA_HIP_REQUIRE(n >= 0 && n <= kNoAllocMaxPoints,
+                    "flatten_sort_noalloc: at most 1048576 points (n = " + std::to_string(n) + ")");
+  if (n == 0) return kOk;
+  const size_t need = key_bits == 64 ? flatten_ws<uint64_t>(n) : flatten_ws<uint32_t>(n);
+  SPIRA_HIP_REQUIRE(need <= kNoAllocScratchBytes, "flatten_sort_noalloc: workspace of " + std::to_string(need) +
+                                                      " bytes exceeds the fixed scratch");
+  void *ws = noalloc_scratch();
+  if (ws == nullptr) return kHipError;
+  // every buffer in the scratch is fully written before it is read (pack +
+  // iota, then the sort), so nothing needs clearing between calls
+  return spira_hip_flatten_sort(coords, n, key_bits, keys_out, perm_out, ws, kNoAllocScratchBytes, stream);
 }
 
 }  // extern "C"
