@@ -85,18 +85,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), kRsrcWord3);
 }
 
-#ifdef SPIRA_BLOCK_TIMING
-// experiment builds only: per-step cycle stamps of wave 0 of a few blocks
-__device__ int64_t g_step_times[8 * 64 * 4];
-#define SPIRA_STEP_STAMP(step, ph)                                                            \
-  {                                                                                           \
-    const int sel_ = (blockIdx.x % 97 == 0 && blockIdx.x / 97 < 8) ? blockIdx.x / 97 : -1;    \
-    if (sel_ >= 0 && threadIdx.x == 0 && (step) >= 0 && (step) < 64)                                       \
-      g_step_times[(sel_ * 64 + (step)) * 4 + (ph)] = __builtin_amdgcn_s_memtime();           \
-  }
-#else
-#define SPIRA_STEP_STAMP(step, ph)
-#endif
 
 namespace ring {
 
@@ -471,13 +459,9 @@ __device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, F
     unroll<NS>([&](auto I) {
       constexpr int i = decltype(I)::value;
       constexpr int slot = (i + NS - 1) % NS;
-      SPIRA_STEP_STAMP(s + i, 0);
       wait_vm<(NS - 2) * C::LPS + (NS - 1) * PL>();
-      SPIRA_STEP_STAMP(s + i, 1);
       __builtin_amdgcn_s_barrier();
-      SPIRA_STEP_STAMP(s + i, 2);
       const StepIn nx = prepare(s + i + NS - 1, std::integral_constant<int, slot>{});
-      SPIRA_STEP_STAMP(s + i, 3);
       compute<C, i>(acc, rb, areg[i], [&](auto KQ) {
         issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value, OP>(cx, nx, op, xr, xr2, wr, areg[slot]);
         issue_slice<C, ALIGNED, CAT, slot, 2 * decltype(KQ)::value + 1, OP>(cx, nx, op, xr, xr2, wr, areg[slot]);
@@ -651,14 +635,6 @@ __device__ __forceinline__ void store_tile_vec(const floatx4 (&acc)[2][2 * WN], 
   }
 }
 
-#ifdef SPIRA_BLOCK_TIMING
-// experiment builds only: per-block wall-clock stamps of the OS kernel
-__device__ int64_t g_block_times[1 << 20];
-#define SPIRA_STAMP(slot) \
-  if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + (slot)] = wall_clock64()
-#else
-#define SPIRA_STAMP(slot)
-#endif
 
 // Output-stationary implicit GEMM.  A block owns BM = 128 logical rows
 // (wave w: rows [32 w, 32 w + 32) as two 16-row MFMA tiles) and BN = 32*WN
@@ -690,7 +666,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const int n0 = blockIdx.y * C::BN;
   const int j0 = blockIdx.z * jper;
   const int jn = ((j0 + jper) < Kc ? (j0 + jper) : Kc) - j0;
-  SPIRA_STAMP(0);
   // offsets [j0, j0 + jn) used by some row of the block, relative to j0
   uint64_t ulo = jn >= 64 ? ~uint64_t(0) : (uint64_t(1) << jn) - 1;
   uint64_t uhi = jn >= 128 ? ~uint64_t(0) : (jn > 64 ? (uint64_t(1) << (jn - 64)) - 1 : 0);
@@ -714,7 +689,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const int nch = (op.CinP + C::KC - 1) / C::KC;
   // OP > 1: OP offsets per step (one channel chunk each)
   const int nsteps = OP > 1 ? (nact + OP - 1) / OP : nact * nch;
-  SPIRA_STAMP(1);
 
   floatx4 acc[2][2 * WN];
   zero_acc<WN>(acc);
@@ -857,10 +831,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     if (tiled) read_tile();
   };
   ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
-  SPIRA_STAMP(2);
-#ifdef SPIRA_BLOCK_TIMING
-  if (threadIdx.x == 0 && blockIdx.x < (1 << 18)) g_block_times[blockIdx.x * 4 + 3] = nact;
-#endif
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -1407,14 +1377,6 @@ using namespace spira_hip;
 
 extern "C" {
 
-#ifdef SPIRA_BLOCK_TIMING
-int spira_hip_debug_block_times(int64_t *out, int n) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_block_times), sizeof(int64_t) * n) == hipSuccess ? 0 : 1;
-}
-int spira_hip_debug_step_times(int64_t *out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_step_times), sizeof(int64_t) * 8 * 64 * 4) == hipSuccess ? 0 : 1;
-}
-#endif
 
 int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int dtype, size_t *bytes) {
   *bytes = mfma_path(dtype) ? static_cast<size_t>(num_offsets) * pad_in(c_in) * pad_out(c_out) * sizeof(_Float16) : 0;

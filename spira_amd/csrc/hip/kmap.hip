@@ -70,6 +70,13 @@ __device__ __forceinline__ void sample_bucket(CT sample, CT v, int64_t base, int
   bhi = p < end ? p : end;
 }
 
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 template <typename CT>
 __device__ __forceinline__ int lds_lower_bound(const CT *win, int n, CT v) {
   int base = 0, len = n;
@@ -95,10 +102,22 @@ __device__ __forceinline__ int64_t global_lower_bound(const CT *__restrict__ src
   return lo;
 }
 
-template <typename CT, int KZ>
+// Layout variants of the search kernel (compile-time, so that the store
+// path carries no per-entry layout tests).
+enum SearchLayout : int {
+  kLayoutOsZ = 0,  // [Tp, K], column iz*O + o (output-stationary, z-major)
+  kLayoutWs = 1,   // [K, Tp], row k (or perm[k]), plus per-(row, tile) counts
+  kLayoutNoz = 2,  // [Tp, K], column k, full offsets and no z-scan (KZ = 1)
+};
+
+// GS: offsets per dx-group when known at compile time (the dy range of the
+// common kernels), else 0 (runtime p.GS, in chunks of kChunk).
+template <typename CT, int KZ, int GS, int LAYOUT>
 __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const SearchParams<CT> p) {
+  constexpr int kChunk = GS > 0 ? GS : 4;
   extern __shared__ __align__(16) char smem[];
   const int g = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // dx-group of this wave
+  const int gs = GS > 0 ? GS : p.GS;
   CT *win = reinterpret_cast<CT *>(smem) + g * kWindowCap;
   int32_t *stage = reinterpret_cast<int32_t *>(smem + p.G * kWindowCap * sizeof(CT));
 
@@ -115,7 +134,7 @@ __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const Searc
 
   if (ballot(valid) == 0) {
     // fully padded tile: every entry is -1
-    if (p.os_layout) {
+    if constexpr (LAYOUT != kLayoutWs) {
       for (int i = threadIdx.x; i < 64 * p.K; i += blockDim.x) p.map[tile * 64 * p.K + i] = -1;
     } else {
       for (int r = g; r < p.K; r += p.G) {
@@ -130,8 +149,8 @@ __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const Searc
   CT vals[2];
   {
     CT mn = max_key<CT>(), mx = CT(0);
-    for (int j = 0; j < p.GS; ++j) {
-      CT q = key + p.off[g * p.GS + j];
+    for (int j = 0; j < gs; ++j) {
+      CT q = key + p.off[g * gs + j];
       if (valid) {
         mn = q < mn ? q : mn;
         mx = q > mx ? q : mx;
@@ -164,54 +183,123 @@ __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const Searc
   }
 
   // 3. stage the window, search, z-scan, store
-  const int64_t lo = lb[0];
-  int64_t hi = lb[1] + KZ;
+  // the window bounds are wave-uniform (ballot results); saying so keeps
+  // them, the window branch and the search trip counts in scalar registers
+  const int64_t lo = uniform64(lb[0]);
+  int64_t hi = uniform64(lb[1]) + KZ;
   if (hi > p.S) hi = p.S;
   const int n = static_cast<int>(hi - lo);
   const bool in_lds = (hi - lo) <= kWindowCap;
   if (in_lds) {
-    for (int i = lane; i < n; i += 64) win[i] = p.src[lo + i];
+    // every load of the window is issued before the first LDS write
+    CT r[kWindowCap / 64];
+#pragma unroll
+    for (int i = 0; i < kWindowCap / 64; ++i) {
+      const int q = lane + 64 * i;
+      r[i] = q < n ? p.src[lo + q] : CT(0);
+    }
+#pragma unroll
+    for (int i = 0; i < kWindowCap / 64; ++i) {
+      const int q = lane + 64 * i;
+      if (q < n) win[q] = r[i];
+    }
     // the window is private to this wave: LDS keeps a wave's accesses in order
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  for (int j = 0; j < p.GS; ++j) {
-    const int o = g * p.GS + j;
-    // padded lanes query the group minimum so that every index stays inside the window
-    CT c = valid ? CT(key + p.off[o]) : vals[0];
-    int64_t idx = in_lds ? lo + lds_lower_bound(win, n, c) : global_lower_bound(p.src, lo, hi, c);
-    int32_t res[KZ];
-    {
-      CT v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
-      res[0] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
+
+  // one entry: [Tp, K] layouts stage the tile block in LDS; [K, Tp] writes
+  // coalesced rows and the row's valid count of this tile
+  auto emit = [&](int o, int iz, int32_t r) {
+    if constexpr (LAYOUT == kLayoutOsZ) {
+      stage[lane * p.K + iz * p.O + o] = r;
+    } else if constexpr (LAYOUT == kLayoutNoz) {
+      stage[lane * p.K + o] = r;
+    } else {
+      const int k = o * KZ + iz;
+      const int row = p.use_perm ? p.perm[k] : k;
+      p.map[row * p.Tp + t] = r;
+      if (p.tile_counts) {
+        const uint64_t m = ballot(r >= 0);
+        if (lane == 0) p.tile_counts[row * p.ntiles + tile] = __builtin_popcountll(m);
+      }
+    }
+  };
+
+  if (in_lds) {
+    // The group's offsets in chunks, the chunk's lower bounds and z-scans
+    // interleaved so that their dependent LDS reads overlap.  The lower bound
+    // is the branch-free form over the wave-uniform window length (every lane
+    // runs the same steps).  Padded lanes, and offsets past the group, query
+    // the group minimum, which keeps every index inside the window.
+    for (int j0 = 0; j0 < gs; j0 += kChunk) {
+      CT c[kChunk];
+      int base[kChunk];
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        const bool act = valid && (GS > 0 || j0 + j < gs);
+        c[j] = act ? CT(key + p.off[g * gs + j0 + j]) : vals[0];
+        base[j] = 0;
+      }
+      for (int len = n; len > 1;) {
+        const int half = len >> 1;
+        CT w[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) w[j] = win[base[j] + half - 1];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) base[j] = w[j] < c[j] ? base[j] + half : base[j];
+        len -= half;
+      }
+      int idx[kChunk];
+      CT v[kChunk];
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        v[j] = n > 0 ? win[base[j]] : CT(0);
+        idx[j] = base[j] + ((n > 0 && v[j] < c[j]) ? 1 : 0);
+      }
+      // z-scan (query_sorted.cuh:8-163).  An index at the window end is past
+      // the end of the sources: the window holds lb(max) + KZ entries unless
+      // it ends at S.
+#pragma unroll
+      for (int iz = 0; iz < KZ; ++iz) {
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+          if (iz > 0) {
+            if (idx[j] < n && v[j] <= c[j]) ++idx[j];
+            c[j] += sz;
+          }
+          v[j] = idx[j] < n ? win[idx[j]] : CT(0);
+        }
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+          if (GS > 0 || j0 + j < gs) {
+            const int32_t r = (valid && idx[j] < n && v[j] == c[j]) ? static_cast<int32_t>(lo + idx[j]) : -1;
+            emit(g * gs + j0 + j, iz, r);
+          }
+        }
+      }
+    }
+  } else {
+    // window larger than the LDS slot (rare): per-lane search in global
+    // memory, restricted to the window (same results)
+    for (int j = 0; j < gs; ++j) {
+      const int o = g * gs + j;
+      CT c = valid ? CT(key + p.off[o]) : vals[0];
+      int64_t idx = global_lower_bound(p.src, lo, hi, c);
+      CT v = idx < p.S ? p.src[idx] : CT(0);
+      emit(o, 0, (valid && idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1);
 #pragma unroll
       for (int iz = 1; iz < KZ; ++iz) {
         if (idx < p.S && v <= c) ++idx;
         c += sz;
-        v = idx < p.S ? (in_lds ? win[idx - lo] : p.src[idx]) : CT(0);
-        res[iz] = (idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1;
-      }
-    }
-#pragma unroll
-    for (int iz = 0; iz < KZ; ++iz) {
-      const int32_t r = valid ? res[iz] : -1;
-      const int k = o * KZ + iz;
-      if (p.os_layout) {
-        const int col = p.zmajor ? iz * p.O + o : k;
-        stage[lane * p.K + col] = r;
-      } else {
-        const int row = p.use_perm ? p.perm[k] : k;
-        p.map[row * p.Tp + t] = r;
-        if (p.tile_counts) {
-          uint64_t m = ballot(r >= 0);
-          if (lane == 0) p.tile_counts[row * p.ntiles + tile] = __builtin_popcountll(m);
-        }
+        v = idx < p.S ? p.src[idx] : CT(0);
+        emit(o, iz, (valid && idx < p.S && v == c) ? static_cast<int32_t>(idx) : -1);
       }
     }
   }
 
-  if (p.os_layout) {
+  if constexpr (LAYOUT != kLayoutWs) {
     __syncthreads();
     int32_t *dst = p.map + tile * 64 * p.K;
     const int total = 64 * p.K;  // multiple of 4
@@ -240,6 +328,40 @@ template <typename CT> static void make_offsets(int kx, int ky, int kz, int sx, 
                                      static_cast<CT>(kmin(kz) * sz));
       }
     }
+}
+
+template <typename CT, int KZ, int LAYOUT>
+static void launch_search_l(int gs, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const SearchParams<CT> &p) {
+  switch (gs) {
+    case 1: hipLaunchKernelGGL((kmap_search_kernel<CT, KZ, 1, LAYOUT>), grid, block, lds, stream, p); break;
+    case 2: hipLaunchKernelGGL((kmap_search_kernel<CT, KZ, 2, LAYOUT>), grid, block, lds, stream, p); break;
+    case 3: hipLaunchKernelGGL((kmap_search_kernel<CT, KZ, 3, LAYOUT>), grid, block, lds, stream, p); break;
+    case 5: hipLaunchKernelGGL((kmap_search_kernel<CT, KZ, 5, LAYOUT>), grid, block, lds, stream, p); break;
+    default: hipLaunchKernelGGL((kmap_search_kernel<CT, KZ, 0, LAYOUT>), grid, block, lds, stream, p); break;
+  }
+}
+
+template <typename CT, int KZ>
+static void launch_search_kz(int gs, int lay, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                             const SearchParams<CT> &p) {
+  if (lay == kLayoutOsZ) launch_search_l<CT, KZ, kLayoutOsZ>(gs, grid, block, lds, stream, p);
+  else launch_search_l<CT, KZ, kLayoutWs>(gs, grid, block, lds, stream, p);
+}
+
+// KZ = 1 serves the full-offset layout (no z-scan) and kernels of depth 1
+template <typename CT>
+static void launch_search(int kz, int gs, int lay, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                          const SearchParams<CT> &p) {
+  switch (kz) {
+    case 1:
+      if (lay == kLayoutNoz) hipLaunchKernelGGL((kmap_search_kernel<CT, 1, 0, kLayoutNoz>), grid, block, lds, stream, p);
+      else launch_search_kz<CT, 1>(gs, lay, grid, block, lds, stream, p);
+      break;
+    case 2: launch_search_kz<CT, 2>(gs, lay, grid, block, lds, stream, p); break;
+    case 3: launch_search_kz<CT, 3>(gs, lay, grid, block, lds, stream, p); break;
+    case 4: launch_search_kz<CT, 4>(gs, lay, grid, block, lds, stream, p); break;
+    default: launch_search_kz<CT, 5>(gs, lay, grid, block, lds, stream, p); break;
+  }
 }
 
 template <typename CT>
@@ -293,14 +415,8 @@ static int search_impl(const CT *src, int64_t S, const CT *tgt, int64_t T, int k
   if (p.Tp == 0) return kOk;
   const size_t lds = p.G * kWindowCap * sizeof(CT) + (p.os_layout ? 64 * K * sizeof(int32_t) : 0);
   dim3 grid(static_cast<unsigned>(p.ntiles)), block(64 * p.G);
-  switch (KZ) {
-    case 1: hipLaunchKernelGGL((kmap_search_kernel<CT, 1>), grid, block, lds, stream, p); break;
-    case 2: hipLaunchKernelGGL((kmap_search_kernel<CT, 2>), grid, block, lds, stream, p); break;
-    case 3: hipLaunchKernelGGL((kmap_search_kernel<CT, 3>), grid, block, lds, stream, p); break;
-    case 4: hipLaunchKernelGGL((kmap_search_kernel<CT, 4>), grid, block, lds, stream, p); break;
-    case 5: hipLaunchKernelGGL((kmap_search_kernel<CT, 5>), grid, block, lds, stream, p); break;
-    default: SPIRA_HIP_REQUIRE(false, "Currently Kernel Size in Z axis can only be 1..5");
-  }
+  const int lay = layout == SPIRA_KMAP_NOZ ? kLayoutNoz : (p.os_layout ? kLayoutOsZ : kLayoutWs);
+  launch_search<CT>(KZ, p.GS, lay, grid, block, lds, stream, p);
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }
