@@ -3,24 +3,28 @@
 Headline (BASELINE.json metric): end-to-end latency of the config-4 workload
 -- SparseResUNet42, fp16, random-init weights, on a 200k-voxel synthetic
 indoor scene -- timed like the reference (scripts/end_to_end_experiment.py:
-156-252): kernel-map cache reset, then `order()` (pack + sort), the
+126-252): the selector (spira_amd.tune) runs first, outside the timed region;
+then per step the kernel-map cache is reset and `order()` (pack + sort), the
 network-wide kernel-map build (`add_all_kernel_maps`) and the forward pass
-inside one event-timed region.  Also reported on the same run:
-  * kmap_build_us: one kernel-map search (config 2, ~100k LiDAR voxels,
-    k=3, 64-bit keys, output-stationary layout) as in mapping_experiment.py;
-  * layer_ms: one output-stationary fp16 layer (config 3, C=64);
-  * config5_ms: the large-kernel network of config 5 (SparseResNetLarge, k=5,
-    fp16) end to end on the ~300k-voxel LiDAR-plus-blobs scene, timed like
-    the headline (10 steps after 5 warm-ups);
-  * roofline: the dominant kernel (output-stationary MFMA conv) against its
-    binding roofline -- HBM for the full-resolution 96->96 layer, whose
-    algorithmic bytes take longer at peak bandwidth than its flops at peak
-    MFMA rate (the MFMA fraction is reported beside it) -- and
-    kmap_roofline: the map search against HBM peak;
-  * cpu_baseline: the same end-to-end pipeline run by the OpenMP CPU
-    restatement (oracle/) on the host cores (one scene).
+run inside one event-timed region.  Also reported on the same run:
+  * config 4 per layer (in-network): every convolution's time inside one
+    steady-state step (HIP events at layer boundaries), its algorithmic bytes
+    and flops, and the per-step dominant family (stride, C_in, C_out,
+    offsets) with its binding roofline -> `roofline`;
+  * config5_ms: the large-kernel SparseResNetLarge (k = 5, fp16) end to end
+    on the ~300k-voxel LiDAR-plus-blobs scene, timed like the headline;
+  * kmap: the map search of config 2 (~100k LiDAR voxels, 64-bit keys) for
+    k = 3 / 5 at stride 1 / 2, per API call (as mapping_experiment.py:81-101
+    times it) and kernel only, against HBM peak;
+  * layers: config 3 (LiDAR, k = 3, stride 1, C = 16 ... 256), every
+    dataflow (output-stationary, fused weight-stationary, gather-GEMM-scatter,
+    hybrids 3-8) timed per layer call (layerwise_experiment.py:100-186), the
+    selector's pick (the fastest), and each against the fp16 MFMA peak;
+  * cpu_baseline: the same legs by the OpenMP CPU restatement (oracle/) on
+    the host cores, each checked against the GPU result: config 4 end to end
+    (headline), the config-2 k = 3 map and a config-3 C = 64 layer.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only legs]
 """
 from __future__ import annotations
 
@@ -29,6 +33,7 @@ import json
 import os
 import sys
 import time
+from collections import defaultdict
 
 import numpy as np
 
@@ -37,12 +42,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the dominant kernel (os_kernel<3,0,true,8,false,1>, 200k
-# voxels, 96 -> 96): rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE over
-# `bench.py --no-cpu --only layer,calib`, each scaled by what the counter
-# reads for the calibration leg's 256 MiB copy (FETCH_SIZE x 2.000,
-# WRITE_SIZE x 1.000): 68049 KiB fetched, 37578 KiB written.
-DOMINANT_TRAFFIC_BYTES = 68049 * 1024 * 2.0 + 37578 * 1024 * 1.0
+# HBM bytes per launch of the dominant family's kernel, from rocprofv3 --pmc
+# FETCH_SIZE and --pmc WRITE_SIZE over `bench.py --only family,calib`, each
+# scaled by what the counter reads for the calibration leg's 256 MiB copy
+# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000; the command and the raw figures
+# are in profiles/).  None until measured for the current dominant kernel.
+DOMINANT_TRAFFIC_BYTES = None
 
 
 def parse():
@@ -50,143 +55,335 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--dataflow", type=int, default=0, help="map dataflow used by every layer")
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--dataflow", type=int, default=0, help="map dataflow of every layer without the selector")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     p.add_argument("--no-fuse", action="store_true", help="run batch norm / ReLU / residual adds unfused")
-    p.add_argument("--only", default="", help="comma list of legs: e2e,kmap,layer,config5 (calib: a plain 256 MiB "
-                                              "device copy, the reference point of the HBM byte counters)")
+    p.add_argument("--no-tune", action="store_true", help="skip the selector (library default launch choices)")
+    p.add_argument("--only", default="", help="comma list of legs: e2e, config5, kmap, layer, family (the "
+                                              "dominant family's layers alone, for counters), calib (a plain "
+                                              "256 MiB device copy: the reference point of the HBM counters)")
+    p.add_argument("--layer-table", default="", help="write the per-layer in-network table (markdown) here")
     return p.parse_args()
 
 
-class Timer:
-    """HIP-event timing on the current stream (the one the kernels run on)."""
-
-    def __init__(self, torch):
-        self.torch = torch
-
-    def __call__(self, fn, reps: int, warmup: int = 2):
-        torch = self.torch
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        times = []
-        for _ in range(reps):
-            s.record()
-            fn()
-            e.record()
-            e.synchronize()
-            times.append(s.elapsed_time(e))
-        return float(np.mean(times)), float(np.min(times))
+def event_time(torch, fn, reps: int, warmup: int = 2) -> float:
+    """Mean ms per call of fn() between HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
 
 
-def e2e_leg(torch, args, coords_np, net="UNet", steps=None, warmup=None):
-    """End-to-end step of `net` (UNet: SparseResUNet42, config 4; ResNetLarge:
-    the k = 5 SparseResNetLarge, config 5): map cache reset, order(), the
-    network-wide map build and the forward pass, event-timed."""
-    import spira_amd
-    from spira_amd.networks import SparseResNetLarge, SparseResUNet42, kmap_schedule
+# ---------------------------------------------------------------------------
+# end to end (configs 4 and 5)
+# ---------------------------------------------------------------------------
+def e2e_inputs(torch, coords_np, cin, seed=7):
+    """Coordinates and fp16 N(0, 1) features of an end-to-end run, on the GPU
+    (seeded, so that the CPU baseline sees the same features)."""
+    g = torch.Generator().manual_seed(seed)
+    feats = torch.randn(coords_np.shape[0], cin, generator=g).half()
     dev = torch.device("cuda:0")
-    torch.manual_seed(0)
-    cin = 3 if net == "UNet" else 4
-    model = (SparseResUNet42 if net == "UNet" else SparseResNetLarge)(in_channels=cin).to(dev).half().eval()
-    steps = args.steps if steps is None else steps
-    warmup = args.warmup if warmup is None else warmup
-    if not args.no_fuse:
-        spira_amd.nn.fuse_epilogues(model)
-    cache = spira_amd.nn.KernelMapCache()
-    spira_amd.set_kernel_map_cache(model, cache)
-    for m in model.modules():
-        if isinstance(m, spira_amd.nn.SparseConv):
-            m._tunable_config["map_dataflow"] = args.dataflow
-    ts, ks, ss = kmap_schedule(net)
-    coords = torch.from_numpy(coords_np).to(dev)
-    feats = torch.randn(coords.shape[0], cin, device=dev, dtype=torch.float16)
+    return torch.from_numpy(coords_np).to(dev), feats.to(dev)
 
-    def step():
-        cache.reset()
-        x = spira_amd.SparseTensor(coordinates=coords, features=feats, double=True)
+
+def layer_groups(net):
+    """(source stride, kernel size, layer stride) of each network-wide map,
+    the key under which the selector reports a map's dataflow (the
+    reference's lookup, scripts/end_to_end_experiment.py:141-150)."""
+    from spira_amd.networks import kmap_schedule
+    _, ks, ss = kmap_schedule(net)
+    return [(tuple(ss[i]), tuple(ks[i]), tuple(b // a for a, b in zip(ss[i], ss[i + 1]))) for i in range(len(ks))]
+
+
+class E2E:
+    """One end-to-end workload: model, inputs, map schedule, and the step
+    (cache reset, order(), network-wide map build, forward)."""
+
+    def __init__(self, torch, args, coords_np, net):
+        import spira_amd
+        from spira_amd.networks import SparseResNetLarge, SparseResUNet42, kmap_schedule
+        self.torch, self.net = torch, net
+        dev = torch.device("cuda:0")
+        torch.manual_seed(0)
+        self.cin = 3 if net == "UNet" else 4
+        self.model = (SparseResUNet42 if net == "UNet" else SparseResNetLarge)(in_channels=self.cin)
+        self.model = self.model.to(dev).half().eval()
+        if not args.no_fuse:
+            spira_amd.nn.fuse_epilogues(self.model)
+        self.cache = spira_amd.nn.KernelMapCache()
+        spira_amd.set_kernel_map_cache(self.model, self.cache)
+        for m in self.model.modules():
+            if isinstance(m, spira_amd.nn.SparseConv):
+                m._tunable_config["map_dataflow"] = args.dataflow
+        self.ts, self.ks, self.ss = kmap_schedule(net)
+        self.coords, self.feats = e2e_inputs(torch, coords_np, self.cin)
+        self.dataflows = [args.dataflow] * len(self.ks)
+        self.chosen = None
+
+    def tune(self):
+        """The selector: dataflow per layer group (0-2, as fast as the model
+        runs them), then the output-stationary launch choices per layer and
+        the row order per map."""
+        import tempfile
+        import spira_amd
+
+        def sample():
+            x = spira_amd.SparseTensor(coordinates=self.coords, features=self.feats, double=True)
+            return x.order()
+
+        with tempfile.TemporaryDirectory() as d:
+            self.model, groups = spira_amd.tune(self.model, [sample() for _ in range(6)], self.cache,
+                                                map_dataflow_options=[0, 1, 2], test_force_os=False, n_samples=5,
+                                                save_dir=d, tune_tag=self.net, force_retune=True,
+                                                allow_gs_tuning=False, return_dataflows=True)
+        self.dataflows = [groups.get(g, d) for g, d in zip(layer_groups(self.net), self.dataflows)]
+        self.chosen = {"map_dataflows": self.dataflows,
+                       "row_orders": {str(k): v for k, v in self.cache.row_order_requests.items()}}
+
+    def step(self):
+        import spira_amd
+        self.cache.reset()
+        x = spira_amd.SparseTensor(coordinates=self.coords, features=self.feats, double=True)
         x.order()
-        cache.add_all_kernel_maps(x._coordinates, ks, ss, ts, (1, 1, 1), [args.dataflow] * len(ks))
-        return model(x)
+        self.cache.add_all_kernel_maps(x._coordinates, self.ks, self.ss, self.ts, (1, 1, 1), self.dataflows)
+        return self.model(x)
 
-    with torch.no_grad():
-        for _ in range(warmup):
-            step()
+    def time(self, steps, warmup):
+        torch = self.torch
+        with torch.no_grad():
+            for _ in range(warmup):
+                self.step()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            s.record()
+            for _ in range(steps):
+                out = self.step()
+            e.record()
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e3 / steps
+        return s.elapsed_time(e) / steps, wall, [o._features for o in out]
+
+
+def layer_work(m, S, T, P, K):
+    """Algorithmic bytes and flops of one layer launch: fp16 features read
+    and written once, fp16 weights, the int32 map read once; 2 P C_in C_out
+    flops (P valid pairs)."""
+    cin, cout = m.in_channels, m.out_channels
+    nbytes = 2.0 * (S * cin + T * cout) + 2.0 * K * cin * cout + (4.0 * K * T if K > 1 else 0.0)
+    return nbytes, 2.0 * P * cin * cout
+
+
+def per_layer_profile(torch, e2e: E2E, reps: int = 5):
+    """Every convolution's in-network time: HIP events at the layer's
+    boundaries inside full steps (mean over `reps` steps), with its shape,
+    valid pairs and algorithmic work."""
+    import spira_amd
+    convs = [(n, m) for n, m in e2e.model.named_modules() if isinstance(m, spira_amd.nn.SparseConv)]
+    rec = defaultdict(list)
+    meta = {}
+    timing = False
+
+    def pre(name, mod, inputs):
+        if timing:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            rec[name].append([ev, None])
+
+    def post(name, mod, inputs, output):
+        if timing:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            rec[name][-1][1] = ev
+            return
+        x = inputs[0]
+        S, T = x._features.shape[0], output._features.shape[0]
+        K = int(np.prod(mod.kernel_size))
+        if mod.is_trivial:
+            P = T
+        else:
+            key = ((tuple(output._stride), tuple(x._stride)) if mod.transposed
+                   else (tuple(x._stride), tuple(output._stride))) + (tuple(mod.kernel_size),)
+            entry = mod._kernel_map_cache._kernel_maps_cache[key]
+            omap, Tf = entry[3], entry[2]  # the forward layer's map and targets
+            os_layout = entry[0] or mod._tunable_config["map_dataflow"] == 0
+            P = int((omap[:Tf] >= 0).sum().item()) if os_layout else int((omap[:, :Tf] >= 0).sum().item())
+        meta[name] = {"S": S, "T": T, "P": P, "K": K, "stride": tuple(output._stride),
+                      "cin": mod.in_channels, "cout": mod.out_channels,
+                      "dataflow": mod._tunable_config["map_dataflow"], "transposed": mod.transposed}
+
+    handles = []
+    for n, m in convs:
+        handles.append(m.register_forward_pre_hook(lambda mod, inp, n=n: pre(n, mod, inp)))
+        handles.append(m.register_forward_hook(lambda mod, inp, out, n=n: post(n, mod, inp, out)))
+    try:
+        with torch.no_grad():
+            timing = False
+            e2e.step()  # shapes and valid pairs (reads back counts: not timed)
+            timing = True
+            for _ in range(reps):
+                e2e.step()
         torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        s.record()
-        for _ in range(steps):
-            out = step()
-        e.record()
-        torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) * 1e3 / steps
-        ms = s.elapsed_time(e) / steps
-    return ms, wall, model, [o._features for o in out]
+    finally:
+        for h in handles:
+            h.remove()
+    rows = []
+    for n, m in convs:
+        if n not in meta:
+            continue
+        ms = float(np.mean([a.elapsed_time(b) for a, b in rec[n]]))
+        d = meta[n]
+        nbytes, flops = layer_work(m, d["S"], d["T"], d["P"], d["K"])
+        rows.append({"layer": n, **d, "ms": ms, "bytes": nbytes, "flops": flops})
+    return rows
 
 
-def kmap_leg(torch, keys_np):
-    """Config 2: build_kmap(dataflow=0) per call as the reference times it
-    (HIP events around the Python call, host overhead included) and the
-    search kernel alone (back-to-back launches from C++)."""
+def family_roofline(rows):
+    """Group the layers by (stride, C_in, C_out, offsets); the family with the
+    largest in-network time per step is the dominant one.  Its roofline: the
+    binding bound of its summed algorithmic work (bytes at HBM peak vs flops
+    at MFMA peak) against its summed time."""
+    fam = defaultdict(lambda: {"ms": 0.0, "bytes": 0.0, "flops": 0.0, "launches": 0})
+    for r in rows:
+        key = (r["stride"][0], r["cin"], r["cout"], r["K"])
+        f = fam[key]
+        f["ms"] += r["ms"]
+        f["bytes"] += r["bytes"]
+        f["flops"] += r["flops"]
+        f["launches"] += 1
+    key, f = max(fam.items(), key=lambda kv: kv[1]["ms"])
+    gbs = f["bytes"] / (f["ms"] * 1e-3) / 1e9
+    tf = f["flops"] / (f["ms"] * 1e-3) / 1e12
+    mfma_bound = f["flops"] / (MFMA_F16_PEAK_TFLOPS * 1e12) > f["bytes"] / (HBM_PEAK_GBS * 1e9)
+    if mfma_bound:
+        rl = {"bound": "mfma", "achieved": tf, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+              "frac": tf / MFMA_F16_PEAK_TFLOPS}
+    else:
+        rl = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
+    rl.update({"traffic": DOMINANT_TRAFFIC_BYTES,
+               "kernel": f"os_kernel family: stride {key[0]}, {key[1]} -> {key[2]} channels, {key[3]} offsets "
+                         f"({f['launches']} launches per step, in-network)",
+               "ms_per_step": f["ms"], "algorithmic_bytes_per_step": f["bytes"],
+               "algorithmic_flops_per_step": f["flops"], "hbm_gbs": gbs, "mfma_tflops": tf,
+               "mfma_frac": tf / MFMA_F16_PEAK_TFLOPS, "hbm_frac": gbs / HBM_PEAK_GBS})
+    fams = sorted(({"family": f"s{k[0]} {k[1]}->{k[2]} K{k[3]}", "ms": v["ms"], "launches": v["launches"],
+                    "mfma_frac": v["flops"] / (v["ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
+                    "hbm_frac": v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                   for k, v in fam.items()), key=lambda d: -d["ms"])
+    return rl, fams, key
+
+
+def write_layer_table(path, rows, step_ms):
+    lines = ["| # | layer | stride | C_in -> C_out | K | T | P | dataflow | in-network us | "
+             "TFLOP/s | MFMA frac | GB/s | HBM frac |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for i, r in enumerate(rows):
+        tf = r["flops"] / (r["ms"] * 1e-3) / 1e12
+        gb = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+        lines.append(f"| {i} | {r['layer']} | {r['stride'][0]} | {r['cin']} -> {r['cout']} | {r['K']} | {r['T']} | "
+                     f"{r['P']} | {r['dataflow']}{' (T)' if r['transposed'] else ''} | {r['ms'] * 1e3:.1f} | "
+                     f"{tf:.0f} | {tf / MFMA_F16_PEAK_TFLOPS:.3f} | {gb:.0f} | {gb / HBM_PEAK_GBS:.3f} |")
+    conv_ms = sum(r["ms"] for r in rows)
+    lines.append("")
+    lines.append(f"Convolutions: {conv_ms:.3f} ms of a {step_ms:.3f} ms step (layer-boundary events, so each "
+                 f"row includes the layer's host launch gaps).")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+# ---------------------------------------------------------------------------
+# config 2: kernel-map search
+# ---------------------------------------------------------------------------
+def kmap_leg(torch, keys):
+    """build_kmap(dataflow=0) per call as the reference times it (HIP events
+    around the Python call, host overhead included) and the search kernel
+    alone (back-to-back launches from C++), k = 3 / 5, stride 1 / 2."""
     from spira_amd.nn import functional as F
     from spira_amd.nn.functional import _native
-    dev = torch.device("cuda:0")
-    keys = torch.from_numpy(keys_np).to(dev)
-    timer = Timer(torch)
-    S = T = keys.shape[0]
     out = {}
-    for k in (3, 5):
-        mean_ms, min_ms = timer(lambda: F.build_kmap(keys, keys, k, 1, 0), reps=20, warmup=3)
-        kern_ms = _native._C.time_kmap_search(keys, keys, (k, k, k), (1, 1, 1), 50)
-        K = k ** 3
-        nbytes = 8 * S + 8 * T + 4 * K * T
-        out[k] = {"us": mean_ms * 1e3, "min_us": min_ms * 1e3, "kernel_us": kern_ms * 1e3, "bytes": nbytes,
-                  "gbs": nbytes / (kern_ms * 1e-3) / 1e9}
+    for s in (1, 2):
+        tgt = keys if s == 1 else F.downsample(keys, (2, 2, 2))
+        S, T = keys.shape[0], tgt.shape[0]
+        for k in (3, 5):
+            api_ms = event_time(torch, lambda: F.build_kmap(keys, tgt, k, 1, 0), reps=20, warmup=3)
+            kern_ms = _native._C.time_kmap_search(keys, tgt, (k, k, k), (1, 1, 1), 50)
+            nbytes = 8 * S + 8 * T + 4 * k ** 3 * T
+            out[f"k{k}s{s}"] = {"api_us": api_ms * 1e3, "kernel_us": kern_ms * 1e3, "S": S, "T": T,
+                                "algorithmic_bytes": nbytes, "gbs": nbytes / (kern_ms * 1e-3) / 1e9,
+                                "frac": nbytes / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
 
 
-def layer_leg(torch, keys_np, channels=(16, 32, 64, 128, 256), reps=20):
-    """Config 3 (LiDAR, k=3, s=1): the output-stationary fp16 layer per
-    channel count, kernel only (back-to-back launches from C++)."""
+# ---------------------------------------------------------------------------
+# config 3: one layer, every dataflow
+# ---------------------------------------------------------------------------
+def layer_leg(torch, keys, channels=(16, 32, 64, 128, 256), reps=10):
+    """Per channel count C (C_in = C_out): each dataflow's layer call timed
+    with HIP events around it (maps built beforehand, like the reference's
+    layerwise experiment), the output-stationary kernel alone, and the
+    selector's pick (the fastest dataflow)."""
     from spira_amd.nn import functional as F
     from spira_amd.nn.functional import _native
     dev = torch.device("cuda:0")
-    keys = torch.from_numpy(keys_np).to(dev)
-    m = F.build_kmap(keys, keys, 3, 1, 0)
     S = T = keys.shape[0]
-    P = int((m[2][:T] >= 0).sum().item())
+    maps = {d: F.build_kmap(keys, keys, 3, 1, d) for d in range(9)}
+    P = int((maps[0][2][:T] >= 0).sum().item())
     out = {}
     for C in channels:
-        X = torch.randn(S, C, device=dev, dtype=torch.float16)
-        W = (torch.randn(27, C, C, device=dev) / np.sqrt(27 * C)).half()
-        ms = _native._C.time_conv_os(S, T, m[2], X, W, reps)
+        g = torch.Generator().manual_seed(C)
+        X = torch.randn(S, C, generator=g).half().to(dev)
+        W = (torch.randn(27, C, C, generator=g) / np.sqrt(27 * C)).half().to(dev)
+        calls = {
+            "os": lambda: F.sparse_convolution_forward_os(S, T, maps[0][2], X, W),
+            "ws_fused": lambda: F.sparse_convolution_forward_ws_merged(S, T, X, W, maps[1][5], maps[1][6],
+                                                                       maps[1][3], maps[1][7], maps[1][8]),
+            "ws_gather_gemm_scatter": lambda: F.sparse_convolution_forward_ws(S, T, X, W, maps[2][3], maps[2][4],
+                                                                              maps[2][5], 16, 16, None, -1),
+        }
+        for d in (3, 5, 7):
+            m = maps[d]
+            calls[f"hybrid{d}"] = (lambda m=m, d=d: F.sparse_convolution_forward_hs_merged(
+                S, T, X, W, m[5], m[6], m[3], None if d == 3 else m[2], m[7], m[8]))
+        for d in (4, 6, 8):
+            m = maps[d]
+            calls[f"hybrid{d}"] = (lambda m=m, d=d: F.sparse_convolution_forward_hs(
+                S, T, X, W, m[3], m[4], m[5], None if d == 4 else m[2], 16, 16))
         flops = 2.0 * P * C * C
-        out[C] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+        res = {}
+        for name, fn in calls.items():
+            ms = event_time(torch, fn, reps=reps)
+            res[name] = {"ms": ms, "mfma_frac": flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS}
+        kern = _native._C.time_conv_os(S, T, maps[0][2], X, W, 20)
+        pick = min(res, key=lambda k: res[k]["ms"])
+        nbytes = 2.0 * (S * C + T * C) + 2.0 * 27 * C * C + 4.0 * 27 * T
+        out[str(C)] = {"dataflows": res, "selector_pick": pick, "selector_ms": res[pick]["ms"],
+                       "os_kernel_ms": kern, "os_kernel_mfma_frac": flops / (kern * 1e-3) / 1e12 /
+                       MFMA_F16_PEAK_TFLOPS, "os_kernel_hbm_frac": nbytes / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return {"pairs": P, "voxels": S, "per_C": out}
 
 
-def dominant_leg(torch, keys_np, C=96, reps=20):
-    """The dominant kernel of the config-4 run: the output-stationary fp16
-    layer at full resolution (200k indoor voxels, k=3, 96 -> 96 channels),
-    kernel only."""
+def family_leg(torch, indoor_np, key, reps=20):
+    """The dominant family's layer shape alone (random features and weights
+    on the config-4 map of its stride), kernel-only back-to-back launches:
+    the launch the rocprofv3 counter runs read."""
     from spira_amd.nn import functional as F
     from spira_amd.nn.functional import _native
     dev = torch.device("cuda:0")
-    keys = torch.from_numpy(keys_np).to(dev)
-    m = F.build_kmap(keys, keys, 3, 1, 0)
-    S = T = keys.shape[0]
-    P = int((m[2][:T] >= 0).sum().item())
-    X = torch.randn(S, C, device=dev, dtype=torch.float16)
-    W = (torch.randn(27, C, C, device=dev) / np.sqrt(27 * C)).half()
-    ms = _native._C.time_conv_os(S, T, m[2], X, W, reps)
-    flops = 2.0 * P * C * C
-    # algorithmic bytes: fp16 features read and written once, fp16 weights,
-    # the int32 map read once
-    nbytes = 2.0 * (S * C + T * C) + 2.0 * 27 * C * C + 4.0 * 27 * T
-    return {"ms": ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12, "pairs": P, "C": C,
-            "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
+    stride, cin, cout, K = key
+    k = round(K ** (1 / 3))
+    keys, _ = F.flat_sort(torch.from_numpy(indoor_np).to(dev), True)
+    ks = keys if stride == 1 else F.downsample(keys, (stride,) * 3)
+    m = F.build_kmap(ks, ks, k, stride, 0)
+    X = torch.randn(ks.shape[0], cin, device=dev).half()
+    W = (torch.randn(K, cin, cout, device=dev) / np.sqrt(K * cin)).half()
+    ms = _native._C.time_conv_os(ks.shape[0], ks.shape[0], m[2], X, W, reps)
+    return {"kernel_ms": ms, "T": int(ks.shape[0])}
 
 
 def calib_leg(torch, mib=256, reps=5):
@@ -202,14 +399,9 @@ def calib_leg(torch, mib=256, reps=5):
     return {"bytes_each_way": mib * (1 << 20), "reps": reps}
 
 
-# ---------------------------------------------------------------------------
-# CPU baseline: the same end-to-end pipeline on the host through the oracle
-# ---------------------------------------------------------------------------
-def cpu_e2e(model, coords_np, feats_np):
-    """The same network end to end on the host through the oracle (fp32,
-    OpenMP C restatement of the maps and convolutions)."""
-    from oracle.network import network_forward
-    return network_forward(model, coords_np, feats_np)
+def rel_err(got, ref):
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2))) or 1.0
+    return float(np.max(np.abs(got.astype(np.float64) - ref))) / rms
 
 
 def main():
@@ -220,82 +412,116 @@ def main():
         sys.exit(2)
     import torch
     from spira_amd import scenes
+    from spira_amd.nn import functional as F
 
     legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer", "config5"}
     with open(os.path.join(ROOT, "BASELINE.json")) as f:
         baseline = json.load(f)
+    dev = torch.device("cuda:0")
 
     indoor = scenes.indoor()
     res = {"metric": baseline["metric"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
            "data": "synthetic (seeded scenes, random-init weights)"}
     cfg = {"workload": "config4: SparseResUNet42 fp16, 200k-voxel indoor scene, end-to-end "
-                       "(order + network-wide kernel maps + forward)",
-           "voxels": int(indoor.shape[0]), "key_bits": 64, "map_dataflow": args.dataflow}
-    model = None
-    if "e2e" in legs:
-        ms, wall, model, _ = e2e_leg(torch, args, indoor)
+                       "(order + network-wide kernel maps + forward; selector run before timing)",
+           "voxels": int(indoor.shape[0]), "key_bits": 64}
+    cpu = {}
+    e2e = None
+    if "e2e" in legs or "family" in legs:
+        e2e = E2E(torch, args, indoor, "UNet")
+        if not args.no_tune:
+            res["untuned_ms_per_step"], _, _ = e2e.time(min(args.steps, 10), min(args.warmup, 5))
+            e2e.tune()
+        ms, wall, gpu_out = e2e.time(args.steps, args.warmup)
         res["value"] = ms
         res["ms_per_step"] = ms
         res["wall_ms_per_step"] = wall
+        cfg["map_dataflows"] = e2e.dataflows
+        if e2e.chosen:
+            cfg["row_orders"] = e2e.chosen["row_orders"]
+        rows = per_layer_profile(torch, e2e)
+        rl, fams, fkey = family_roofline(rows)
+        res["roofline"] = rl
+        res["families"] = fams[:6]
+        cfg["levels"] = {f"s{r['stride'][0]}": {"T": r["T"], "P_over_T": round(r["P"] / r["T"], 2)}
+                         for r in rows if r["K"] == 27 and not r["transposed"]}
+        if args.layer_table:
+            write_layer_table(args.layer_table, rows, ms)
+        if "family" in legs:
+            res["family_kernel"] = family_leg(torch, indoor, fkey)
+        if not args.no_cpu:
+            # the same network, weights and input features through the oracle
+            # (fp32) on the host cores, timed; outputs checked against the GPU's
+            from oracle import oracle as orc
+            from oracle.network import network_forward
+            feats = e2e.feats.float().cpu().numpy()
+            t0 = time.perf_counter()
+            ref = network_forward(e2e.model, indoor, feats)
+            cpu_ms = (time.perf_counter() - t0) * 1e3
+            errs = [rel_err(g.float().cpu().numpy(), rf) for g, (rf, _) in zip(gpu_out, ref)]
+            res["cpu_baseline"] = {"value": cpu_ms, "unit": "ms", "cores": orc.threads(), "kind": "port",
+                                   "sample": "one full config-4 step (sort, downsample, all maps, all 42 layers, "
+                                             "fp32) by the OpenMP oracle, on the GPU run's weights and inputs",
+                                   "max_err_vs_gpu_x_rms": max(errs), "levels_compared": len(errs)}
     if "config5" in legs:
         # config 5: the large-kernel (k = 5) SparseResNetLarge on the ~300k-voxel
         # scene of merged LiDAR rings and Gaussian blobs, timed like config 4
         blobs = scenes.lidar_blobs()
-        c5, _, _, _ = e2e_leg(torch, args, blobs, net="ResNetLarge", steps=10, warmup=5)
-        res["config5_ms"] = c5
+        c5 = E2E(torch, args, blobs, "ResNetLarge")
+        if not args.no_tune:
+            res["config5_untuned_ms"], _, _ = c5.time(5, 3)
+            c5.tune()
+        res["config5_ms"], _, _ = c5.time(10, 5)
         cfg["config5_voxels"] = int(blobs.shape[0])
-    lidar = scenes.lidar()
-    from oracle import oracle as orc
-    lkeys, _ = orc.flatten_sort(lidar, True)
+        del c5
+    if "kmap" in legs or "layer" in legs:
+        lidar = scenes.lidar()
+        lkeys, _ = F.flat_sort(torch.from_numpy(lidar).to(dev), True)
+        cfg["kmap_voxels"] = int(lkeys.shape[0])
     if "kmap" in legs:
         km = kmap_leg(torch, lkeys)
-        res["kmap_build_us"] = km[3]["us"]
-        res["kmap_build_us_k5"] = km[5]["us"]
-        res["kmap_kernel_us"] = km[3]["kernel_us"]
-        res["kmap_kernel_us_k5"] = km[5]["kernel_us"]
-        res["kmap_roofline"] = {"bound": "hbm", "achieved": km[3]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                "frac": km[3]["gbs"] / HBM_PEAK_GBS, "traffic": None,
-                                "kernel": "kmap_search_kernel<u64,3> (config 2, k=3, OS layout)",
-                                "algorithmic_bytes": km[3]["bytes"]}
-        res["kmap_roofline_k5"] = {"achieved": km[5]["gbs"], "frac": km[5]["gbs"] / HBM_PEAK_GBS,
-                                   "algorithmic_bytes": km[5]["bytes"]}
-        cfg["kmap_voxels"] = int(lkeys.shape[0])
+        res["kmap"] = km
+        res["kmap_build_us"] = km["k3s1"]["api_us"]
+        res["kmap_kernel_us"] = km["k3s1"]["kernel_us"]
+        res["kmap_roofline"] = {"bound": "hbm", "achieved": km["k3s1"]["gbs"], "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": km["k3s1"]["frac"], "traffic": None,
+                                "kernel": "kmap_search_kernel<u64,3,3,0> (config 2, k=3, stride 1, OS layout)",
+                                "algorithmic_bytes": km["k3s1"]["algorithmic_bytes"]}
+        if not args.no_cpu:
+            from oracle import oracle as orc
+            kn = lkeys.cpu().numpy()
+            t0 = time.perf_counter()
+            ref = orc.search(kn, kn, (3, 3, 3), (1, 1, 1), orc.OS)
+            cpu_ms = (time.perf_counter() - t0) * 1e3
+            got = F.build_kmap(lkeys, lkeys, 3, 1, 0)[2].cpu().numpy()
+            cpu["kmap_k3s1"] = {"value": cpu_ms * 1e3, "unit": "us", "cores": orc.threads(), "kind": "port",
+                                "sample": "the config-2 k=3 stride-1 map (output-stationary layout)",
+                                "bit_exact_vs_gpu": bool(np.array_equal(got, ref))}
     if "layer" in legs:
         ly = layer_leg(torch, lkeys)
-        res["layer_ms"] = ly["per_C"][64]["ms"]
-        res["layer_sweep"] = {str(c): {"ms": v["ms"], "tflops": v["tflops"],
-                                       "frac": v["tflops"] / MFMA_F16_PEAK_TFLOPS}
-                              for c, v in ly["per_C"].items()}
-        res["layer_pairs"] = ly["pairs"]
-        ikeys, _ = orc.flatten_sort(indoor, True)
-        dm = dominant_leg(torch, ikeys)
-        # the binding roofline: the larger of bytes / HBM peak and flops /
-        # MFMA peak
-        hbm_bound = dm["bytes"] / (HBM_PEAK_GBS * 1e9) >= dm["flops"] / (MFMA_F16_PEAK_TFLOPS * 1e12)
-        if hbm_bound:
-            rl = {"bound": "hbm", "achieved": dm["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                  "frac": dm["gbs"] / HBM_PEAK_GBS}
-        else:
-            rl = {"bound": "mfma", "achieved": dm["tflops"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                  "frac": dm["tflops"] / MFMA_F16_PEAK_TFLOPS}
-        res["roofline"] = {**rl, "mfma_tflops": dm["tflops"], "mfma_frac": dm["tflops"] / MFMA_F16_PEAK_TFLOPS,
-                           "algorithmic_bytes": dm["bytes"],
-                           "traffic": DOMINANT_TRAFFIC_BYTES,
-                           "traffic_gbs": DOMINANT_TRAFFIC_BYTES / (dm["ms"] * 1e-3) / 1e9,
-                           "kernel": "os_kernel<3,0,true,8,false,1> (config 4 full resolution, 200k voxels, k=3, 96->96, "
-                                     "fp16, 128-channel steps)",
-                           "ms": dm["ms"], "algorithmic_flops": dm["flops"], "valid_pairs": dm["pairs"]}
+        res["layers"] = ly
+        res["layer_ms"] = ly["per_C"]["64"]["selector_ms"]
+        if not args.no_cpu:
+            from oracle import oracle as orc
+            C = 64
+            kn = lkeys.cpu().numpy()
+            omap = orc.search(kn, kn, (3, 3, 3), (1, 1, 1), orc.OS)
+            g = torch.Generator().manual_seed(C)
+            X = torch.randn(kn.shape[0], C, generator=g).half()
+            W = (torch.randn(27, C, C, generator=g) / np.sqrt(27 * C)).half()
+            t0 = time.perf_counter()
+            ref = orc.conv_os_f32(omap, kn.shape[0], X.float().numpy(), W.float().numpy())
+            cpu_ms = (time.perf_counter() - t0) * 1e3
+            got = F.sparse_convolution_forward_os(kn.shape[0], kn.shape[0], torch.from_numpy(omap).to(dev),
+                                                  X.to(dev), W.to(dev)).float().cpu().numpy()
+            cpu["layer_c64"] = {"value": cpu_ms, "unit": "ms", "cores": orc.threads(), "kind": "port",
+                                "sample": "one config-3 C=64 layer (fp32 sums)", "max_err_vs_gpu_x_rms":
+                                rel_err(got, ref)}
+    if cpu:
+        res["cpu_baselines"] = cpu
     if "calib" in legs:
         res["calib"] = calib_leg(torch)
-    if not args.no_cpu and model is not None:
-        feats = np.random.default_rng(0).standard_normal((indoor.shape[0], 3)).astype(np.float32)
-        t0 = time.perf_counter()
-        cpu_e2e(model, indoor, feats)
-        cpu_ms = (time.perf_counter() - t0) * 1e3
-        res["cpu_baseline"] = {"value": cpu_ms, "unit": "ms", "cores": orc.threads(), "kind": "port",
-                               "sample": "one full config-4 scene end-to-end (sort, downsample, all maps, "
-                                         "all 42 layers, fp32) by the OpenMP oracle"}
     res["config"] = cfg
     print(json.dumps(res))
 

@@ -92,6 +92,24 @@ int spira_hip_downsample_execute(const void *keys, int64_t n, int key_bits, int 
                                  const spira_hip_downsample_plan_t *plan, void *out_keys, uint32_t *d_count,
                                  void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Workspace bytes for spira_hip_downsample_chain. */
+int spira_hip_downsample_chain_workspace(int64_t n, int key_bits, size_t *bytes);
+
+/* Downsample one key set to a chain of strides without reading anything back:
+ * level l (strides[3l .. 3l+2]) is sorted unique (keys & stride mask), written
+ * to out_keys[l] (capacity n each), its count to d_counts[l] (device).  Each
+ * stride must be a power of two and a multiple of the previous level's (the
+ * first of 1), with (x ratio) * (y ratio) at most 16.  The keys must be sorted ascending (as
+ * flatten_sort leaves them); *d_unsorted (device, zeroed by the caller) is
+ * set to 1 when they are not, in which case the outputs are undefined and
+ * the caller takes spira_hip_downsample per stride instead.  Same results as
+ * spira_hip_downsample per stride.  (reference: cuda_streamed_output_generate,
+ * torch/cuda_arg_sort_coordinates.cu:107-200, which masks, sorts and uniques
+ * the full key set once per stride.) */
+int spira_hip_downsample_chain(const void *keys, int64_t n, int key_bits, int levels, const int32_t *strides,
+                               void *const *out_keys, uint32_t *d_counts, uint32_t *d_unsorted, void *workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+
 /* ----------------------------------------------------------- kernel maps */
 
 #define SPIRA_KMAP_OS 0     /* [Tp, K] int32, column iz*O + o (z-major)            */
@@ -208,13 +226,41 @@ int spira_hip_prepared_weights_bytes(int num_offsets, int c_in, int c_out, int d
 int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, int c_out, int dtype, void *prepared,
                               hipStream_t stream);
 
+/* Launch choices of the fp16 output-stationary kernel (spira_hip_conv_os);
+ * a field left 0 is the library's own choice, so a zeroed struct (or a null
+ * pointer) is the default schedule.  They change the schedule, never the
+ * result:
+ *   col_tile       output channels per column tile: 32, 64, 96 or 128;
+ *   step_channels  input channels per pipeline step: 32, 64 or 128;
+ *   offset_splits  blocks a row tile's kernel offsets are split over (fp32
+ *                  partial sums in the workspace + a finalize pass);
+ *   offset_pack    kernel offsets per step for 16-, 32- and 64-channel
+ *                  inputs of kernels above 27 offsets: 1 (none), 2 or 4.
+ * (No reference counterpart: these are the selector's CDNA4 parameters; the
+ * reference selector sweeps gather / scatter tile sizes instead,
+ * source/spira/nn/conv.py:217-307.) */
+typedef struct {
+  int col_tile;
+  int step_channels;
+  int offset_splits;
+  int offset_pack;
+} spira_hip_os_tuning_t;
+
 /* Workspace bytes of spira_hip_conv_os: an fp32 [num_targets, c_out]
  * partial-sum buffer when a small layer (fewer row blocks than CUs) splits
  * its offsets over blocks.  The workspace must be zero-filled before its
  * first use; every call leaves it zero-filled, so a caller keeps one buffer
  * per stream (calls that overlap on one buffer race). */
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
-                                size_t *bytes);
+                                const spira_hip_os_tuning_t *tuning, size_t *bytes);
+
+/* The launch spira_hip_conv_os would make for a layer (c_in2 > 0: the
+ * concatenated form; has_map 0: the identity map) under `tuning`: plan[0..5]
+ * = column tile (output channels), step channels, offset splits, kernel
+ * offsets per step, grid x, grid y.  Runs on the host only.  (No reference
+ * counterpart: it lets a caller or a test see what a tuning changes.) */
+int spira_hip_conv_os_plan(int64_t num_targets, int num_offsets, int c_in, int c_in2, int c_out, int has_map,
+                           int out_mode, const spira_hip_os_tuning_t *tuning, int32_t *plan);
 
 /* Output-stationary implicit GEMM: targets[t] = sum_j sources[map[t, j]] @
  * weights[j] for map entries >= 0; map is [>= num_targets, num_offsets]
@@ -231,7 +277,8 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
  * that order (row i = target row_order[i]); group_masks (nullable, needs
  * num_offsets <= 128) are the 128-row valid-column unions of
  * spira_hip_kmap_row_order for the rows in that order, which let a block skip
- * offsets none of its rows uses.  Both change the schedule, not the result.
+ * offsets none of its rows uses.  Both change the schedule, not the result,
+ * as does `tuning` (nullable; the workspace size depends on it).
  * (reference: cuda_sparse_convolution_forward_os,
  * torch/cuda_sparse_convolution_forward.cu:448-496; SparseConvolutionForward_OS
  * cuda/functions/sparse_convolution.cu:1354-1393; kernels
@@ -242,7 +289,8 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
                       const uint64_t *group_masks, const void *sources,
                       int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
                       void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
-                      int relu, void *workspace, size_t workspace_bytes, hipStream_t stream);
+                      int relu, const spira_hip_os_tuning_t *tuning, void *workspace, size_t workspace_bytes,
+                      hipStream_t stream);
 
 /* spira_hip_conv_os over the channel concatenation [sources | sources2] of two
  * fp16 feature arrays ([num_sources, c_in] and [num_sources, c_in2]; c_in a
@@ -256,8 +304,8 @@ int spira_hip_conv_os_concat(int64_t num_targets, int num_offsets, const int32_t
                              const int32_t *row_order, const uint64_t *group_masks, const void *sources,
                              const void *sources2, int64_t num_sources, int c_in, int c_in2, const void *prepared,
                              int c_out, void *targets, int out_mode, const float *scale, const float *shift,
-                             const void *residual, int relu, void *workspace, size_t workspace_bytes,
-                             hipStream_t stream);
+                             const void *residual, int relu, const spira_hip_os_tuning_t *tuning, void *workspace,
+                             size_t workspace_bytes, hipStream_t stream);
 
 /* Fused weight-stationary pass over a compacted pair list: for compacted row r
  * (pairs naddrs[r]..naddrs[r+1] of in_idx/out_idx) target_acc[out] +=

@@ -24,7 +24,7 @@ Stride = Tuple[int, int, int]
 
 
 def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray,
-                    dataflow: int = 0) -> List[Tuple[np.ndarray, Stride]]:
+                    dataflow="layer") -> List[Tuple[np.ndarray, Stride]]:
     """Outputs of ``model`` (SparseResUNet42-style: ``stem`` / ``encoders`` /
     ``decoders``; or a SparseResNet-style ModuleList of stages) as
     (features in sorted-key order, tensor stride) pairs, like the GPU
@@ -38,13 +38,15 @@ def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray,
     their half map (sparse_convolution.cu:1002-1124).  Dataflows 1 and 2 use
     canonical weight rows.  The half maps differ from the full map where the
     reference's z walk wraps (voxels at x = y = 0), so each dataflow is
-    evaluated with its own maps."""
+    evaluated with its own maps.  ``"layer"`` (the default): each layer's own
+    ``_tunable_config["map_dataflow"]`` (0, 1 or 2; what the selector chose
+    for its group)."""
     import torch
     from spira_amd import nn as spnn
     from spira_amd.networks import SparseResBlock
 
-    if dataflow not in (0, 1, 2):
-        raise ValueError(f"dataflow must be 0, 1 or 2, not {dataflow}")
+    if dataflow not in (0, 1, 2, "layer"):
+        raise ValueError(f"dataflow must be 0, 1, 2 or 'layer', not {dataflow}")
     keys, perm = orc.flatten_sort(coords_np, True)
     x = np.ascontiguousarray(feats_np[perm], dtype=np.float32)
     vox: Dict[Stride, np.ndarray] = {(1, 1, 1): keys}
@@ -57,6 +59,9 @@ def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray,
 
     def conv(layer, feats, stride):
         W = layer.kernel.detach().float().cpu().numpy()
+        d = layer._tunable_config["map_dataflow"] if dataflow == "layer" else dataflow
+        if d not in (0, 1, 2) or layer._tunable_config.get("force_os", False):
+            raise ValueError(f"the oracle network evaluates dataflows 0, 1 and 2 without force_os, not {d}")
         if layer.is_trivial:
             return feats @ W[0], stride
         if layer.transposed:
@@ -65,14 +70,15 @@ def network_forward(model, coords_np: np.ndarray, feats_np: np.ndarray,
         else:
             out_stride = tuple(a * b for a, b in zip(stride, layer.stride))
             key = (stride, out_stride, layer.kernel_size)
+        key = key + (d,)
         if key not in maps:
-            maps[key] = orc.build_kmap(coords_of(key[0]), coords_of(key[1]), layer.kernel_size, key[0], dataflow)
+            maps[key] = orc.build_kmap(coords_of(key[0]), coords_of(key[1]), layer.kernel_size, key[0], d)
         m = maps[key]
         S, T = (m[1], m[0]) if layer.transposed else (m[0], m[1])
-        if dataflow == 0:
+        if d == 0:
             omap = orc.convert_transposed_os(m[2], m[0]) if layer.transposed else m[2]
             return orc.conv_os_f32(omap, T, feats, W), out_stride
-        if dataflow == 1:
+        if d == 1:
             y = orc.conv_ws_merged(S, T, feats, W, m[5], m[3], transpose=layer.transposed)
         else:
             sm, tm = (m[4], m[3]) if layer.transposed else (m[3], m[4])

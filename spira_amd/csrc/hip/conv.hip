@@ -1182,24 +1182,16 @@ static inline int bm_for(int wn) {
 
 // offsets per split: small layers split their offsets so that the grid
 // covers the chip; a split never exceeds 128 offsets (the block's 128-bit
-// active-offset set)
-static int choose_jper(int64_t blocks_xy, int Kc, int cus) {
+// active-offset set).  splits > 0: that many splits, as asked.
+static int choose_jper(int64_t blocks_xy, int Kc, int cus, int splits = 0) {
   int jper = Kc;
-  static const int mult = [] {
-    const char *e = std::getenv("SPIRA_OS_JPER_WANT");
-    return e && *e ? std::atoi(e) : 1;
-  }();
-  const int64_t want = static_cast<int64_t>(cus) * mult;
-  if (blocks_xy < want && Kc > 1) {
-    const int64_t splits = std::min<int64_t>(Kc, div_up(want, blocks_xy));
-    jper = static_cast<int>(div_up(Kc, splits));
+  if (splits > 0) {
+    jper = static_cast<int>(div_up(Kc, std::min(splits, Kc)));
+  } else if (blocks_xy < cus && Kc > 1) {
+    const int64_t n = std::min<int64_t>(Kc, div_up(cus, blocks_xy));
+    jper = static_cast<int>(div_up(Kc, n));
   }
   return std::min(jper, 128);
-}
-
-static int env_int(const char *name, int dflt) {
-  const char *v = std::getenv(name);
-  return v && *v ? std::atoi(v) : dflt;
 }
 
 // Operands of the MMA core; byte sizes must fit the 31-bit buffer offsets
@@ -1254,56 +1246,117 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
 // larger grids.  (Measured on the config-4 layers: 96 -> 96 at 200k voxels
 // 52.3 -> 46.6 us, 256 -> 256 at stride 8 111.6 -> 101.7 us; 128 -> 128 at
 // stride 4, 529 blocks of the widest tile, 79.7 -> 92.7 us, so it keeps
-// 64-channel steps.)  SPIRA_OS_KC=32 / 64 / 128 overrides (measurements).
-static int os_nks(int CinP, int wn, int64_t blocks, int cus) {
-  static const int kc = env_int("SPIRA_OS_KC", 0);
-  if (kc == 32) return 2;
-  if (kc == 64) return CinP >= 64 ? 4 : 2;
-  if (kc == 128) return CinP >= 96 ? 8 : (CinP >= 64 ? 4 : 2);
+// 64-channel steps.)  A tuning's step_channels (32, 64, 128) overrides.
+static int os_nks(int CinP, int wn, int64_t blocks, int cus, int step_channels) {
+  if (step_channels == 32) return 2;
+  if (step_channels == 64) return CinP >= 64 ? 4 : 2;
+  if (step_channels == 128) return CinP >= 96 ? 8 : (CinP >= 64 ? 4 : 2);
   if ((CinP == 96 || CinP % 128 == 0) && CinP >= 96 && (wn <= 3 || 2 * blocks <= 3 * static_cast<int64_t>(cus)))
     return 8;
   return CinP >= 64 ? 4 : 2;
 }
 
-template <int MODE>
-static void launch_os_any(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
-                          const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
-                          void *Y, const Epilogue &epi) {
-  const int nks = os_nks(op.CinP, wn, static_cast<int64_t>(grid.x) * grid.y * grid.z, device_cu_count());
-  const bool cat = op.X2 != nullptr;
+// Column-tile width of the output-stationary kernel: the widest tile, made
+// narrower once (more column blocks, each re-gathering its rows) when the
+// grid has fewer than SPIRA_OS_MIN_BLOCKS (default 1) blocks per CU; a grid
+// still short of the CUs then splits its offsets (choose_jper).  (Measured
+// on the config-4 layers: s8 128 -> 128, 134 row blocks, is fastest with
+// one halving (42.9 us, 46.7 us without); s16 256 -> 256, 32 row blocks,
+// took 53.0 us narrowed down to 32-column tiles against 34.8 us without,
+// as every narrowing multiplies the gathered rows.  More than one block per
+// CU this way, or by more offset splits, costs more in re-gathered rows /
+// atomics than the added occupancy returns.)
+static int os_wn(int64_t num_targets, int c_out, int cus, int col_tile) {
+  if (col_tile == 32 || col_tile == 64 || col_tile == 96 || col_tile == 128) return col_tile / 32;
+  int wn = wn_for(c_out);
+  const int64_t bx = div_up(num_targets, bm_for(1));
+  if (wn > 1 && bx * div_up(pad_out(c_out), 32 * wn) < cus) wn = wn == 3 ? 1 : wn / 2;
+  return wn;
+}
+
+static spira_hip_os_tuning_t tuning_of(const spira_hip_os_tuning_t *t) {
+  spira_hip_os_tuning_t r{};
+  if (t) r = *t;
+  return r;
+}
+
+static int check_tuning(const spira_hip_os_tuning_t &t) {
+  SPIRA_HIP_REQUIRE(t.col_tile == 0 || t.col_tile == 32 || t.col_tile == 64 || t.col_tile == 96 || t.col_tile == 128,
+                    "conv_os tuning: col_tile must be 0, 32, 64, 96 or 128");
+  SPIRA_HIP_REQUIRE(t.step_channels == 0 || t.step_channels == 32 || t.step_channels == 64 ||
+                        t.step_channels == 128,
+                    "conv_os tuning: step_channels must be 0, 32, 64 or 128");
+  SPIRA_HIP_REQUIRE(t.offset_splits >= 0 && t.offset_splits <= 128, "conv_os tuning: offset_splits must be 0..128");
+  SPIRA_HIP_REQUIRE(t.offset_pack == 0 || t.offset_pack == 1 || t.offset_pack == 2 || t.offset_pack == 4,
+                    "conv_os tuning: offset_pack must be 0, 1, 2 or 4");
+  return kOk;
+}
+
+// The launch of one output-stationary call: column tile (wn), rows per
+// block, offsets per split (jper), 16-channel slices per step (nks), kernel
+// offsets per step (pack: 1, 2 or 4) and the grid.
+struct OsPlan {
+  int wn, bm, jper, splits, nks, pack;
+  bool aligned;
+  int64_t gx, gy;
+};
+
+static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, bool has_map, bool native_store,
+                      const spira_hip_os_tuning_t &tn) {
+  OsPlan pl{};
+  const int cus = device_cu_count();
+  pl.wn = os_wn(T, Cout, cus, tn.col_tile);
+  pl.bm = bm_for(pl.wn);
+  pl.gx = div_up(T, pl.bm);
+  pl.gy = div_up(pad_out(Cout), 32 * pl.wn);
+  // small layers (fewer blocks than CUs) split their offsets over grid z
+  pl.jper = choose_jper(pl.gx * pl.gy, Kc, cus, tn.offset_splits);
+  pl.splits = static_cast<int>(div_up(Kc, pl.jper));
+  pl.aligned = Cin % 8 == 0;
+  pl.nks = pl.aligned ? os_nks(CinP, pl.wn, pl.gx * pl.gy * pl.splits, cus, tn.step_channels) : 2;
+  pl.pack = 1;
   // offset packing: 16- and 32-channel inputs of kernels with more than 27
   // offsets (map entries fetched per step) run four offsets per step (64-
   // or 128-channel steps) instead of a step per offset.  (Measured, kernel
   // only, 300k voxels, 125 offsets: 16 -> 16 262 -> 182 us, 32 -> 32 273 ->
   // 213 us, 32 -> 64 299 -> 256 us; with 27 offsets (map tile in LDS) it was
-  // slower: 17.5 -> 18.3-20.9 us at 200k voxels.)  SPIRA_OS_PACK=0 switches
-  // it off, =2 packs pairs of offsets (measurements).
-  static const int pack = env_int("SPIRA_OS_PACK", 4);
+  // slower: 17.5 -> 18.3-20.9 us at 200k voxels.)  64-channel inputs: two
+  // offsets per 128-channel step when the column tile is at most 64 wide
+  // (64 -> 64 at 125 offsets 420 -> 390 us; 64 -> 128 594 -> 601 us, so
+  // wider tiles keep one offset per step).  A tuning's offset_pack 1
+  // switches it off, 2 packs pairs of 16- or 32-channel offsets.
+  const int want = tn.offset_pack == 0 ? 4 : tn.offset_pack;
+  const bool packable = native_store && has_map && !cat && pl.aligned && pl.splits == 1 && Kc > ring::kMapTileK;
+  if (packable && want > 1 && (CinP == 16 || CinP == 32)) {
+    pl.pack = want;
+    pl.nks = want == 2 ? CinP / 8 : CinP / 4;  // KC = pack * CinP
+  } else if (packable && want > 1 && CinP == 64 && pl.wn <= 2) {
+    pl.pack = 2;
+    pl.nks = 8;
+  }
+  return pl;
+}
+
+template <int MODE>
+static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
+                          const uint64_t *rowmask, int64_t T, int Kc, const Operands &op, void *Y,
+                          const Epilogue &epi) {
+  const int wn = pl.wn, jper = pl.jper, nks = pl.nks;
+  const bool cat = op.X2 != nullptr;
   if constexpr (MODE == kStoreNative) {
-    if (pack && map && !cat && op.Cin % 8 == 0 && (op.CinP == 16 || op.CinP == 32) && jper >= Kc &&
-        Kc > ring::kMapTileK) {
-      if (pack == 2) {
-        if (op.CinP == 16) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-        else launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      } else if (op.CinP == 16) {
-        launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      } else {
-        launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      }
+    if (pl.pack == 4) {
+      if (nks == 4) launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      else launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
       return;
     }
-    // 64-channel inputs: two offsets per 128-channel step when the column
-    // tile is at most 64 wide (300k voxels, 125 offsets: 64 -> 64 420 ->
-    // 390 us; 64 -> 128 594 -> 601 us, so wider tiles keep one offset per
-    // step).  SPIRA_OS_PACK64=0 switches it off (measurements).
-    static const int pack64 = env_int("SPIRA_OS_PACK64", 1);
-    if (pack && pack64 && map && !cat && op.Cin % 8 == 0 && op.CinP == 64 && jper >= Kc && Kc > ring::kMapTileK &&
-        wn <= 2) {
-      launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+    if (pl.pack == 2) {
+      if (nks == 2) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      else if (nks == 4) launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      else launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
       return;
     }
   }
-  if (op.Cin % 8 != 0) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  if (!pl.aligned) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
   else if (cat) {
     // channel concatenations: storage-dtype outputs (split or not)
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
@@ -1396,34 +1449,34 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
   return kOk;
 }
 
-// Column-tile width of the output-stationary kernel: the widest tile, made
-// narrower once (more column blocks, each re-gathering its rows) when the
-// grid has fewer than SPIRA_OS_MIN_BLOCKS (default 1) blocks per CU; a grid
-// still short of the CUs then splits its offsets (choose_jper).  (Measured
-// on the config-4 layers: s8 128 -> 128, 134 row blocks, is fastest with
-// one halving (42.9 us, 46.7 us without); s16 256 -> 256, 32 row blocks,
-// took 53.0 us narrowed down to 32-column tiles against 34.8 us without,
-// as every narrowing multiplies the gathered rows.  More than one block per
-// CU this way, or by more offset splits, costs more in re-gathered rows /
-// atomics than the added occupancy returns.)
-static int os_wn(int64_t num_targets, int c_out, int cus) {
-  static const int mult = env_int("SPIRA_OS_MIN_BLOCKS", 1);
-  int wn = wn_for(c_out);
-  const int64_t bx = div_up(num_targets, bm_for(1));
-  if (wn > 1 && bx * div_up(pad_out(c_out), 32 * wn) < static_cast<int64_t>(mult) * cus) wn = wn == 3 ? 1 : wn / 2;
-  return wn;
-}
-
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,
-                                size_t *bytes) {
+                                const spira_hip_os_tuning_t *tuning, size_t *bytes) {
   (void)c_in;
   *bytes = 0;
+  const spira_hip_os_tuning_t tn = tuning_of(tuning);
+  if (int rc = check_tuning(tn)) return rc;
   if (!mfma_path(dtype) || out_mode != SPIRA_OUT_STORE || num_targets <= 0) return kOk;
-  const int wn = os_wn(num_targets, c_out, device_cu_count());
-  const int bm = bm_for(wn);
-  const int64_t blocks = div_up(num_targets, bm) * div_up(pad_out(c_out), 32 * wn);
-  if (choose_jper(blocks, num_offsets, device_cu_count()) < num_offsets)
+  const OsPlan pl = plan_os(num_targets, num_offsets, c_in, pad_in(c_in), false, c_out, true, true, tn);
+  if (pl.splits > 1)
     *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
+  return kOk;
+}
+
+int spira_hip_conv_os_plan(int64_t num_targets, int num_offsets, int c_in, int c_in2, int c_out, int has_map,
+                           int out_mode, const spira_hip_os_tuning_t *tuning, int32_t *plan) {
+  const spira_hip_os_tuning_t tn = tuning_of(tuning);
+  if (int rc = check_tuning(tn)) return rc;
+  SPIRA_HIP_REQUIRE(plan != nullptr && num_targets > 0 && num_offsets > 0 && c_in > 0 && c_out > 0,
+                    "conv_os_plan: empty layer or no output array");
+  const int cin_all = c_in + c_in2;
+  const OsPlan pl = plan_os(num_targets, num_offsets, cin_all, pad_in(cin_all), c_in2 > 0, c_out, has_map != 0,
+                            out_mode == SPIRA_OUT_STORE, tn);
+  plan[0] = pl.wn * 32;
+  plan[1] = pl.nks * 16;
+  plan[2] = pl.splits;
+  plan[3] = pl.pack;
+  plan[4] = static_cast<int32_t>(pl.gx);
+  plan[5] = static_cast<int32_t>(pl.gy);
   return kOk;
 }
 
@@ -1436,8 +1489,11 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
                         const uint64_t *group_masks, const void *sources, const void *sources2, int64_t num_sources,
                         int c_in, int c_in2, const void *weights, const void *prepared, int c_out, int dtype,
                         void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
-                        int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                        int relu, const spira_hip_os_tuning_t *tuning, void *workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   SPIRA_HIP_REQUIRE(dtype == SPIRA_F16 || dtype == SPIRA_F32, "conv_os: dtype must be fp16 or fp32");
+  const spira_hip_os_tuning_t tn = tuning_of(tuning);
+  if (int rc = check_tuning(tn)) return rc;
   SPIRA_HIP_REQUIRE(c_in2 == 0 || (sources2 && dtype == SPIRA_F16 && c_in % 32 == 0 && c_in2 % 8 == 0),
                     "conv_os_concat: fp16 only, the first part's channels a multiple of 32, the second's of 8");
   SPIRA_HIP_REQUIRE(out_mode >= SPIRA_OUT_STORE && out_mode <= SPIRA_OUT_ADD_F32, "conv_os: bad out_mode");
@@ -1452,14 +1508,12 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
   const Epilogue epi = make_epi(scale, shift, residual, relu);
   if (mfma_path(dtype)) {
     SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
-    const int CoutP = pad_out(c_out);
-    const int wn = os_wn(num_targets, c_out, device_cu_count());
-    const int bm = bm_for(wn);
-    const int64_t bx = div_up(num_targets, bm), by = div_up(CoutP, 32 * wn);
-    // small layers (fewer blocks than CUs) split their offsets over grid z
-    const int jper = choose_jper(bx * by, num_offsets, device_cu_count());
-    const int splits = static_cast<int>(div_up(num_offsets, jper));
-    dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(by), static_cast<unsigned>(splits));
+    const int cin_all = c_in + c_in2;
+    const OsPlan pl = plan_os(num_targets, num_offsets, cin_all, pad_in(cin_all), c_in2 > 0, c_out,
+                              out_in_map != nullptr, out_mode == SPIRA_OUT_STORE, tn);
+    const int jper = pl.jper;
+    const int splits = pl.splits;
+    dim3 grid(static_cast<unsigned>(pl.gx), static_cast<unsigned>(pl.gy), static_cast<unsigned>(splits));
     SPIRA_HIP_REQUIRE(num_targets * num_offsets * 4 < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
     // (out_in_map may be null: the identity map, handled in the kernel)
     Operands op;
@@ -1467,11 +1521,11 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
     if (rc0) return rc0;
     if (splits == 1) {
       if (out_mode == SPIRA_OUT_STORE)
-        launch_os_any<kStoreNative>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kStoreNative>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op, targets, epi);
       else if (out_mode == SPIRA_OUT_STORE_F32)
-        launch_os_any<kStoreF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kStoreF32>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op, targets, epi);
       else
-        launch_os_any<kAddF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, targets, epi);
+        launch_os_any<kAddF32>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op, targets, epi);
     } else {
       float *acc = nullptr;
       if (out_mode == SPIRA_OUT_STORE) {
@@ -1486,7 +1540,7 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
         int rc = fill_f32(acc, num_targets * c_out, 0.f, stream);
         if (rc) return rc;
       }
-      launch_os_any<kAtomicF32>(wn, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, jper, op, acc, epi);
+      launch_os_any<kAtomicF32>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op, acc, epi);
       SPIRA_HIP_LAUNCH_CHECK();
       if (out_mode == SPIRA_OUT_STORE)
         hipLaunchKernelGGL(finalize_kernel<_Float16>, dim3(div_up(num_targets * c_out, 256)), dim3(256), 0, stream,
@@ -1513,22 +1567,23 @@ int spira_hip_conv_os(int64_t num_targets, int num_offsets, const int32_t *out_i
                       const uint64_t *group_masks, const void *sources,
                       int64_t num_sources, int c_in, const void *weights, const void *prepared, int c_out, int dtype,
                       void *targets, int out_mode, const float *scale, const float *shift, const void *residual,
-                      int relu, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                      int relu, const spira_hip_os_tuning_t *tuning, void *workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
   return conv_os_impl(num_targets, num_offsets, out_in_map, row_order, group_masks, sources, nullptr, num_sources,
                       c_in, 0, weights, prepared, c_out, dtype, targets, out_mode, scale, shift, residual, relu,
-                      workspace, workspace_bytes, stream);
+                      tuning, workspace, workspace_bytes, stream);
 }
 
 int spira_hip_conv_os_concat(int64_t num_targets, int num_offsets, const int32_t *out_in_map,
                              const int32_t *row_order, const uint64_t *group_masks, const void *sources,
                              const void *sources2, int64_t num_sources, int c_in, int c_in2, const void *prepared,
                              int c_out, void *targets, int out_mode, const float *scale, const float *shift,
-                             const void *residual, int relu, void *workspace, size_t workspace_bytes,
-                             hipStream_t stream) {
+                             const void *residual, int relu, const spira_hip_os_tuning_t *tuning, void *workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
   SPIRA_HIP_REQUIRE(sources2 != nullptr && c_in2 > 0, "conv_os_concat: needs a second source part");
   return conv_os_impl(num_targets, num_offsets, out_in_map, row_order, group_masks, sources, sources2, num_sources,
                       c_in, c_in2, nullptr, prepared, c_out, SPIRA_F16, targets, out_mode, scale, shift, residual,
-                      relu, workspace, workspace_bytes, stream);
+                      relu, tuning, workspace, workspace_bytes, stream);
 }
 
 int spira_hip_conv_ws_fused(int64_t num_sources, int64_t num_targets, const int32_t *in_idx, const int32_t *out_idx,

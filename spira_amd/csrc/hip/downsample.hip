@@ -534,6 +534,224 @@ static int downsample_impl(const CT *keys, int64_t n, int sx, int sy, int sz, CT
   return execute_impl<CT>(keys, n, sx, sy, sz, &h, out, d_count, ws, ws_bytes, s);
 }
 
+// ---------------------------------------------------------------------------
+// chained downsample: a sorted key set to a chain of nested strides, each
+// level computed from the previous level's output, with no host read.
+//
+// For stride b from a key set at stride a (b = a * r per axis, powers of two;
+// level 1 takes a = 1): the keys of one output run (equal masked x and y)
+// come from the r_x * r_y input rows (x0 + i a_x, y0 + j a_y), and inside one
+// row the masked keys are non-decreasing (the row is sorted by z and masking
+// z is monotone).  So the run's masked keys are a merge of r_x r_y sorted
+// rows: each key's place is the run's start (the number of keys of earlier
+// runs) plus its index in its own row plus, per other row of the run, the
+// number of that row's keys ordered before it (ties go to the earlier row);
+// all by binary searches over the sorted input.  Duplicates are then
+// adjacent: a flag + scan + compaction leaves the sorted unique keys.
+// ---------------------------------------------------------------------------
+constexpr int kChainMaxRows = 16;  // input rows per output run and level
+
+template <typename CT>
+__device__ __forceinline__ int64_t key_lower_bound(const CT *__restrict__ a, int64_t lo, int64_t hi, CT v) {
+  while (lo < hi) {
+    const int64_t m = (lo + hi) >> 1;
+    if (a[m] < v) lo = m + 1;
+    else hi = m;
+  }
+  return lo;
+}
+
+// first position in [lo, hi) whose masked key is >= v (UPPER: > v); the
+// masked keys of the range are non-decreasing
+template <typename CT, bool UPPER>
+__device__ __forceinline__ int64_t masked_bound(const CT *__restrict__ a, int64_t lo, int64_t hi, CT mask, CT v) {
+  while (lo < hi) {
+    const int64_t m = (lo + hi) >> 1;
+    const CT w = a[m] & mask;
+    if (UPPER ? (w <= v) : (w < v)) lo = m + 1;
+    else hi = m;
+  }
+  return lo;
+}
+
+// key of (x, y, 0); x or y past its field: one past every key of the
+// previous x (or of all keys)
+template <typename CT> __device__ __forceinline__ bool row_key(uint64_t x, uint64_t y, CT &k) {
+  if (y > Layout<CT>::YONES) {
+    ++x;
+    y = 0;
+  }
+  if (x > Layout<CT>::XONES) return false;
+  k = static_cast<CT>((static_cast<CT>(x) << Layout<CT>::XS) | (static_cast<CT>(y) << Layout<CT>::YS));
+  return true;
+}
+
+template <typename CT>
+__device__ __forceinline__ int64_t lb_row(const CT *__restrict__ in, int64_t lo, int64_t n, uint64_t x, uint64_t y) {
+  CT k;
+  return row_key<CT>(x, y, k) ? key_lower_bound(in, lo, n, k) : n;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_merge_kernel(const CT *__restrict__ in, const uint32_t *__restrict__ n_dev,
+                                                          int64_t n_cap, CT mask, uint32_t ax, uint32_t ay, int rx,
+                                                          int ry, CT *__restrict__ merged,
+                                                          uint32_t *__restrict__ unsorted) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  if (i >= n) return;
+  const CT key = in[i];
+  if (unsorted && i > 0 && in[i - 1] > key) atomicOr(unsorted, 1u);
+  const CT k = key & mask;
+  if (rx == 1 && ry == 1) {  // one row per run: the masked keys are in order already
+    merged[i] = k;
+    return;
+  }
+  const uint64_t x = static_cast<uint64_t>((key >> Layout<CT>::XS) & Layout<CT>::XONES);
+  const uint64_t y = static_cast<uint64_t>((key >> Layout<CT>::YS) & Layout<CT>::YONES);
+  const uint64_t x0 = x & ~(static_cast<uint64_t>(ax) * rx - 1);
+  const uint64_t y0 = y & ~(static_cast<uint64_t>(ay) * ry - 1);
+  const int own = static_cast<int>((x - x0) / ax) * ry + static_cast<int>((y - y0) / ay);
+  // rows of the run in key order: q = ix * ry + iy, [rs[q], re[q])
+  int64_t rs[kChainMaxRows], re[kChainMaxRows];
+  int64_t pos = lb_row<CT>(in, 0, n, x0, 0);  // keys of columns before x0
+  int64_t col = pos;
+  for (int ix = 0; ix < rx; ++ix) {
+    const uint64_t xi = x0 + static_cast<uint64_t>(ix) * ax;
+    const int64_t cs = ix == 0 ? col : lb_row<CT>(in, col, n, xi, 0);
+    int64_t b = lb_row<CT>(in, cs, n, xi, y0);
+    pos += b - cs;  // keys of column xi with y < y0 (earlier runs)
+    for (int iy = 0; iy < ry; ++iy) {
+      const int q = ix * ry + iy;
+      rs[q] = b;
+      b = lb_row<CT>(in, b, n, xi, y0 + static_cast<uint64_t>(iy + 1) * ay);
+      re[q] = b;
+    }
+    col = cs;
+  }
+  int64_t rank = pos + (i - rs[own]);
+  const int nrows = rx * ry;
+  for (int q = 0; q < nrows; ++q) {
+    if (q < own) rank += masked_bound<CT, true>(in, rs[q], re[q], mask, k) - rs[q];
+    else if (q > own) rank += masked_bound<CT, false>(in, rs[q], re[q], mask, k) - rs[q];
+  }
+  // A sorted input makes the ranks a permutation of [0, n); unsorted input
+  // (reported through `unsorted` at level 1) can push them out of range, and
+  // such a key is dropped rather than written out of bounds.
+  if (rank < 0 || rank >= n) {
+    if (unsorted) atomicOr(unsorted, 1u);
+    return;
+  }
+  merged[rank] = k;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_flag_kernel(const CT *__restrict__ merged, const uint32_t *__restrict__ n_dev,
+                                                         int64_t n_cap, uint32_t *__restrict__ flags) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p >= n_cap) return;
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  flags[p] = (p < n && (p == 0 || merged[p] != merged[p - 1])) ? 1u : 0u;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_compact_kernel(const CT *__restrict__ merged,
+                                                            const uint32_t *__restrict__ flags,
+                                                            const uint32_t *__restrict__ pos, int64_t n_cap,
+                                                            CT *__restrict__ out, uint32_t *__restrict__ count) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p >= n_cap) return;
+  if (flags[p]) out[pos[p]] = merged[p];
+  if (p == n_cap - 1) *count = pos[p] + flags[p];
+}
+
+static size_t chain_scan_bytes(int64_t n) {
+  size_t b = 0;
+  (void)rocprim::exclusive_scan(nullptr, b, static_cast<const uint32_t *>(nullptr), static_cast<uint32_t *>(nullptr),
+                                0u, static_cast<size_t>(n), rocprim::plus<uint32_t>());
+  return b;
+}
+
+template <typename CT> struct ChainParts {
+  CT *merged;
+  uint32_t *flags, *pos;
+  void *temp;
+  size_t temp_bytes, total;
+};
+
+template <typename CT> static ChainParts<CT> chain_parts(int64_t n, void *base) {
+  ChainParts<CT> p{};
+  char *b = static_cast<char *>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char *q = b ? b + off : nullptr;
+    off += align256(bytes);
+    return q;
+  };
+  p.merged = reinterpret_cast<CT *>(take(n * sizeof(CT)));
+  p.flags = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
+  p.pos = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
+  p.temp_bytes = chain_scan_bytes(n);
+  p.temp = take(p.temp_bytes);
+  p.total = off;
+  return p;
+}
+
+// a level's stride ratio on one axis; 0 if the strides do not chain
+static int chain_ratio(int prev, int cur) {
+  if (!is_pow2(prev) || !is_pow2(cur) || cur % prev != 0) return 0;
+  return cur / prev;
+}
+
+template <typename CT>
+static int chain_impl(const CT *keys, int64_t n, int levels, const int32_t *strides, void *const *outs,
+                      uint32_t *d_counts, uint32_t *d_unsorted, void *ws, size_t ws_bytes, hipStream_t s) {
+  SPIRA_HIP_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "downsample_chain: n out of range");
+  SPIRA_HIP_REQUIRE(levels >= 1 && strides && outs && d_counts && d_unsorted, "downsample_chain: bad arguments");
+  int prev[3] = {1, 1, 1};
+  for (int l = 0; l < levels; ++l) {
+    int r[3];
+    for (int a = 0; a < 3; ++a) {
+      r[a] = chain_ratio(prev[a], strides[3 * l + a]);
+      prev[a] = strides[3 * l + a];
+    }
+    SPIRA_HIP_REQUIRE(r[0] > 0 && r[1] > 0 && r[2] > 0 && r[0] * r[1] <= kChainMaxRows,
+                      "downsample_chain: each stride must be a power of two and a multiple of the previous one, "
+                      "with at most 16 input rows (x ratio times y ratio) per output run");
+    SPIRA_HIP_REQUIRE(outs[l] != nullptr, "downsample_chain: missing output array");
+  }
+  if (n == 0) {
+    for (int l = 0; l < levels; ++l) hipLaunchKernelGGL(zero_count_kernel, dim3(1), dim3(1), 0, s, d_counts + l);
+    SPIRA_HIP_LAUNCH_CHECK();
+    return kOk;
+  }
+  SPIRA_HIP_REQUIRE(ws != nullptr && ws_bytes >= chain_parts<CT>(n, nullptr).total,
+                    "downsample_chain: workspace too small");
+  ChainParts<CT> p = chain_parts<CT>(n, ws);
+  const dim3 grid(static_cast<unsigned>(div_up(n, 256)));
+  int a[3] = {1, 1, 1};
+  for (int l = 0; l < levels; ++l) {
+    const int *b = strides + 3 * l;
+    const CT *in = l == 0 ? keys : static_cast<const CT *>(outs[l - 1]);
+    const uint32_t *n_dev = l == 0 ? nullptr : d_counts + (l - 1);
+    const CT mask = stride_mask<CT>(b[0], b[1], b[2]);
+    hipLaunchKernelGGL(chain_merge_kernel<CT>, grid, dim3(256), 0, s, in, n_dev, n, mask,
+                       static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]), b[0] / a[0], b[1] / a[1], p.merged,
+                       l == 0 ? d_unsorted : nullptr);
+    SPIRA_HIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(chain_flag_kernel<CT>, grid, dim3(256), 0, s, p.merged, n_dev, n, p.flags);
+    SPIRA_HIP_LAUNCH_CHECK();
+    size_t tb = p.temp_bytes;
+    SPIRA_HIP_TRY(rocprim::exclusive_scan(p.temp, tb, p.flags, p.pos, 0u, static_cast<size_t>(n),
+                                          rocprim::plus<uint32_t>(), s));
+    hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.flags, p.pos, n,
+                       static_cast<CT *>(outs[l]), d_counts + l);
+    SPIRA_HIP_LAUNCH_CHECK();
+    for (int q = 0; q < 3; ++q) a[q] = b[q];
+  }
+  return kOk;
+}
+
 }  // namespace spira_hip
 
 using namespace spira_hip;
@@ -576,6 +794,24 @@ int spira_hip_downsample_execute(const void *keys, int64_t n, int key_bits, int 
                                   static_cast<uint64_t *>(out_keys), d_count, workspace, workspace_bytes, stream);
   return execute_impl<uint32_t>(static_cast<const uint32_t *>(keys), n, sx, sy, sz, plan,
                                 static_cast<uint32_t *>(out_keys), d_count, workspace, workspace_bytes, stream);
+}
+
+int spira_hip_downsample_chain_workspace(int64_t n, int key_bits, size_t *bytes) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample_chain: key_bits must be 32 or 64");
+  *bytes = n <= 0 ? 0
+                  : (key_bits == 64 ? chain_parts<uint64_t>(n, nullptr).total : chain_parts<uint32_t>(n, nullptr).total);
+  return kOk;
+}
+
+int spira_hip_downsample_chain(const void *keys, int64_t n, int key_bits, int levels, const int32_t *strides,
+                               void *const *out_keys, uint32_t *d_counts, uint32_t *d_unsorted, void *workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "downsample_chain: key_bits must be 32 or 64");
+  if (key_bits == 64)
+    return chain_impl<uint64_t>(static_cast<const uint64_t *>(keys), n, levels, strides, out_keys, d_counts,
+                                d_unsorted, workspace, workspace_bytes, stream);
+  return chain_impl<uint32_t>(static_cast<const uint32_t *>(keys), n, levels, strides, out_keys, d_counts, d_unsorted,
+                              workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

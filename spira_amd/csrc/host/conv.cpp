@@ -96,52 +96,26 @@ static std::unordered_map<const c10::TensorImpl *, OrderEntry> &order_cache() {
 }
 
 static bool &row_order_flag() {
-  static bool on = [] {
-    const char *e = std::getenv("SPIRA_OS_ROW_ORDER");
-    return !(e && e[0] == '0');
-  }();
+  static bool on = true;
   return on;
 }
 static bool row_order_enabled() { return row_order_flag(); }
-// Maps with fewer targets than this skip the row order: its sort costs more
-// than the few small blocks it would save.
-static int64_t row_order_min_targets() {
-  static const int64_t v = [] {
-    const char *e = std::getenv("SPIRA_OS_ROW_ORDER_MIN_T");
-    return e ? std::atoll(e) : int64_t(100000);
-  }();
-  return v;
-}
-// Maps of fewer offsets than this (SPIRA_OS_ROW_ORDER_MIN_K, default 27)
-// skip the row order: a k = 2 down / up-sampling map serves a single layer,
-// and its sort costs more than that layer saves (config-4 network: 3.28 ->
-// 3.07 ms per step without the order of its two k = 2 maps)
-static int64_t row_order_min_offsets() {
-  static const int64_t v = [] {
-    const char *e = std::getenv("SPIRA_OS_ROW_ORDER_MIN_K");
-    return e ? std::atoll(e) : int64_t(27);
-  }();
-  return v;
-}
 void set_row_order(bool on) { row_order_flag() = on; }
-// Maps of more offsets than this (SPIRA_OS_ROW_ORDER_MAX_K, default 57) skip
-// the row order: above 57 columns the sort keys cannot hold the column mask,
-// the order takes 64-bit keys and a second pass over the map, and for the
-// 125-offset maps of config 5 it cost more than it saved (SparseResNetLarge
-// on the 300k-voxel scene: 6.61 ms per step with it, 5.87 ms without).
-static int64_t row_order_max_offsets() {
-  static const int64_t v = [] {
-    const char *e = std::getenv("SPIRA_OS_ROW_ORDER_MAX_K");
-    return e ? std::atoll(e) : int64_t(57);
-  }();
-  return v;
-}
 
-// whether the fp16 output-stationary kernel walks a map of T targets and K
-// offsets in row order
-static bool row_order_applies(int64_t T, int64_t K) {
-  return row_order_enabled() && T > 0 && T >= row_order_min_targets() && K <= 128 && K >= row_order_min_offsets() &&
-         K <= row_order_max_offsets();
+// Default rule for walking an output-stationary map in row order (fp16):
+// maps of at least 100k targets and 27 to 57 offsets.  Below 100k targets
+// the sort costs more than the few small blocks it saves; a k = 2 down /
+// up-sampling map (8 offsets) serves a single layer, and its sort cost more
+// than that layer saved (config-4 network: 3.28 -> 3.07 ms per step without
+// the order of its two k = 2 maps); above 57 offsets the sort keys cannot
+// hold the column mask, the order takes 64-bit keys and a second pass over
+// the map, and for the 125-offset maps of config 5 it cost more than it saved
+// (SparseResNetLarge on the 300k-voxel scene: 6.61 ms per step with it, 5.87
+// ms without).  A layer's tuning may ask for it on (1) or off (0) instead.
+static bool row_order_applies(int64_t T, int64_t K, int request = -1) {
+  if (!row_order_enabled() || T <= 0 || K > 128) return false;
+  if (request >= 0) return request == 1;
+  return T >= 100000 && K >= 27 && K <= 57;
 }
 
 static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
@@ -183,12 +157,13 @@ static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
 // stream than the one that will read them), or nothing if the kernel uses
 // no row order for this map.  No reference counterpart (the row order is
 // this build's own).
-std::vector<torch::Tensor> prepare_row_order(const torch::Tensor &map, int64_t T) {
+std::vector<torch::Tensor> prepare_row_order(const torch::Tensor &map, int64_t T, int64_t request) {
   SPIRA_CHECK_ARG(map.dim() == 2 && map.scalar_type() == torch::kInt32, "out_in_map must be 2-D int32");
   require_device(map, "out_in_map");
   SPIRA_CHECK_ARG(map.size(0) >= T, "out_in_map has fewer rows than targets");
   const int64_t K = map.size(1);
-  if (!row_order_applies(T, K)) return {};
+  SPIRA_CHECK_ARG(request >= -1 && request <= 1, "row order request must be -1, 0 or 1");
+  if (!row_order_applies(T, K, static_cast<int>(request))) return {};
   const OrderEntry &e = row_order_of(map, T);
   std::vector<torch::Tensor> out{e.order, e.ordered_map};
   if (e.masks.defined()) out.push_back(e.masks);
@@ -274,10 +249,33 @@ static torch::Tensor zeroed_workspace(size_t bytes, const torch::Device &dev) {
   return t;
 }
 
+// A layer's output-stationary launch choices: the kernel's
+// (spira_hip_os_tuning_t, 0 = automatic) and the row order (-1 automatic,
+// 0 off, 1 on).  From Python: a 5-tuple (col_tile, step_channels,
+// offset_splits, offset_pack, row_order).
+struct OsTune {
+  spira_hip_os_tuning_t k{};
+  int row_order = -1;
+};
+using TuneArg = std::optional<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>>;
+static OsTune tune_of(const TuneArg &t) {
+  OsTune r;
+  if (!t.has_value()) return r;
+  auto [a, b, c, d, e] = *t;
+  r.k.col_tile = static_cast<int>(a);
+  r.k.step_channels = static_cast<int>(b);
+  r.k.offset_splits = static_cast<int>(c);
+  r.k.offset_pack = static_cast<int>(d);
+  r.row_order = static_cast<int>(e);
+  SPIRA_CHECK_ARG(r.row_order >= -1 && r.row_order <= 1, "row_order must be -1, 0 or 1");
+  return r;
+}
+
 static bool epi_empty(const Epi &e) { return !e.scale && !e.shift && !e.residual && !e.relu; }
 
 static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::Tensor &X0, const torch::Tensor &W,
-                   int w0, int K, void *out, int mode, const Epi &epi = Epi(), const torch::Tensor *X2 = nullptr) {
+                   int w0, int K, void *out, int mode, const Epi &epi = Epi(), const torch::Tensor *X2 = nullptr,
+                   const OsTune &tn = OsTune()) {
   const auto dev = X0.device();
   const int dtype = dtype_of(X0);
   // a channel concatenation [X0 | X2] is gathered from its two parts when
@@ -299,11 +297,11 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   size_t wsb = 0;
   const int64_t cin_run =
       (!split && dtype == SPIRA_F16 && W.size(1) % 8 != 0) ? (W.size(1) + 7) / 8 * 8 : W.size(1);
-  check_rc(spira_hip_conv_os_workspace(T, K, cin_run, W.size(2), dtype, mode, &wsb), "conv_os");
+  check_rc(spira_hip_conv_os_workspace(T, K, cin_run, W.size(2), dtype, mode, &tn.k, &wsb), "conv_os");
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && row_order_applies(T, K)) {
+  if (map && dtype == SPIRA_F16 && row_order_applies(T, K, tn.row_order)) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
@@ -317,7 +315,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   if (split) {
     check_rc(spira_hip_conv_os_concat(T, K, mp, order, masks, X.data_ptr(), X2->data_ptr(), S, X.size(1), X2->size(1),
                                       prow_ptr(P, W, w0), W.size(2), out, mode, epi.scale, epi.shift, epi.residual,
-                                      epi.relu, wsp, wsb, current_stream()),
+                                      epi.relu, &tn.k, wsp, wsb, current_stream()),
              "sparse_convolution_forward_os");
     return;
   }
@@ -325,7 +323,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   torch::Tensor Xp = X;
   if (cin != W.size(1)) Xp = torch::constant_pad_nd(X.narrow(0, 0, S), {0, cin - W.size(1)});
   check_rc(spira_hip_conv_os(T, K, mp, order, masks, Xp.data_ptr(), S, cin, wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),
-                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, wsp, wsb,
+                             dtype, out, mode, epi.scale, epi.shift, epi.residual, epi.relu, &tn.k, wsp, wsb,
                              current_stream()),
            "sparse_convolution_forward_os");
 }
@@ -335,7 +333,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
 torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const torch::Tensor &X,
                          const torch::Tensor &W, const std::optional<torch::Tensor> &scale,
                          const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
-                         bool relu, const std::optional<torch::Tensor> &x2) {
+                         bool relu, const std::optional<torch::Tensor> &x2, const TuneArg &tuning) {
   const torch::Tensor *X2 = x2.has_value() ? &*x2 : nullptr;
   check_features(X, W, X2);
   SPIRA_CHECK_ARG(out_in_map.dim() == 2, "out_in_map must be 2-D");
@@ -343,7 +341,7 @@ torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, 
                   out_in_map.size(1));
   auto Y = torch::empty({T, W.size(2)}, X.options());
   run_os(&out_in_map, S, T, X, W, 0, static_cast<int>(W.size(0)), Y.data_ptr(), SPIRA_OUT_STORE,
-         epi_of(scale, shift, residual, relu, T, W.size(2), X), X2);
+         epi_of(scale, shift, residual, relu, T, W.size(2), X), X2, tune_of(tuning));
   return Y;
 }
 
@@ -352,14 +350,14 @@ torch::Tensor forward_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, 
 // the torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313).
 torch::Tensor forward_dense(const torch::Tensor &X, const torch::Tensor &W, const std::optional<torch::Tensor> &scale,
                             const std::optional<torch::Tensor> &shift, const std::optional<torch::Tensor> &residual,
-                            bool relu, const std::optional<torch::Tensor> &x2) {
+                            bool relu, const std::optional<torch::Tensor> &x2, const TuneArg &tuning) {
   const torch::Tensor *X2 = x2.has_value() ? &*x2 : nullptr;
   check_features(X, W, X2);
   SPIRA_CHECK_ARG(W.size(0) == 1, "a dense layer has one weight offset, got ", W.size(0));
   const int64_t T = X.size(0);
   auto Y = torch::empty({T, W.size(2)}, X.options());
   run_os(nullptr, T, T, X, W, 0, 1, Y.data_ptr(), SPIRA_OUT_STORE, epi_of(scale, shift, residual, relu, T, W.size(2), X),
-         X2);
+         X2, tune_of(tuning));
   return Y;
 }
 
@@ -637,18 +635,22 @@ float time_scatter(int64_t tile, const std::optional<double> &threshold, bool is
 // launch.  No reference counterpart: a measurement probe for the roofline
 // report (the reference times its layers from Python,
 // scripts/layerwise_experiment.py:100-186).
-float time_conv_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const torch::Tensor &X,
-                   const torch::Tensor &W, int64_t reps) {
-  check_features(X, W);
+float time_conv_os(int64_t S, int64_t T, const std::optional<torch::Tensor> &out_in_map, const torch::Tensor &X,
+                   const torch::Tensor &W, int64_t reps, const std::optional<torch::Tensor> &x2,
+                   const TuneArg &tuning) {
+  const torch::Tensor *X2 = x2.has_value() ? &*x2 : nullptr;
+  check_features(X, W, X2);
   SPIRA_CHECK_ARG(reps >= 1, "reps must be positive");
   auto Y = torch::empty({T, W.size(2)}, X.options());
   const int K = static_cast<int>(W.size(0));
-  run_os(&out_in_map, S, T, X, W, 0, K, Y.data_ptr(), SPIRA_OUT_STORE);  // warm: order, weights
+  const torch::Tensor *map = out_in_map.has_value() ? &*out_in_map : nullptr;
+  const OsTune tn = tune_of(tuning);
+  run_os(map, S, T, X, W, 0, K, Y.data_ptr(), SPIRA_OUT_STORE, Epi(), X2, tn);  // warm: order, weights
   auto s = current_stream();
   hipEvent_t a, b;
   SPIRA_CHECK_ARG(hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess, "event creation failed");
   SPIRA_CHECK_ARG(hipEventRecord(a, s) == hipSuccess, "event record failed");
-  for (int64_t i = 0; i < reps; ++i) run_os(&out_in_map, S, T, X, W, 0, K, Y.data_ptr(), SPIRA_OUT_STORE);
+  for (int64_t i = 0; i < reps; ++i) run_os(map, S, T, X, W, 0, K, Y.data_ptr(), SPIRA_OUT_STORE, Epi(), X2, tn);
   SPIRA_CHECK_ARG(hipEventRecord(b, s) == hipSuccess, "event record failed");
   SPIRA_CHECK_ARG(hipEventSynchronize(b) == hipSuccess, "event synchronisation failed");
   float ms = 0.f;
@@ -658,6 +660,19 @@ float time_conv_os(int64_t S, int64_t T, const torch::Tensor &out_in_map, const 
   return ms / static_cast<float>(reps);
 }
 
+// The launch the output-stationary kernel would make (spira_hip_conv_os_plan):
+// (col_tile, step_channels, offset_splits, offsets_per_step, grid_x, grid_y).
+// No reference counterpart: it shows what a layer's tuning changes.
+std::vector<int64_t> conv_os_plan(int64_t T, int64_t K, int64_t cin, int64_t cin2, int64_t cout, bool has_map,
+                                  const TuneArg &tuning) {
+  const OsTune tn = tune_of(tuning);
+  int32_t plan[6] = {};
+  check_rc(spira_hip_conv_os_plan(T, static_cast<int>(K), static_cast<int>(cin), static_cast<int>(cin2),
+                                  static_cast<int>(cout), has_map ? 1 : 0, SPIRA_OUT_STORE, &tn.k, plan),
+           "conv_os_plan");
+  return std::vector<int64_t>(plan, plan + 6);
+}
+
 // (reference: cuda_free_buffers / cuda_reset_error, torch/cuda_memory_buffer.cu:7-16)
 void free_buffers() { c10::hip::HIPCachingAllocator::emptyCache(); }
 void reset_error() { (void)hipGetLastError(); }
@@ -665,7 +680,9 @@ void reset_error() { (void)hipGetLastError(); }
 void register_conv(pybind11::module_ &m) {
   m.def("cuda_sparse_convolution_forward_os", &forward_os);
   m.def("cuda_dense_forward", &forward_dense);
-  m.def("time_conv_os", &time_conv_os);
+  m.def("time_conv_os", &time_conv_os, pybind11::arg("S"), pybind11::arg("T"), pybind11::arg("out_in_map"),
+        pybind11::arg("X"), pybind11::arg("W"), pybind11::arg("reps"), pybind11::arg("x2") = pybind11::none(),
+        pybind11::arg("tuning") = pybind11::none());
   m.def("cuda_sparse_convolution_forward_ws", &forward_ws);
   m.def("cuda_sparse_convolution_forward_ws_merged", &forward_ws_merged);
   m.def("cuda_sparse_convolution_forward_hs", &forward_hs);
@@ -677,7 +694,11 @@ void register_conv(pybind11::module_ &m) {
   m.def("cuda_reset_error", &reset_error);
   m.def("set_os_row_order", &set_row_order);
   m.def("kmap_row_order", &kmap_row_order);
-  m.def("prepare_row_order", &prepare_row_order);
+  m.def("conv_os_plan", &conv_os_plan, pybind11::arg("T"), pybind11::arg("K"), pybind11::arg("cin"),
+        pybind11::arg("cin2"), pybind11::arg("cout"), pybind11::arg("has_map"),
+        pybind11::arg("tuning") = pybind11::none());
+  m.def("prepare_row_order", &prepare_row_order, pybind11::arg("map"), pybind11::arg("T"),
+        pybind11::arg("request") = -1);
 }
 
 }  // namespace spira_host

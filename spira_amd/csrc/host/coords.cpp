@@ -64,6 +64,22 @@ torch::Tensor downsample(const torch::Tensor &keys, int sx, int sy, int sz) {
   return out.slice(0, 0, nu);
 }
 
+// Whether the target strides form a chain spira_hip_downsample_chain takes:
+// powers of two, each a multiple of the previous one per axis (the first of
+// 1), with x ratio times y ratio at most 16 per level.
+static bool chainable(const std::vector<Int3> &strides) {
+  int prev[3] = {1, 1, 1};
+  auto pow2 = [](int v) { return v > 0 && (v & (v - 1)) == 0; };
+  for (auto &t : strides) {
+    const int cur[3] = {std::get<0>(t), std::get<1>(t), std::get<2>(t)};
+    for (int a = 0; a < 3; ++a)
+      if (!pow2(cur[a]) || cur[a] % prev[a] != 0) return false;
+    if ((cur[0] / prev[0]) * (cur[1] / prev[1]) > 16) return false;
+    for (int a = 0; a < 3; ++a) prev[a] = cur[a];
+  }
+  return true;
+}
+
 // One downsample per target stride: every plan on the current stream, one
 // host read of all plans, then each execution on its own pool stream, and
 // one host read of all counts at the end (reference:
@@ -75,6 +91,37 @@ std::vector<torch::Tensor> streamed_output_generate(const torch::Tensor &keys, c
   const auto dev = keys.device();
   const int64_t n = keys.size(0);
   const size_t B = strides.size();
+  // Nested power-of-two strides (2, 4, 8, 16 ...): every level from the
+  // previous one, no host read until the counts (spira_hip_downsample_chain);
+  // keys that turn out unsorted fall through to the per-stride path below.
+  if (n > 0 && B > 0 && chainable(strides)) {
+    std::vector<int32_t> st;
+    for (auto &t : strides) {
+      auto [sx, sy, sz] = t;
+      st.insert(st.end(), {sx, sy, sz});
+    }
+    std::vector<torch::Tensor> outs;
+    std::vector<void *> ptrs;
+    for (size_t i = 0; i < B; ++i) {
+      outs.push_back(torch::empty_like(keys));
+      ptrs.push_back(outs.back().data_ptr());
+    }
+    auto cnt = torch::zeros({static_cast<int64_t>(B + 1)}, torch::TensorOptions(dev).dtype(torch::kInt32));
+    size_t cwb = 0;
+    check_rc(spira_hip_downsample_chain_workspace(n, bits, &cwb), "streamed_output_generate");
+    auto cws = workspace(cwb, dev);
+    uint32_t *c = reinterpret_cast<uint32_t *>(cnt.data_ptr<int32_t>());
+    check_rc(spira_hip_downsample_chain(keys.data_ptr(), n, bits, static_cast<int>(B), st.data(), ptrs.data(), c,
+                                        c + B, cws.data_ptr(), cwb, current_stream()),
+             "streamed_output_generate");
+    auto h = cnt.cpu();
+    const int32_t *hc = h.data_ptr<int32_t>();
+    if (hc[B] == 0) {
+      std::vector<torch::Tensor> res;
+      for (size_t i = 0; i < B; ++i) res.push_back(outs[i].slice(0, 0, hc[i]));
+      return res;
+    }
+  }
   auto counts = torch::zeros({static_cast<int64_t>(std::max<size_t>(B, 1))},
                              torch::TensorOptions(dev).dtype(torch::kInt32));
   constexpr int64_t PB = sizeof(spira_hip_downsample_plan_t);

@@ -42,6 +42,10 @@ class KernelMapCache:
     def __init__(self):
         self._kernel_maps_cache: Dict[tuple, list] = {}
         self._coordinates_cache: Dict[tuple, torch.Tensor] = {}
+        #: per map key (source stride, target stride, kernel size): walk the
+        #: output-stationary map in row order (1) or not (0); maps without an
+        #: entry follow the library's default rule.  Set by the selector.
+        self.row_order_requests: Dict[tuple, int] = {}
 
     def reset(self) -> None:
         self._coordinates_cache.clear()
@@ -107,9 +111,13 @@ class KernelMapCache:
             self._coordinates_cache[as_tuple(ts, size=3)] = voxels[i + 1]
         kmaps = F.build_kmap_streamed(voxels, kernel_sizes, list(source_strides)[:-1], dataflow)
         if self.prepare_row_orders:
+            s_prev = as_tuple(init_stride, size=3)
             for i, d in enumerate(dataflow):
+                t_stride = as_tuple(source_strides[i + 1], size=3)
+                key = (s_prev, t_stride, as_tuple(kernel_sizes[i], size=3))
+                s_prev = t_stride
                 if d == 0:
-                    F.prepare_row_order(kmaps[i][2], kmaps[i][1])
+                    F.prepare_row_order(kmaps[i][2], kmaps[i][1], self.row_order_requests.get(key, -1))
         for i in range(len(kernel_sizes)):
             t_stride = as_tuple(source_strides[i + 1], size=3)
             self._kernel_maps_cache[(s_stride, t_stride, as_tuple(kernel_sizes[i], size=3))] = [False, *kmaps[i]]
@@ -143,8 +151,12 @@ class SparseConv(Module):
             "scatter_tile_size": min(out_channels, 16),
             "map_dataflow": 2,
             "force_os": False,
+            # output-stationary launch choices (col_tile, step_channels,
+            # offset_splits, offset_pack, row_order); None = automatic
+            "os_tuning": None,
         }
         self._tuning_data = None
+        self._os_tuning_data = None
         # fused epilogue (spira_amd.nn.fusion): an absorbed eval-mode batch
         # norm (plain attribute, not a submodule) and ReLU
         object.__setattr__(self, "_epi_bn", None)
@@ -178,8 +190,11 @@ class SparseConv(Module):
     @contextlib.contextmanager
     def tune_gs(self, free_buffers: bool = True):
         """Record (masks, sizes) of gather-scatter runs while inside, then sweep
-        the bucket threshold and the gather / scatter tile sizes by timing
-        (reference conv.py:217-307)."""
+        the bucket threshold by timing the grouped GEMM (reference
+        conv.py:217-307).  The reference's gather / scatter tile sweep has no
+        counterpart here: the gather and scatter kernels of this build have
+        no tile parameter (the keys stay in the config for file
+        compatibility); the CDNA4 launch choices are swept by ``tune_os``."""
         try:
             self._tuning_data = []
             if free_buffers:
@@ -201,22 +216,28 @@ class SparseConv(Module):
                 t = float(np.average(t))
                 if best is None or t < best:
                     best, self._tunable_config["threshold"] = t, thr
-            for key, channels, probe in (("gather_tile_size", self.in_channels, F.cuda_time_gather),
-                                         ("scatter_tile_size", self.out_channels, F.cuda_time_scatter)):
-                best = None
-                for tile in range(4, channels + 1, 4):
-                    if channels % tile:
-                        continue
-                    t = float(np.average([
-                        probe(threshold=self._tunable_config["threshold"], tile_size=tile, weights=self.kernel,
-                              source_masks=sm, target_masks=tm, kernel_map_sizes=nb)
-                        for _ in range(self.__NUM_TUNING_ROUNDS__) for sm, tm, nb in self._tuning_data]))
-                    if best is None or t < best:
-                        best, self._tunable_config[key] = t, tile
             if free_buffers:
                 F.cuda_free_buffers()
         finally:
             self._tuning_data = None
+
+    @contextlib.contextmanager
+    def tune_os(self, reps: int = 10):
+        """Record the output-stationary calls made while inside, then choose
+        this layer's launch choices -- column tile, step channels, offset
+        splits and offset packing -- by timing the recorded calls on the
+        kernel, one field at a time over two passes (the CDNA4 counterpart of
+        the reference's gather / scatter tile sweep, conv.py:217-307).  The
+        row order field is left as it is: it is decided per map (its sort is
+        shared by every layer on the map), by ``spira_amd.utils.helpers``."""
+        try:
+            self._os_tuning_data = []
+            yield
+            data = self._os_tuning_data
+            if data and self.kernel.is_cuda and self.kernel.dtype == torch.float16:
+                self._tunable_config["os_tuning"] = choose_os_tuning(self, data, reps)
+        finally:
+            self._os_tuning_data = None
 
     def forward(self, inputs: SparseTensor, residual: Optional[SparseTensor] = None) -> SparseTensor:
         """residual (fused res blocks only): features added after the batch
@@ -242,7 +263,10 @@ class SparseConv(Module):
             raise ValueError("a residual is only taken by a conv with an active fused epilogue")
         if self.is_trivial:
             if x.is_cuda:
-                y = F.dense_forward(x, self.kernel, epilogue=epilogue, sources2=x2)
+                y = F.dense_forward(x, self.kernel, epilogue=epilogue, sources2=x2,
+                                    tuning=self._tunable_config.get("os_tuning"))
+                if self._os_tuning_data is not None:
+                    self._os_tuning_data.append((x.shape[0], x.shape[0], None, x, x2, None))
                 epilogue_done = True
             else:
                 y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
@@ -263,7 +287,11 @@ class SparseConv(Module):
             S, T = (m[1], m[0]) if self.transposed else (m[0], m[1])
             cfg = self._tunable_config
             if d == 0 or force_os:
-                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue, sources2=x2)
+                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue, sources2=x2,
+                                                    tuning=cfg.get("os_tuning"))
+                if self._os_tuning_data is not None:
+                    mkey = None if self.transposed else (tuple(inputs._stride), tuple(stride), self.kernel_size)
+                    self._os_tuning_data.append((S, T, m[2], x, x2, mkey))
             elif d == 1:
                 y = F.sparse_convolution_forward_ws_merged(S, T, x, self.kernel, m[5], m[6], m[3], m[7], m[8],
                                                            self.transposed, epilogue=epilogue)
@@ -299,3 +327,60 @@ class SparseConv(Module):
         elif self.bias is not None and epilogue is None:
             y += self.bias
         return SparseTensor(features=y, coordinates=coords, stride=stride)
+
+
+def os_candidates(c_in: int, c_out: int, volume: int) -> List[List[int]]:
+    """Values tried per output-stationary launch field (0 = automatic):
+    column tiles up to the output width, step channels up to the padded input
+    width, offset splits, and offset packing where it applies (16-, 32- and
+    64-channel inputs of kernels above 27 offsets)."""
+    cin_p = (c_in + 15) // 16 * 16
+    cols = [0] + [c for c in (32, 64, 96, 128) if c <= (c_out + 31) // 32 * 32]
+    steps = [0, 32] + ([64] if cin_p >= 64 else []) + ([128] if cin_p >= 96 else [])
+    splits = [0, 1, 2, 4] if volume > 1 else [0]
+    packs = [0, 1, 2, 4] if (volume > 27 and cin_p in (16, 32, 64)) else [0]
+    return [cols, steps, splits, packs]
+
+
+def time_os_calls(layer: "SparseConv", calls, tuning: tuple, reps: int) -> float:
+    """Kernel time (ms) of a layer's recorded output-stationary calls under
+    `tuning`; one call per distinct shape is timed."""
+    from .functional import _native
+    seen, total = set(), 0.0
+    for S, T, omap, x, x2, _ in calls:
+        key = (S, T, None if omap is None else omap.data_ptr(), x.shape[1], None if x2 is None else x2.shape[1])
+        if key in seen:
+            continue
+        seen.add(key)
+        total += _native._C.time_conv_os(S, T, omap, x, layer.kernel, reps, x2, tuple(tuning))
+    return total
+
+
+def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10) -> tuple:
+    """Coordinate search over the launch fields of ``os_candidates``: each
+    field in turn takes its fastest value with the others fixed, twice
+    over; a value the library rejects is skipped."""
+    cur = layer._tunable_config.get("os_tuning")
+    row_order = -1 if cur is None else int(cur[4])
+    cands = os_candidates(layer.in_channels, layer.out_channels, int(np.prod(layer.kernel_size)))
+    best = [0, 0, 0, 0]
+
+    def cost(fields):
+        try:
+            return time_os_calls(layer, calls, tuple(fields) + (row_order,), reps)
+        except RuntimeError:
+            F.cuda_reset_error()
+            return float("inf")
+
+    best_t = cost(best)
+    for _ in range(2):
+        for i, values in enumerate(cands):
+            for v in values:
+                if v == best[i]:
+                    continue
+                trial = list(best)
+                trial[i] = v
+                t = cost(trial)
+                if t < best_t:
+                    best, best_t = trial, t
+    return tuple(best) + (row_order,)

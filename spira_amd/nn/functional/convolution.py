@@ -111,21 +111,34 @@ def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sou
                                                         mapsize, qmapsize, bool(transpose), *_epi(epilogue))
 
 
-def dense_forward(sources, weights, *, epilogue=None, sources2=None):
+def _tuning(tuning) -> Optional[tuple]:
+    """An output-stationary launch choice: None (automatic) or a 5-tuple
+    (col_tile, step_channels, offset_splits, offset_pack, row_order); 0 (and
+    -1 for row_order) in a field = automatic."""
+    if tuning is None:
+        return None
+    t = tuple(int(v) for v in tuning)
+    if len(t) != 5:
+        raise ValueError(f"an output-stationary tuning has 5 fields, got {len(t)}")
+    return t
+
+
+def dense_forward(sources, weights, *, epilogue=None, sources2=None, tuning=None):
     """sources @ weights[0] (a 1x1x1, stride-1 layer) with the fused epilogue,
     on the output-stationary kernel with the identity map (reference: the
     torch.mm path of SparseConv.forward, source/spira/nn/conv.py:310-313).
     ``sources2``: the input is the channel concatenation [sources | sources2],
     gathered from its two parts without materialising it."""
     _gpu(sources)
-    return _C.cuda_dense_forward(_c(sources), _c(weights), *_epi(epilogue), _c(sources2))
+    return _C.cuda_dense_forward(_c(sources), _c(weights), *_epi(epilogue), _c(sources2), _tuning(tuning))
 
 
 def sparse_convolution_forward_os(num_sources: int, num_targets: int, out_in_map, sources, weights, *,
-                                  epilogue=None, sources2=None):
+                                  epilogue=None, sources2=None, tuning=None):
     """``sources2``: the layer input is the channel concatenation
     [sources | sources2] (a decoder's skip connection), gathered from its two
-    parts without materialising it."""
+    parts without materialising it.  ``tuning``: the layer's launch choices
+    (see ``_tuning``); they change the schedule, never the result."""
     _gpu(sources)
     return _C.cuda_sparse_convolution_forward_os(num_sources, num_targets, _c(out_in_map), _c(sources),
-                                                 _c(weights), *_epi(epilogue), _c(sources2))
+                                                 _c(weights), *_epi(epilogue), _c(sources2), _tuning(tuning))

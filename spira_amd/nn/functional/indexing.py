@@ -67,14 +67,15 @@ def build_kmap_streamed(voxels: List[torch.Tensor], kernel_sizes: List[ScalarOrT
     return _C.cuda_binary_search_streamed(voxels, kernel_sizes, source_strides, list(dataflow))
 
 
-def prepare_row_order(kmap: torch.Tensor, num_targets: int) -> List[torch.Tensor]:
+def prepare_row_order(kmap: torch.Tensor, num_targets: int, request: int = -1) -> List[torch.Tensor]:
     """Queue the row order of an output-stationary map on the current stream
-    if the fp16 convolution kernel will walk it in row order (large maps of
-    27 or more offsets), so that it is computed with the maps instead of at
-    the first layer that uses it.  Returns the row order's tensors (empty if
-    the map gets none)."""
+    if the fp16 convolution kernel will walk it in row order (by default:
+    large maps of 27 to 57 offsets; ``request`` 1 / 0 asks for it / against
+    it), so that it is computed with the maps instead of at the first layer
+    that uses it.  Returns the row order's tensors (empty if the map gets
+    none)."""
     _require_gpu(kmap)
-    return list(_C.prepare_row_order(kmap, int(num_targets)))
+    return list(_C.prepare_row_order(kmap, int(num_targets), int(request)))
 
 
 def downsample(coordinates: torch.Tensor, target_stride: Tuple[int, int, int]) -> torch.Tensor:

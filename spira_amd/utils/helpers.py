@@ -27,7 +27,7 @@ from .typing import ScalarOrTuple
 
 __all__ = ["as_tuple", "make_divisible", "set_kernel_map_cache", "tune", "StableTimeAccumulator",
            "DataflowConfig", "set_config_for_group", "measure_model_time", "tune_dataflows", "tune_gs",
-           "apply_tuned_configs", "save_tuning_results", "load_tuning_results"]
+           "tune_os", "tune_row_orders", "apply_tuned_configs", "save_tuning_results", "load_tuning_results"]
 
 
 def set_kernel_map_cache(module: Module, cache) -> Module:
@@ -188,6 +188,88 @@ def tune_gs(model: Module, kernel_map_cache, data_loader, n_samples: int = 10) -
                 break
 
 
+def _forward_once(model: Module, kernel_map_cache, sample) -> None:
+    if kernel_map_cache is not None:
+        kernel_map_cache.reset()
+    with torch.no_grad():
+        model(sample)
+    torch.cuda.synchronize()
+
+
+def tune_os(model: Module, kernel_map_cache, sample, reps: int = 10) -> None:
+    """Output-stationary launch choices of every fp16 layer that runs the
+    output-stationary kernel (``SparseConv.tune_os``), from one forward pass
+    of `sample`, then the row order per map (``tune_row_orders``)."""
+    SparseConv = _sparse_conv_cls()
+    with contextlib.ExitStack() as stack:
+        for m in model.modules():
+            if isinstance(m, SparseConv):
+                stack.enter_context(m.tune_os(reps))
+        _forward_once(model, kernel_map_cache, sample)
+    tune_row_orders(model, kernel_map_cache, sample, reps)
+
+
+def _row_order_ms(omap: torch.Tensor, num_targets: int, reps: int = 5) -> float:
+    """Time (ms) to compute a map's row order (on fresh copies: the order is
+    cached per map tensor)."""
+    from ..nn.functional import _native
+    copies = [omap.clone() for _ in range(reps)]
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for c in copies:
+        _native._C.kmap_row_order(c, int(num_targets))
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10) -> Dict[Tuple, int]:
+    """Walk each output-stationary map (27..128 offsets, non-transposed
+    layers) in row order or not, whichever is faster for the layers that read
+    it, counting the order's sort once per map.  Sets every such layer's
+    row-order field and the cache's request for the map; returns the
+    requests."""
+    SparseConv = _sparse_conv_cls()
+    from ..nn.conv import time_os_calls
+    convs = [m for m in model.modules() if isinstance(m, SparseConv)]
+    for m in convs:
+        m._os_tuning_data = []
+    try:
+        _forward_once(model, kernel_map_cache, sample)
+        by_map: Dict[Tuple, list] = defaultdict(list)
+        for m in convs:
+            if m.kernel.dtype != torch.float16 or not m.kernel.is_cuda:
+                continue
+            for call in m._os_tuning_data:
+                omap, key = call[2], call[5]
+                if omap is None or key is None or not (27 <= omap.shape[1] <= 128):
+                    continue
+                by_map[key].append((m, call))
+        requests: Dict[Tuple, int] = {}
+        for key, entries in by_map.items():
+            totals = {}
+            for r in (0, 1):
+                t = 0.0
+                for m, call in entries:
+                    cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, -1)
+                    t += time_os_calls(m, [call], tuple(cur[:4]) + (r,), reps)
+                totals[r] = t
+            omap, T = entries[0][1][2], entries[0][1][1]
+            totals[1] += _row_order_ms(omap, T)
+            r = 1 if totals[1] < totals[0] else 0
+            requests[key] = r
+            for m, _ in entries:
+                cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, -1)
+                m._tunable_config["os_tuning"] = tuple(cur[:4]) + (r,)
+        if kernel_map_cache is not None:
+            kernel_map_cache.row_order_requests.update(requests)
+        return requests
+    finally:
+        for m in convs:
+            m._os_tuning_data = None
+
+
 def apply_tuned_configs(model: Module, name_to_group: Dict[str, Tuple], best_configs: Dict[Tuple, DataflowConfig],
                         layer_configs: Optional[Dict[str, Dict]] = None) -> None:
     SparseConv = _sparse_conv_cls()
@@ -195,9 +277,10 @@ def apply_tuned_configs(model: Module, name_to_group: Dict[str, Tuple], best_con
         for name, m in model.named_modules():
             if isinstance(m, SparseConv) and name in layer_configs:
                 cfg = layer_configs[name]
-                for k in ("gather_tile_size", "scatter_tile_size", "threshold"):
+                for k in ("gather_tile_size", "scatter_tile_size", "threshold", "os_tuning"):
                     if k in cfg:
-                        m._tunable_config[k] = cfg[k]
+                        m._tunable_config[k] = tuple(cfg[k]) if k == "os_tuning" and cfg[k] is not None \
+                            else cfg[k]
     group_to_layers = defaultdict(list)
     for name, gid in name_to_group.items():
         group_to_layers[gid].append(name)
@@ -207,7 +290,7 @@ def apply_tuned_configs(model: Module, name_to_group: Dict[str, Tuple], best_con
 
 
 def save_tuning_results(name_to_group: Dict, best_configs: Dict[Tuple, DataflowConfig], save_path: str,
-                        model: Module) -> None:
+                        model: Module, row_order_requests: Optional[Dict[Tuple, int]] = None) -> None:
     SparseConv = _sparse_conv_cls()
     d = os.path.dirname(save_path)
     if d:
@@ -219,13 +302,16 @@ def save_tuning_results(name_to_group: Dict, best_configs: Dict[Tuple, DataflowC
         "best_configs": {k: {"map_dataflow": v.map_dataflow, "force_os": v.force_os}
                          for k, v in best_configs.items()},
         "layer_configs": layer_configs,
+        "row_order_requests": dict(row_order_requests or {}),
     }, save_path)
 
 
-def load_tuning_results(load_path: str):
+def load_tuning_results(load_path: str, with_row_orders: bool = False):
     # the file holds only dicts / tuples / numbers: the weights-only loader suffices
     data = torch.load(load_path, weights_only=True)
     best = {k: DataflowConfig(v["map_dataflow"], v["force_os"]) for k, v in data["best_configs"].items()}
+    if with_row_orders:
+        return data["name_to_group"], best, data.get("layer_configs", {}), data.get("row_order_requests", {})
     return data["name_to_group"], best, data.get("layer_configs", {})
 
 
@@ -233,8 +319,10 @@ def tune(model: Module, data_loader: Iterable, kernel_map_cache=None, map_datafl
          test_force_os: bool = True, n_samples: int = 10, n_samples_for_gs: int = 1,
          save_dir: str = ".tune_configs", tune_tag: str = "default", force_retune: bool = False,
          allow_gs_tuning: bool = True, verbose: bool = False,
-         return_dataflows: bool = False) -> Union[Module, Tuple[Module, Dict]]:
-    """Select a dataflow per layer group by measurement (see module doc)."""
+         return_dataflows: bool = False, allow_os_tuning: bool = True) -> Union[Module, Tuple[Module, Dict]]:
+    """Select a dataflow per layer group by measurement (see module doc),
+    then (``allow_os_tuning``) the output-stationary launch choices of every
+    layer and the row order of every output-stationary map."""
     SparseConv = _sparse_conv_cls()
     if map_dataflow_options is None:
         map_dataflow_options = list(range(9))
@@ -248,8 +336,10 @@ def tune(model: Module, data_loader: Iterable, kernel_map_cache=None, map_datafl
     save_path = os.path.join(save_dir, f"{tune_tag}.pt")
     if os.path.exists(save_path) and not force_retune:
         try:
-            name_to_group, best, layer_configs = load_tuning_results(save_path)
+            name_to_group, best, layer_configs, requests = load_tuning_results(save_path, with_row_orders=True)
             apply_tuned_configs(model, name_to_group, best, layer_configs)
+            if kernel_map_cache is not None:
+                kernel_map_cache.row_order_requests.update(requests)
             groups = {g: c.map_dataflow for g, c in best.items()}
             return (model, groups) if return_dataflows else model
         except Exception as e:  # unreadable cache: tune again
@@ -284,6 +374,11 @@ def tune(model: Module, data_loader: Iterable, kernel_map_cache=None, map_datafl
     best = tune_dataflows(model, samples, group_to_name, options, kernel_map_cache, n_samples=n_samples,
                           verbose=verbose)
     apply_tuned_configs(model, name_to_group, best, None)
-    save_tuning_results(name_to_group, best, save_path, model)
+    requests: Dict[Tuple, int] = {}
+    if allow_os_tuning and samples and torch.cuda.is_available():
+        tune_os(model, kernel_map_cache, samples[0])
+        if kernel_map_cache is not None:
+            requests = dict(kernel_map_cache.row_order_requests)
+    save_tuning_results(name_to_group, best, save_path, model, requests)
     groups = {g: c.map_dataflow for g, c in best.items()}
     return (model, groups) if return_dataflows else model

@@ -69,12 +69,23 @@ def _grid(xs, ys, zs):
     return g.reshape(-1, 3).astype(np.int32)
 
 
-def _ds_case(dev, keys_np, bits, strides):
+# Target-stride lists whose strides nest (powers of two, each a multiple of
+# the previous one): the streamed call takes the chained path (each level from
+# the previous one, no host read); unsorted keys fall back to the per-stride
+# path.  The anisotropic list merges 2 x 4 input rows per output run.
+CHAINS = [[(2, 2, 2), (4, 4, 4), (8, 8, 16), (16, 16, 16)], [(1, 1, 2), (2, 2, 2), (4, 8, 8)],
+          [(1, 1, 1), (4, 4, 4)]]
+
+
+def _ds_case(dev, keys_np, bits, strides, chains=()):
     tk = torch.from_numpy(keys_np).to(dev)
     for s in strides:
         assert np.array_equal(np_(F.downsample(tk, s)), orc.downsample(keys_np, s)), s
-    for o, s in zip(F.streamed_output_generate(tk, strides), strides):
-        assert np.array_equal(np_(o), orc.downsample(keys_np, s)), s
+    for lst in [strides, *chains]:
+        outs = F.streamed_output_generate(tk, lst)
+        assert len(outs) == len(lst)
+        for o, s in zip(outs, lst):
+            assert np.array_equal(np_(o), orc.downsample(keys_np, s)), (lst, s)
 
 
 @pytest.mark.parametrize("bits", [32, 64])
@@ -92,12 +103,12 @@ def test_downsample_paths(dev, bits):
     slab = _grid([4, 5], range(0, 85), range(0, 85))  # 14450 keys in one run at x stride 2
     for c in (scattered, np.concatenate([scattered, slab]), np.concatenate([scattered, plane])):
         rk, _ = orc.flatten_sort(c, bits == 64)
-        _ds_case(dev, rk, bits, strides)
-        _ds_case(dev, rng.permutation(rk), bits, strides)  # unsorted
-        _ds_case(dev, np.sort(np.concatenate([rk, rk[::3]])), bits, strides)  # duplicates
+        _ds_case(dev, rk, bits, strides, CHAINS)
+        _ds_case(dev, rng.permutation(rk), bits, strides, CHAINS)  # unsorted
+        _ds_case(dev, np.sort(np.concatenate([rk, rk[::3]])), bits, strides, CHAINS)  # duplicates
     for c in (scattered[:1], scattered[:2]):
         rk, _ = orc.flatten_sort(c, bits == 64)
-        _ds_case(dev, rk, bits, strides)
+        _ds_case(dev, rk, bits, strides, CHAINS)
 
 
 def test_downsample_wide_sort_keys(dev):
@@ -109,13 +120,13 @@ def test_downsample_wide_sort_keys(dev):
     slab = _grid([-2, -1], range(-40, 41), range(0, 91))  # 14742 keys in one x run at stride 2
     for c in (pts, np.concatenate([pts, slab])):
         rk, _ = orc.flatten_sort(np.unique(c, axis=0), True)
-        _ds_case(dev, rk, 64, [(2, 2, 2), (4, 4, 4), (1, 2, 1), (16, 16, 16)])
+        _ds_case(dev, rk, 64, [(2, 2, 2), (4, 4, 4), (1, 2, 1), (16, 16, 16)], CHAINS)
 
 
 def test_downsample_indoor_scene(dev):
     """Config-4 scene: runs of up to ~16.5k keys (the 32k-key block tile)."""
     rk, _ = orc.flatten_sort(scenes.indoor(), True)
-    _ds_case(dev, rk, 64, [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)])
+    _ds_case(dev, rk, 64, [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)], CHAINS)
 
 
 @pytest.mark.parametrize("bits", [32, 64])

@@ -66,7 +66,7 @@ def test_network_matches_oracle(dev, name):
     feats = np.random.default_rng(7).standard_normal((len(coords), cin)).astype(np.float32)
     # oracle first, on the fp32 weights rounded to fp16 (the GPU network's weights)
     model = model.half().float()
-    ref = network_forward(model, coords, feats)
+    ref = network_forward(model, coords, feats, 0)
     gpu_model = model.to(dev).half().eval()
     spira_amd.nn.fuse_epilogues(gpu_model)
     out = _gpu_forward(gpu_model, name, coords, feats, dev)
