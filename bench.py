@@ -125,6 +125,22 @@ class E2E:
         self.coords, self.feats = e2e_inputs(torch, coords_np, self.cin)
         self.dataflows = [args.dataflow] * len(self.ks)
         self.chosen = None
+        self.randomise_norms()
+
+    def randomise_norms(self, seed=42):
+        """Batch-norm statistics and affine parameters drawn at random (the
+        parity tests' choice): with the library's default statistics the
+        random-init network shrinks its activations ~3x per layer, into
+        fp16's subnormal range at the coarse levels."""
+        import spira_amd
+        g = self.torch.Generator().manual_seed(seed)
+        for m in self.model.modules():
+            if isinstance(m, spira_amd.nn.BatchNorm):
+                n = m.running_mean.numel()
+                m.running_mean.copy_(0.1 * self.torch.randn(n, generator=g))
+                m.running_var.copy_(0.5 + self.torch.rand(n, generator=g))
+                m.weight.data.copy_(0.5 + self.torch.rand(n, generator=g))
+                m.bias.data.copy_(0.1 * self.torch.randn(n, generator=g))
 
     def tune(self):
         """The selector: dataflow per layer group (0-2, as fast as the model

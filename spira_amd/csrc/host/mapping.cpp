@@ -161,6 +161,17 @@ KmapTuple binary_search(const torch::Tensor &sources, const torch::Tensor &targe
   return finish_map(pm, P, QP, stream);
 }
 
+// Output-stationary maps on one pool stream each instead of back to back on
+// the current stream.  Off by default: measured on MI355X, the fan-out's
+// host work (an event record and wait per stream) costs more than the
+// overlap returns -- config-4 step 2.92 ms concurrent vs 2.85 ms serial,
+// config 5 (seven 125-offset maps) 4.75 vs 4.71 ms.
+static bool &concurrent_maps() {
+  static bool on = false;
+  return on;
+}
+void set_concurrent_maps(bool on) { concurrent_maps() = on; }
+
 // Network-wide build: map i reads sources voxels[i/2] and targets
 // voxels[(i+1)/2] (the layer list alternates submanifold / downsampling
 // maps); every map runs on its own pool stream and the pair counts of all
@@ -181,18 +192,20 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
   auto sizes_host = torch::empty({static_cast<int64_t>(std::max<size_t>(2 * n, 2))},
                                  torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
   std::vector<KmapTuple> out;
-  // Output-stationary maps are one search kernel each: they go on the
-  // current stream back to back (a stream fan-out costs more host time per
-  // map than the kernel takes; measured end to end, either way gives the
-  // same step time).  The other dataflows run several kernels and
-  // a size read-back per map: one pool stream each.
+  // Every map on a pool stream of its own (concurrent_maps()), so that the
+  // searches of all layers run concurrently; by default output-stationary maps
+  // (one search kernel each) go back to back on the current stream and the
+  // other dataflows (several kernels and a size read-back per map) on pool
+  // streams.  The current stream waits for all of them.
   std::vector<size_t> side_of(n, 0);
   size_t nside = 0;
   for (size_t i = 0; i < n; ++i)
-    if (dataflow[i] != 0) side_of[i] = nside++;
+    if (concurrent_maps() || dataflow[i] != 0) side_of[i] = nside++;
   StreamFan fan(dev, nside);
   const hipStream_t cur = current_stream();
-  auto stream_of = [&](size_t i) { return dataflow[i] == 0 ? cur : fan[side_of[i]]; };
+  auto stream_of = [&](size_t i) {
+    return (concurrent_maps() || dataflow[i] != 0) ? fan[side_of[i]] : cur;
+  };
   for (size_t i = 0; i < n; ++i) {
     // half maps: dataflow 2 uses the position in the list (mapping.cu:1129),
     // the other dataflows compare the set sizes (mapping.cu:955)
@@ -284,6 +297,7 @@ float time_kmap_search(const torch::Tensor &sources, const torch::Tensor &target
 
 void register_mapping(pybind11::module_ &m) {
   m.def("time_kmap_search", &time_kmap_search);
+  m.def("set_concurrent_maps", &set_concurrent_maps);
   m.def("cuda_binary_search", &binary_search);
   m.def("cuda_binary_search_streamed", &binary_search_streamed);
   m.def("cuda_binary_search_no_small_z", &binary_search_no_small_z);
