@@ -58,6 +58,19 @@ int spira_hip_flatten_sort(const int32_t *coords, int64_t n, int key_bits, void 
 int spira_hip_flatten_sort_noalloc(const int32_t *coords, int64_t n, int key_bits, void *keys_out, int32_t *perm_out,
                                    hipStream_t stream);
 
+/* Workspace bytes for spira_hip_radix_sort_pairs. */
+int spira_hip_radix_sort_workspace(int64_t n, int key_bits, size_t *bytes);
+
+/* Stable ascending sort of n (key, int32 value) pairs, keys unsigned 32- or
+ * 64-bit: (keys_in, vals_in) -> (keys_out, vals_out); the inputs are left
+ * unchanged, n < 2^30.  A hand-written LSD radix sort (8-bit digits,
+ * digits shared by every key skipped, decoupled look-back); flatten_sort
+ * keeps rocPRIM's sort, which is faster at the benchmark sizes (reference:
+ * the cub::DeviceRadixSort::SortPairs call of FlattenSort,
+ * cuda/functions/arg_sort_coodrinates.cu:36-88). */
+int spira_hip_radix_sort_pairs(const void *keys_in, const int32_t *vals_in, void *keys_out, int32_t *vals_out,
+                               int64_t n, int key_bits, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Workspace bytes for spira_hip_downsample, _plan and _execute. */
 int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes);
 
