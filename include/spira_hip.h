@@ -248,7 +248,11 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
  *   offset_splits  blocks a row tile's kernel offsets are split over (fp32
  *                  partial sums in the workspace + a finalize pass);
  *   offset_pack    kernel offsets per step for 16-, 32- and 64-channel
- *                  inputs of kernels above 27 offsets: 1 (none), 2 or 4.
+ *                  inputs of kernels above 27 offsets: 1 (none), 2 or 4;
+ *   block_order    1: the blocks that the hardware sends to one XCD (one
+ *                  of 8 L2 slices) take one contiguous range of row tiles,
+ *                  so that each L2 serves a slab of the map; 0 (default):
+ *                  row tiles in dispatch order.
  * (No reference counterpart: these are the selector's CDNA4 parameters; the
  * reference selector sweeps gather / scatter tile sizes instead,
  * source/spira/nn/conv.py:217-307.) */
@@ -257,6 +261,7 @@ typedef struct {
   int step_channels;
   int offset_splits;
   int offset_pack;
+  int block_order;
 } spira_hip_os_tuning_t;
 
 /* Workspace bytes of spira_hip_conv_os: an fp32 [num_targets, c_out]
@@ -271,7 +276,8 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
  * concatenated form; has_map 0: the identity map) under `tuning`: plan[0..5]
  * = column tile (output channels), step channels, offset splits, kernel
  * offsets per step, grid x, grid y.  Runs on the host only.  (No reference
- * counterpart: it lets a caller or a test see what a tuning changes.) */
+ * counterpart: it lets a caller or a test see what a tuning changes.)  plan[6]
+ * = block order. */
 int spira_hip_conv_os_plan(int64_t num_targets, int num_offsets, int c_in, int c_in2, int c_out, int has_map,
                            int out_mode, const spira_hip_os_tuning_t *tuning, int32_t *plan);
 

@@ -636,6 +636,23 @@ __device__ __forceinline__ void store_tile_vec(const floatx4 (&acc)[2][2 * WN], 
 }
 
 
+// XCD-contiguous block order: the hardware hands workgroup w (in x, y, z
+// dispatch order) to XCD w % 8; remapped, the workgroups of XCD x take one
+// contiguous range of the logical (row tile, column tile, split) order,
+// column tiles innermost, so that the XCD's L2 serves one slab of rows (and
+// the column tiles of a row tile run on one XCD, close in time).
+__device__ __forceinline__ void xcd_block(int64_t &bx, int &by, int &bz) {
+  constexpr int64_t kXcds = 8;
+  const int64_t X = gridDim.x, Y = gridDim.y, Z = gridDim.z, G = X * Y * Z;
+  const int64_t w = blockIdx.x + X * (blockIdx.y + Y * static_cast<int64_t>(blockIdx.z));
+  const int64_t q = G / kXcds, r = G % kXcds, x = w % kXcds, i = w / kXcds;
+  const int64_t L = x * q + (x < r ? x : r) + i;  // a bijection of [0, G)
+  bz = static_cast<int>(L / (X * Y));
+  const int64_t rem = L % (X * Y);
+  bx = rem / Y;
+  by = static_cast<int>(rem % Y);
+}
+
 // Output-stationary implicit GEMM.  A block owns BM = 128 logical rows
 // (wave w: rows [32 w, 32 w + 32) as two 16-row MFMA tiles) and BN = 32*WN
 // output channels; grid = (row blocks, column blocks, offset splits), split z
@@ -647,7 +664,7 @@ template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
-                                                    Operands op, void *Y, Epilogue epi) {
+                                                    Operands op, void *Y, Epilogue epi, int xcd_order) {
   using C = typename ring::TileOf<WN, NKS>::C;
   constexpr int MT = C::BM / 128, NS = C::NS;
   __shared__ __align__(1024) char ring_lds[C::LDS];
@@ -662,9 +679,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   __shared__ int32_t orow_s[4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, kh = lane >> 5;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * C::BM;
-  const int n0 = blockIdx.y * C::BN;
-  const int j0 = blockIdx.z * jper;
+  int64_t bx = blockIdx.x;
+  int by = blockIdx.y, bz = blockIdx.z;
+  if (xcd_order) xcd_block(bx, by, bz);
+  const int64_t row0 = bx * C::BM;
+  const int n0 = by * C::BN;
+  const int j0 = bz * jper;
   const int jn = ((j0 + jper) < Kc ? (j0 + jper) : Kc) - j0;
   // offsets [j0, j0 + jn) used by some row of the block, relative to j0
   uint64_t ulo = jn >= 64 ? ~uint64_t(0) : (uint64_t(1) << jn) - 1;
@@ -1228,10 +1248,10 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
 template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
-                      void *Y, const Epilogue &epi) {
+                      void *Y, const Epilogue &epi, int xcd = 0) {
 #define SPIRA_OS_CALL(W)                                                                                             \
   hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
-                     jper, op, Y, epi)
+                     jper, op, Y, epi, xcd)
   SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
 #undef SPIRA_OS_CALL
 }
@@ -1289,6 +1309,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
   SPIRA_HIP_REQUIRE(t.offset_splits >= 0 && t.offset_splits <= 128, "conv_os tuning: offset_splits must be 0..128");
   SPIRA_HIP_REQUIRE(t.offset_pack == 0 || t.offset_pack == 1 || t.offset_pack == 2 || t.offset_pack == 4,
                     "conv_os tuning: offset_pack must be 0, 1, 2 or 4");
+  SPIRA_HIP_REQUIRE(t.block_order == 0 || t.block_order == 1, "conv_os tuning: block_order must be 0 or 1");
   return kOk;
 }
 
@@ -1296,7 +1317,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
 // block, offsets per split (jper), 16-channel slices per step (nks), kernel
 // offsets per step (pack: 1, 2 or 4) and the grid.
 struct OsPlan {
-  int wn, bm, jper, splits, nks, pack;
+  int wn, bm, jper, splits, nks, pack, xcd;
   bool aligned;
   int64_t gx, gy;
 };
@@ -1313,6 +1334,7 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
   pl.jper = choose_jper(pl.gx * pl.gy, Kc, cus, tn.offset_splits);
   pl.splits = static_cast<int>(div_up(Kc, pl.jper));
   pl.aligned = Cin % 8 == 0;
+  pl.xcd = tn.block_order;
   pl.nks = pl.aligned ? os_nks(CinP, pl.wn, pl.gx * pl.gy * pl.splits, cus, tn.step_channels) : 2;
   pl.pack = 1;
   // offset packing: 16- and 32-channel inputs of kernels with more than 27
@@ -1345,28 +1367,28 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
   const bool cat = op.X2 != nullptr;
   if constexpr (MODE == kStoreNative) {
     if (pl.pack == 4) {
-      if (nks == 4) launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      else launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      if (nks == 4) launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       return;
     }
     if (pl.pack == 2) {
-      if (nks == 2) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      else if (nks == 4) launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      else launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      if (nks == 2) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 4) launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       return;
     }
   }
-  if (!pl.aligned) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  if (!pl.aligned) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (cat) {
     // channel concatenations: storage-dtype outputs (split or not)
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
-      if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-      else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+      if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
     }
-  } else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-  else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
-  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi);
+  } else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
 }
 
 template <bool AL>
@@ -1477,6 +1499,7 @@ int spira_hip_conv_os_plan(int64_t num_targets, int num_offsets, int c_in, int c
   plan[3] = pl.pack;
   plan[4] = static_cast<int32_t>(pl.gx);
   plan[5] = static_cast<int32_t>(pl.gy);
+  plan[6] = pl.xcd;
   return kOk;
 }
 

@@ -251,21 +251,22 @@ static torch::Tensor zeroed_workspace(size_t bytes, const torch::Device &dev) {
 
 // A layer's output-stationary launch choices: the kernel's
 // (spira_hip_os_tuning_t, 0 = automatic) and the row order (-1 automatic,
-// 0 off, 1 on).  From Python: a 5-tuple (col_tile, step_channels,
-// offset_splits, offset_pack, row_order).
+// 0 off, 1 on).  From Python: a 6-tuple (col_tile, step_channels,
+// offset_splits, offset_pack, block_order, row_order).
 struct OsTune {
   spira_hip_os_tuning_t k{};
   int row_order = -1;
 };
-using TuneArg = std::optional<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>>;
+using TuneArg = std::optional<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t>>;
 static OsTune tune_of(const TuneArg &t) {
   OsTune r;
   if (!t.has_value()) return r;
-  auto [a, b, c, d, e] = *t;
+  auto [a, b, c, d, o, e] = *t;
   r.k.col_tile = static_cast<int>(a);
   r.k.step_channels = static_cast<int>(b);
   r.k.offset_splits = static_cast<int>(c);
   r.k.offset_pack = static_cast<int>(d);
+  r.k.block_order = static_cast<int>(o);
   r.row_order = static_cast<int>(e);
   SPIRA_CHECK_ARG(r.row_order >= -1 && r.row_order <= 1, "row_order must be -1, 0 or 1");
   return r;
@@ -661,16 +662,17 @@ float time_conv_os(int64_t S, int64_t T, const std::optional<torch::Tensor> &out
 }
 
 // The launch the output-stationary kernel would make (spira_hip_conv_os_plan):
-// (col_tile, step_channels, offset_splits, offsets_per_step, grid_x, grid_y).
+// (col_tile, step_channels, offset_splits, offsets_per_step, grid_x, grid_y,
+// block_order).
 // No reference counterpart: it shows what a layer's tuning changes.
 std::vector<int64_t> conv_os_plan(int64_t T, int64_t K, int64_t cin, int64_t cin2, int64_t cout, bool has_map,
                                   const TuneArg &tuning) {
   const OsTune tn = tune_of(tuning);
-  int32_t plan[6] = {};
+  int32_t plan[7] = {};
   check_rc(spira_hip_conv_os_plan(T, static_cast<int>(K), static_cast<int>(cin), static_cast<int>(cin2),
                                   static_cast<int>(cout), has_map ? 1 : 0, SPIRA_OUT_STORE, &tn.k, plan),
            "conv_os_plan");
-  return std::vector<int64_t>(plan, plan + 6);
+  return std::vector<int64_t>(plan, plan + 7);
 }
 
 // (reference: cuda_free_buffers / cuda_reset_error, torch/cuda_memory_buffer.cu:7-16)

@@ -152,7 +152,8 @@ class SparseConv(Module):
             "map_dataflow": 2,
             "force_os": False,
             # output-stationary launch choices (col_tile, step_channels,
-            # offset_splits, offset_pack, row_order); None = automatic
+            # offset_splits, offset_pack, block_order, row_order); None =
+            # automatic
             "os_tuning": None,
         }
         self._tuning_data = None
@@ -332,14 +333,14 @@ class SparseConv(Module):
 def os_candidates(c_in: int, c_out: int, volume: int) -> List[List[int]]:
     """Values tried per output-stationary launch field (0 = automatic):
     column tiles up to the output width, step channels up to the padded input
-    width, offset splits, and offset packing where it applies (16-, 32- and
-    64-channel inputs of kernels above 27 offsets)."""
+    width, offset splits, offset packing where it applies (16-, 32- and
+    64-channel inputs of kernels above 27 offsets), and the block order."""
     cin_p = (c_in + 15) // 16 * 16
     cols = [0] + [c for c in (32, 64, 96, 128) if c <= (c_out + 31) // 32 * 32]
     steps = [0, 32] + ([64] if cin_p >= 64 else []) + ([128] if cin_p >= 96 else [])
     splits = [0, 1, 2, 4] if volume > 1 else [0]
     packs = [0, 1, 2, 4] if (volume > 27 and cin_p in (16, 32, 64)) else [0]
-    return [cols, steps, splits, packs]
+    return [cols, steps, splits, packs, [0, 1]]
 
 
 def time_os_calls(layer: "SparseConv", calls, tuning: tuple, reps: int) -> float:
@@ -361,9 +362,9 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10) -> tuple:
     field in turn takes its fastest value with the others fixed, twice
     over; a value the library rejects is skipped."""
     cur = layer._tunable_config.get("os_tuning")
-    row_order = -1 if cur is None else int(cur[4])
+    row_order = -1 if cur is None else int(cur[5])
     cands = os_candidates(layer.in_channels, layer.out_channels, int(np.prod(layer.kernel_size)))
-    best = [0, 0, 0, 0]
+    best = [0, 0, 0, 0, 0]
 
     def cost(fields):
         try:

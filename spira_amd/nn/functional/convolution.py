@@ -112,14 +112,14 @@ def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sou
 
 
 def _tuning(tuning) -> Optional[tuple]:
-    """An output-stationary launch choice: None (automatic) or a 5-tuple
-    (col_tile, step_channels, offset_splits, offset_pack, row_order); 0 (and
-    -1 for row_order) in a field = automatic."""
+    """An output-stationary launch choice: None (automatic) or a 6-tuple
+    (col_tile, step_channels, offset_splits, offset_pack, block_order,
+    row_order); 0 (and -1 for row_order) in a field = automatic."""
     if tuning is None:
         return None
     t = tuple(int(v) for v in tuning)
-    if len(t) != 5:
-        raise ValueError(f"an output-stationary tuning has 5 fields, got {len(t)}")
+    if len(t) != 6:
+        raise ValueError(f"an output-stationary tuning has 6 fields, got {len(t)}")
     return t
 
 

@@ -252,16 +252,16 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10) -> 
             for r in (0, 1):
                 t = 0.0
                 for m, call in entries:
-                    cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, -1)
-                    t += time_os_calls(m, [call], tuple(cur[:4]) + (r,), reps)
+                    cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, 0, -1)
+                    t += time_os_calls(m, [call], tuple(cur[:5]) + (r,), reps)
                 totals[r] = t
             omap, T = entries[0][1][2], entries[0][1][1]
             totals[1] += _row_order_ms(omap, T)
             r = 1 if totals[1] < totals[0] else 0
             requests[key] = r
             for m, _ in entries:
-                cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, -1)
-                m._tunable_config["os_tuning"] = tuple(cur[:4]) + (r,)
+                cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, 0, -1)
+                m._tunable_config["os_tuning"] = tuple(cur[:5]) + (r,)
         if kernel_map_cache is not None:
             kernel_map_cache.row_order_requests.update(requests)
         return requests

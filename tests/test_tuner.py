@@ -47,7 +47,7 @@ def test_cache_file_round_trip(tmp_path):
     best = {g: DataflowConfig(i % 3, i % 2 == 1) for i, g in enumerate(groups)}
     for i, (n, m) in enumerate(_convs(model)):
         m._tunable_config.update(threshold=0.25 * (i % 4), gather_tile_size=8, scatter_tile_size=16,
-                                 os_tuning=(32 * (1 + i % 4), 64, i % 3, 1, i % 2))
+                                 os_tuning=(32 * (1 + i % 4), 64, i % 3, 1, i % 2, i % 2))
     path = os.path.join(tmp_path, "cfg", "tag.pt")
     requests = {((2, 2, 2), (2, 2, 2), (3, 3, 3)): 1}
     save_tuning_results(name_to_group, best, path, model, requests)
@@ -77,27 +77,28 @@ def test_os_tuning_changes_the_launch():
     from spira_amd.nn.functional import _native
     C = _native._C
     default = C.conv_os_plan(17044, 27, 256, 0, 256, True)
-    assert default == C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 0, 0, 0, -1))
-    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (96, 0, 0, 0, -1))[0] == 96
-    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (96, 0, 0, 0, -1))[5] == 3  # 256 / 96 column tiles
-    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 32, 0, 0, -1))[1] == 32
-    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 128, 0, 0, -1))[1] == 128
-    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 0, 3, 0, -1))[2] == 3
+    assert default == C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 0, 0, 0, 0, -1))
+    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (96, 0, 0, 0, 0, -1))[0] == 96
+    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (96, 0, 0, 0, 0, -1))[5] == 3  # 256 / 96 column tiles
+    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 32, 0, 0, 0, -1))[1] == 32
+    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 128, 0, 0, 0, -1))[1] == 128
+    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 0, 3, 0, 0, -1))[2] == 3
     # offset packing: 16-channel inputs of 125-offset kernels pack 4 by default
     assert C.conv_os_plan(300000, 125, 16, 0, 16, True)[3] == 4
-    assert C.conv_os_plan(300000, 125, 16, 0, 16, True, (0, 0, 0, 1, -1))[3] == 1
-    assert C.conv_os_plan(300000, 125, 16, 0, 16, True, (0, 0, 0, 2, -1))[3] == 2
+    assert C.conv_os_plan(300000, 125, 16, 0, 16, True, (0, 0, 0, 1, 0, -1))[3] == 1
+    assert C.conv_os_plan(300000, 125, 16, 0, 16, True, (0, 0, 0, 2, 0, -1))[3] == 2
     # (27-offset kernels never pack)
-    assert C.conv_os_plan(300000, 27, 16, 0, 16, True, (0, 0, 0, 4, -1))[3] == 1
+    assert C.conv_os_plan(300000, 27, 16, 0, 16, True, (0, 0, 0, 4, 0, -1))[3] == 1
+    assert C.conv_os_plan(17044, 27, 256, 0, 256, True, (0, 0, 0, 0, 1, -1))[6] == 1
     with pytest.raises(RuntimeError, match=r"\[Spira\].*col_tile"):
-        C.conv_os_plan(1000, 27, 32, 0, 32, True, (48, 0, 0, 0, -1))
+        C.conv_os_plan(1000, 27, 32, 0, 32, True, (48, 0, 0, 0, 0, -1))
 
 
 def test_os_candidates():
     from spira_amd.nn.conv import os_candidates
-    cols, steps, splits, packs = os_candidates(256, 256, 27)
-    assert cols == [0, 32, 64, 96, 128] and steps == [0, 32, 64, 128] and packs == [0]
-    cols, steps, splits, packs = os_candidates(16, 16, 125)
+    cols, steps, splits, packs, orders = os_candidates(256, 256, 27)
+    assert cols == [0, 32, 64, 96, 128] and steps == [0, 32, 64, 128] and packs == [0] and orders == [0, 1]
+    cols, steps, splits, packs, orders = os_candidates(16, 16, 125)
     assert cols == [0, 32] and steps == [0, 32] and packs == [0, 1, 2, 4]
     assert os_candidates(3, 32, 1)[2] == [0]
 
@@ -194,7 +195,7 @@ def test_os_tuning_keeps_results(dev, tmp_path):
                    n_samples=2, save_dir=str(tmp_path), tune_tag="os", allow_gs_tuning=False)
     tuned = [m for m in model.modules() if isinstance(m, spira_amd.nn.SparseConv)
              and m._tunable_config["os_tuning"] is not None]
-    assert len(tuned) >= 20 and all(len(m._tunable_config["os_tuning"]) == 5 for m in tuned)
+    assert len(tuned) >= 20 and all(len(m._tunable_config["os_tuning"]) == 6 for m in tuned)
     after = run()
     for a, b in zip(before, after):
         rms = float(a.pow(2).mean().sqrt()) or 1.0
