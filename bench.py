@@ -42,12 +42,37 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the dominant family's kernel, from rocprofv3 --pmc
-# FETCH_SIZE and --pmc WRITE_SIZE over `bench.py --only family,calib`, each
-# scaled by what the counter reads for the calibration leg's 256 MiB copy
-# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000; the command and the raw figures
-# are in profiles/).  None until measured for the current dominant kernel.
-DOMINANT_TRAFFIC_BYTES = None
+# HBM bytes per launch of each submanifold family's output-stationary kernel
+# (plus the finalize kernel of a launch with offset splits), at the tuned
+# launch the selector chose in the measured run: the family leg replays every
+# family 20 times back to back, and the counters are averaged over those
+# dispatches.  From rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE over
+# `bench.py --only e2e,family,calib --no-cpu --tune-dir D --steps 2
+# --warmup 1`, each scaled by what the counter reads for the calibration
+# leg's 256 MiB copy (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000).  The
+# commands, tunings and raw figures are in profiles/os_kernel_traffic.md; a
+# default run re-tunes and can choose other launches, whose traffic differs.
+MEASURED_TRAFFIC = {
+    "s1 3->32 K27": 58955866,  # FETCH 22432.5 KiB, WRITE 12709.2 KiB
+    "s1 32->32 K27": 82384608,  # FETCH 33868.9 KiB, WRITE 12715.9 KiB
+    "s1 96->96 K27": 177937101,  # FETCH 68093.0 KiB, WRITE 37580.7 KiB
+    "s1 128->96 K27": 188672141,  # FETCH 73335.4 KiB, WRITE 37579.3 KiB
+    "s2 32->32 K27": 93101069,  # FETCH 40618.7 KiB, WRITE 9681.6 KiB
+    "s2 96->96 K27": 238373446,  # FETCH 101965.5 KiB, WRITE 28855.5 KiB
+    "s2 128->96 K27": 253492176,  # FETCH 109375.4 KiB, WRITE 28800.1 KiB
+    "s4 32->64 K27": 28899328,  # FETCH 9880.6 KiB, WRITE 8460.9 KiB
+    "s4 64->64 K27": 40941530,  # FETCH 15760.5 KiB, WRITE 8460.9 KiB
+    "s4 128->128 K27": 104293747,  # FETCH 42463.8 KiB, WRITE 16921.8 KiB
+    "s4 192->128 K27": 167001728,  # FETCH 73082.9 KiB, WRITE 16921.8 KiB
+    "s8 64->128 K27": 21468160,  # FETCH 8352.0 KiB, WRITE 4261.0 KiB
+    "s8 128->128 K27": 18822016,  # FETCH 7059.9 KiB, WRITE 4261.0 KiB
+    "s8 256->256 K27": 49884784,  # FETCH 20084.4 KiB, WRITE 8546.9 KiB
+    "s8 384->256 K27": 73468358,  # FETCH 31588.8 KiB, WRITE 8568.9 KiB
+    "s16 128->256 K27": 28908800,  # FETCH 7122.6 KiB, WRITE 13986.0 KiB
+    "s16 256->256 K27": 42386432,  # FETCH 9707.5 KiB, WRITE 21978.0 KiB
+}
+# the same for the config-2 k=3 stride-1 map search (`--only kmap,calib`)
+KMAP_TRAFFIC = 16050790  # FETCH 2558.8 KiB, WRITE 10557.0 KiB
 
 
 def parse():
@@ -57,6 +82,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--dataflow", type=int, default=0, help="map dataflow of every layer without the selector")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    p.add_argument("--tune-dir", default=None,
+                   help="keep the selector's result in this folder and reuse it when present "
+                        "(profiler passes replay one selection instead of searching under the counters)")
     p.add_argument("--no-fuse", action="store_true", help="run batch norm / ReLU / residual adds unfused")
     p.add_argument("--no-tune", action="store_true", help="skip the selector (library default launch choices)")
     p.add_argument("--only", default="", help="comma list of legs: e2e, config5, kmap, layer, family (the "
@@ -125,6 +153,7 @@ class E2E:
         self.coords, self.feats = e2e_inputs(torch, coords_np, self.cin)
         self.dataflows = [args.dataflow] * len(self.ks)
         self.chosen = None
+        self.tune_dir = args.tune_dir
         self.randomise_norms()
 
     def randomise_norms(self, seed=42):
@@ -153,10 +182,11 @@ class E2E:
             x = spira_amd.SparseTensor(coordinates=self.coords, features=self.feats, double=True)
             return x.order()
 
-        with tempfile.TemporaryDirectory() as d:
+        with tempfile.TemporaryDirectory() as tmp:
+            d = self.tune_dir or tmp
             self.model, groups = spira_amd.tune(self.model, [sample() for _ in range(6)], self.cache,
                                                 map_dataflow_options=[0, 1, 2], test_force_os=False, n_samples=5,
-                                                save_dir=d, tune_tag=self.net, force_retune=True,
+                                                save_dir=d, tune_tag=self.net, force_retune=self.tune_dir is None,
                                                 allow_gs_tuning=False, return_dataflows=True)
         self.dataflows = [groups.get(g, d) for g, d in zip(layer_groups(self.net), self.dataflows)]
         self.chosen = {"map_dataflows": self.dataflows,
@@ -232,7 +262,8 @@ def per_layer_profile(torch, e2e: E2E, reps: int = 5):
             P = int((omap[:Tf] >= 0).sum().item()) if os_layout else int((omap[:, :Tf] >= 0).sum().item())
         meta[name] = {"S": S, "T": T, "P": P, "K": K, "stride": tuple(output._stride),
                       "cin": mod.in_channels, "cout": mod.out_channels,
-                      "dataflow": mod._tunable_config["map_dataflow"], "transposed": mod.transposed}
+                      "dataflow": mod._tunable_config["map_dataflow"], "transposed": mod.transposed,
+                      "tuning": mod._tunable_config.get("os_tuning")}
 
     handles = []
     for n, m in convs:
@@ -260,6 +291,10 @@ def per_layer_profile(torch, e2e: E2E, reps: int = 5):
     return rows
 
 
+def family_name(key):
+    return f"s{key[0]} {key[1]}->{key[2]} K{key[3]}"
+
+
 def family_roofline(rows):
     """Group the layers by (stride, C_in, C_out, offsets); the family with the
     largest in-network time per step is the dominant one.  Its roofline: the
@@ -282,13 +317,13 @@ def family_roofline(rows):
               "frac": tf / MFMA_F16_PEAK_TFLOPS}
     else:
         rl = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
-    rl.update({"traffic": DOMINANT_TRAFFIC_BYTES,
+    rl.update({"traffic": MEASURED_TRAFFIC.get(family_name(key)),
                "kernel": f"os_kernel family: stride {key[0]}, {key[1]} -> {key[2]} channels, {key[3]} offsets "
                          f"({f['launches']} launches per step, in-network)",
                "ms_per_step": f["ms"], "algorithmic_bytes_per_step": f["bytes"],
                "algorithmic_flops_per_step": f["flops"], "hbm_gbs": gbs, "mfma_tflops": tf,
                "mfma_frac": tf / MFMA_F16_PEAK_TFLOPS, "hbm_frac": gbs / HBM_PEAK_GBS})
-    fams = sorted(({"family": f"s{k[0]} {k[1]}->{k[2]} K{k[3]}", "ms": v["ms"], "launches": v["launches"],
+    fams = sorted(({"family": family_name(k), "key": k, "ms": v["ms"], "launches": v["launches"],
                     "mfma_frac": v["flops"] / (v["ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS,
                     "hbm_frac": v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS}
                    for k, v in fam.items()), key=lambda d: -d["ms"])
@@ -384,22 +419,34 @@ def layer_leg(torch, keys, channels=(16, 32, 64, 128, 256), reps=10):
     return {"pairs": P, "voxels": S, "per_C": out}
 
 
-def family_leg(torch, indoor_np, key, reps=20):
-    """The dominant family's layer shape alone (random features and weights
-    on the config-4 map of its stride), kernel-only back-to-back launches:
-    the launch the rocprofv3 counter runs read."""
+def family_leg(torch, indoor_np, rows, fams):
+    """Every submanifold family's layer shape alone (random features and
+    weights on the config-4 map of its stride, the in-network layer's tuned
+    launch and row order), in a fixed order (by stride, then channels): 1 warm
+    launch and 20 back-to-back launches each, the runs of identical dispatches
+    the rocprofv3 counter passes read."""
     from spira_amd.nn import functional as F
     from spira_amd.nn.functional import _native
     dev = torch.device("cuda:0")
-    stride, cin, cout, K = key
-    k = round(K ** (1 / 3))
+    out = {}
     keys, _ = F.flat_sort(torch.from_numpy(indoor_np).to(dev), True)
-    ks = keys if stride == 1 else F.downsample(keys, (stride,) * 3)
-    m = F.build_kmap(ks, ks, k, stride, 0)
-    X = torch.randn(ks.shape[0], cin, device=dev).half()
-    W = (torch.randn(K, cin, cout, device=dev) / np.sqrt(K * cin)).half()
-    ms = _native._C.time_conv_os(ks.shape[0], ks.shape[0], m[2], X, W, reps)
-    return {"kernel_ms": ms, "T": int(ks.shape[0])}
+    for key in sorted(f["key"] for f in fams):
+        stride, cin, cout, K = key
+        layer = next(r for r in rows if (r["stride"][0], r["cin"], r["cout"], r["K"]) == key)
+        if K != 27 or layer["transposed"] or layer["S"] != layer["T"]:
+            continue
+        ks = keys if stride == 1 else F.downsample(keys, (stride,) * 3)
+        m = F.build_kmap(ks, ks, 3, stride, 0)
+        T = int(ks.shape[0])
+        X = torch.randn(T, cin, device=dev).half()
+        W = (torch.randn(K, cin, cout, device=dev) / np.sqrt(K * cin)).half()
+        tuning = layer["tuning"]
+        ms = _native._C.time_conv_os(T, T, m[2], X, W, 20, tuning=tuning)
+        plan = _native._C.conv_os_plan(T, K, cin, 0, cout, True, tuning)
+        out[family_name(key)] = {"kernel_ms": ms, "T": T, "grid": [plan[4], plan[5]],
+                                 "tuning": list(tuning) if tuning else None,
+                                 "traffic": MEASURED_TRAFFIC.get(family_name(key))}
+    return out
 
 
 def calib_leg(torch, mib=256, reps=5):
@@ -465,7 +512,7 @@ def main():
         if args.layer_table:
             write_layer_table(args.layer_table, rows, ms)
         if "family" in legs:
-            res["family_kernel"] = family_leg(torch, indoor, fkey)
+            res["family_kernels"] = family_leg(torch, indoor, rows, fams)
         if not args.no_cpu:
             # the same network, weights and input features through the oracle
             # (fp32) on the host cores, timed; outputs checked against the GPU's
@@ -501,7 +548,7 @@ def main():
         res["kmap_build_us"] = km["k3s1"]["api_us"]
         res["kmap_kernel_us"] = km["k3s1"]["kernel_us"]
         res["kmap_roofline"] = {"bound": "hbm", "achieved": km["k3s1"]["gbs"], "peak": HBM_PEAK_GBS,
-                                "unit": "GB/s", "frac": km["k3s1"]["frac"], "traffic": None,
+                                "unit": "GB/s", "frac": km["k3s1"]["frac"], "traffic": KMAP_TRAFFIC,
                                 "kernel": "kmap_search_kernel<u64,3,3,0> (config 2, k=3, stride 1, OS layout)",
                                 "algorithmic_bytes": km["k3s1"]["algorithmic_bytes"]}
         if not args.no_cpu:

@@ -235,9 +235,20 @@ def test_wide_window_fallback(dev):
         assert_tuple_equal(got, orc.build_kmap(rk, rt, (3, 3, 3), (1, 1, 1), d), f"wide d={d}")
 
 
-def test_streamed_build_matches_single(dev, scene_small):
-    """Network-wide build (UNet layer list) equals per-layer builds."""
+@pytest.mark.parametrize("concurrent", [False, True])
+def test_streamed_build_matches_single(dev, scene_small, concurrent):
+    """Network-wide build (UNet layer list) equals per-layer builds, also
+    with every map on a side stream of its own (the opt-in fan-out)."""
+    from spira_amd.nn.functional import _native
     rk, tk = _keys(scene_small, 64, dev)
+    _native._C.set_concurrent_maps(concurrent)
+    try:
+        _check_streamed(tk)
+    finally:
+        _native._C.set_concurrent_maps(False)
+
+
+def _check_streamed(tk):
     target_strides = [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)]
     voxels = [tk] + list(F.streamed_output_generate(tk, target_strides))
     ks = [(3, 3, 3), (2, 2, 2)] * 4 + [(3, 3, 3)]
