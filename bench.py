@@ -90,6 +90,8 @@ def parse():
     p.add_argument("--only", default="", help="comma list of legs: e2e, config5, kmap, layer, family (the "
                                               "dominant family's layers alone, for counters), calib (a plain "
                                               "256 MiB device copy: the reference point of the HBM counters)")
+    p.add_argument("--concurrent-maps", action="store_true",
+                   help="build every layer map on a side stream of its own (the library's opt-in fan-out)")
     p.add_argument("--layer-table", default="", help="write the per-layer in-network table (markdown) here")
     return p.parse_args()
 
@@ -477,6 +479,9 @@ def main():
     from spira_amd import scenes
     from spira_amd.nn import functional as F
 
+    if args.concurrent_maps:
+        from spira_amd.nn.functional import _native
+        _native._C.set_concurrent_maps(True)
     legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer", "config5"}
     with open(os.path.join(ROOT, "BASELINE.json")) as f:
         baseline = json.load(f)
@@ -488,7 +493,7 @@ def main():
            "data": "synthetic (seeded scenes, random-init weights)"}
     cfg = {"workload": "config4: SparseResUNet42 fp16, 200k-voxel indoor scene, end-to-end "
                        "(order + network-wide kernel maps + forward; selector run before timing)",
-           "voxels": int(indoor.shape[0]), "key_bits": 64}
+           "voxels": int(indoor.shape[0]), "key_bits": 64, "concurrent_maps": bool(args.concurrent_maps)}
     cpu = {}
     e2e = None
     if "e2e" in legs or "family" in legs:
