@@ -357,12 +357,16 @@ def time_os_calls(layer: "SparseConv", calls, tuning: tuple, reps: int) -> float
     return total
 
 
-def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10) -> tuple:
+def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Optional[int] = None,
+                     with_time: bool = False):
     """Coordinate search over the launch fields of ``os_candidates``: each
     field in turn takes its fastest value with the others fixed, twice
-    over; a value the library rejects is skipped."""
-    cur = layer._tunable_config.get("os_tuning")
-    row_order = -1 if cur is None else int(cur[5])
+    over; a value the library rejects is skipped.  The row-order field is
+    held at `row_order` (default: the layer's current one, else -1, the
+    library's rule).  Returns the tuning (and its time with `with_time`)."""
+    if row_order is None:
+        cur = layer._tunable_config.get("os_tuning")
+        row_order = -1 if cur is None else int(cur[5])
     cands = os_candidates(layer.in_channels, layer.out_channels, int(np.prod(layer.kernel_size)))
     best = [0, 0, 0, 0, 0]
 
@@ -384,4 +388,5 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10) -> tuple:
                 t = cost(trial)
                 if t < best_t:
                     best, best_t = trial, t
-    return tuple(best) + (row_order,)
+    tuning = tuple(best) + (row_order,)
+    return (tuning, best_t) if with_time else tuning

@@ -196,7 +196,7 @@ def _forward_once(model: Module, kernel_map_cache, sample) -> None:
     torch.cuda.synchronize()
 
 
-def tune_os(model: Module, kernel_map_cache, sample, reps: int = 10) -> None:
+def tune_os(model: Module, kernel_map_cache, sample, reps: int = 10, verbose: bool = False) -> None:
     """Output-stationary launch choices of every fp16 layer that runs the
     output-stationary kernel (``SparseConv.tune_os``), from one forward pass
     of `sample`, then the row order per map (``tune_row_orders``)."""
@@ -206,7 +206,7 @@ def tune_os(model: Module, kernel_map_cache, sample, reps: int = 10) -> None:
             if isinstance(m, SparseConv):
                 stack.enter_context(m.tune_os(reps))
         _forward_once(model, kernel_map_cache, sample)
-    tune_row_orders(model, kernel_map_cache, sample, reps)
+    tune_row_orders(model, kernel_map_cache, sample, reps, verbose)
 
 
 def _row_order_ms(omap: torch.Tensor, num_targets: int, reps: int = 5) -> float:
@@ -224,14 +224,17 @@ def _row_order_ms(omap: torch.Tensor, num_targets: int, reps: int = 5) -> float:
     return a.elapsed_time(b) / reps
 
 
-def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10) -> Dict[Tuple, int]:
+def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
+                    verbose: bool = False) -> Dict[Tuple, int]:
     """Walk each output-stationary map (27..128 offsets, non-transposed
     layers) in row order or not, whichever is faster for the layers that read
-    it, counting the order's sort once per map.  Sets every such layer's
-    row-order field and the cache's request for the map; returns the
-    requests."""
+    it, counting the order's sort once per map.  The launch choices depend on
+    the order (a row-ordered walk skips more offsets and prefers other step
+    and tile sizes), so each layer's launch is searched again under both
+    orders.  Sets every such layer's tuning and the cache's request for the
+    map; returns the requests."""
     SparseConv = _sparse_conv_cls()
-    from ..nn.conv import time_os_calls
+    from ..nn.conv import choose_os_tuning
     convs = [m for m in model.modules() if isinstance(m, SparseConv)]
     for m in convs:
         m._os_tuning_data = []
@@ -248,20 +251,21 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10) -> 
                 by_map[key].append((m, call))
         requests: Dict[Tuple, int] = {}
         for key, entries in by_map.items():
-            totals = {}
+            totals, picks = {}, {}
             for r in (0, 1):
-                t = 0.0
-                for m, call in entries:
-                    cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, 0, -1)
-                    t += time_os_calls(m, [call], tuple(cur[:5]) + (r,), reps)
-                totals[r] = t
+                picks[r] = [choose_os_tuning(m, [call], reps, row_order=r, with_time=True) for m, call in entries]
+                totals[r] = sum(t for _, t in picks[r])
             omap, T = entries[0][1][2], entries[0][1][1]
             totals[1] += _row_order_ms(omap, T)
             r = 1 if totals[1] < totals[0] else 0
             requests[key] = r
-            for m, _ in entries:
-                cur = m._tunable_config.get("os_tuning") or (0, 0, 0, 0, 0, -1)
-                m._tunable_config["os_tuning"] = tuple(cur[:5]) + (r,)
+            if verbose:
+                print(f"[Spira] map {key}: {len(entries)} layers, {1e3 * totals[0]:.1f} us in index order, "
+                      f"{1e3 * totals[1]:.1f} us in row order (sort included) -> row order {r}")
+                for (m, _), (t0, ms0), (t1, ms1) in zip(entries, picks[0], picks[1]):
+                    print(f"    {m.in_channels}->{m.out_channels}: {t0} {1e3 * ms0:.1f} us | {t1} {1e3 * ms1:.1f} us")
+            for (m, _), (tuning, _) in zip(entries, picks[r]):
+                m._tunable_config["os_tuning"] = tuning
         if kernel_map_cache is not None:
             kernel_map_cache.row_order_requests.update(requests)
         return requests
@@ -376,7 +380,7 @@ def tune(model: Module, data_loader: Iterable, kernel_map_cache=None, map_datafl
     apply_tuned_configs(model, name_to_group, best, None)
     requests: Dict[Tuple, int] = {}
     if allow_os_tuning and samples and torch.cuda.is_available():
-        tune_os(model, kernel_map_cache, samples[0])
+        tune_os(model, kernel_map_cache, samples[0], verbose=verbose)
         if kernel_map_cache is not None:
             requests = dict(kernel_map_cache.row_order_requests)
     save_tuning_results(name_to_group, best, save_path, model, requests)
