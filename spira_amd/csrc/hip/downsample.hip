@@ -592,21 +592,12 @@ __device__ __forceinline__ int64_t lb_row(const CT *__restrict__ in, int64_t lo,
   return row_key<CT>(x, y, k) ? key_lower_bound(in, lo, n, k) : n;
 }
 
+// Rank of key i in its output run by binary searches over the whole input
+// (any ratios); -1 if the ranks cannot be formed (unsorted input).
 template <typename CT>
-__global__ __launch_bounds__(256) void chain_merge_kernel(const CT *__restrict__ in, const uint32_t *__restrict__ n_dev,
-                                                          int64_t n_cap, CT mask, uint32_t ax, uint32_t ay, int rx,
-                                                          int ry, CT *__restrict__ merged,
-                                                          uint32_t *__restrict__ unsorted) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
-  if (i >= n) return;
-  const CT key = in[i];
-  if (unsorted && i > 0 && in[i - 1] > key) atomicOr(unsorted, 1u);
+__device__ int64_t chain_rank_search(const CT *__restrict__ in, int64_t n, int64_t i, CT key, CT mask, uint32_t ax,
+                                     uint32_t ay, int rx, int ry) {
   const CT k = key & mask;
-  if (rx == 1 && ry == 1) {  // one row per run: the masked keys are in order already
-    merged[i] = k;
-    return;
-  }
   const uint64_t x = static_cast<uint64_t>((key >> Layout<CT>::XS) & Layout<CT>::XONES);
   const uint64_t y = static_cast<uint64_t>((key >> Layout<CT>::YS) & Layout<CT>::YONES);
   const uint64_t x0 = x & ~(static_cast<uint64_t>(ax) * rx - 1);
@@ -635,9 +626,223 @@ __global__ __launch_bounds__(256) void chain_merge_kernel(const CT *__restrict__
     if (q < own) rank += masked_bound<CT, true>(in, rs[q], re[q], mask, k) - rs[q];
     else if (q > own) rank += masked_bound<CT, false>(in, rs[q], re[q], mask, k) - rs[q];
   }
+  return rank;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_merge_kernel(const CT *__restrict__ in, const uint32_t *__restrict__ n_dev,
+                                                          int64_t n_cap, CT mask, uint32_t ax, uint32_t ay, int rx,
+                                                          int ry, CT *__restrict__ merged,
+                                                          uint32_t *__restrict__ unsorted) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  if (i >= n) return;
+  const CT key = in[i];
+  if (unsorted && i > 0 && in[i - 1] > key) atomicOr(unsorted, 1u);
+  const CT k = key & mask;
+  if (rx == 1 && ry == 1) {  // one row per run: the masked keys are in order already
+    merged[i] = k;
+    return;
+  }
+  const int64_t rank = chain_rank_search<CT>(in, n, i, key, mask, ax, ay, rx, ry);
   // A sorted input makes the ranks a permutation of [0, n); unsorted input
   // (reported through `unsorted` at level 1) can push them out of range, and
   // such a key is dropped rather than written out of bounds.
+  if (rank < 0 || rank >= n) {
+    if (unsorted) atomicOr(unsorted, 1u);
+    return;
+  }
+  merged[rank] = k;
+}
+
+// ----- x-tables: the columns (keys of one x) of a level's sorted input
+//
+// xs[c] / xe[c] = first / one-past-last position of column x = xmin + c * ax
+// (xmin: the x of the first key, ax: the level's input stride), for c <
+// kXtCap.  Only present columns are written; a reader accepts an entry only
+// if the keys around its two ends show that it bounds exactly column x, so
+// stale entries (absent columns, earlier levels) are never used.  With
+// sorted input the entries of present columns are always fresh.
+constexpr int64_t kXtCap = int64_t(1) << 16;
+
+template <typename CT> __device__ __forceinline__ uint64_t key_x(CT k) {
+  return static_cast<uint64_t>((k >> Layout<CT>::XS) & Layout<CT>::XONES);
+}
+
+// table slot of column x, or -1 (x below xmin, off the stride grid, past
+// the table)
+__device__ __forceinline__ int64_t xt_slot(uint64_t x, uint64_t xmin, uint32_t ax) {
+  if (x < xmin) return -1;
+  const uint64_t d = x - xmin;
+  if (d % ax != 0) return -1;
+  const uint64_t c = d / ax;
+  return c < static_cast<uint64_t>(kXtCap) ? static_cast<int64_t>(c) : -1;
+}
+
+// the level-1 table from the input keys (stride 1)
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_xtable_kernel(const CT *__restrict__ in, int64_t n,
+                                                           int32_t *__restrict__ xs, int32_t *__restrict__ xe) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t x = key_x(in[i]);
+  const int64_t c = xt_slot(x, key_x(in[0]), 1u);
+  if (c < 0) return;
+  if (i == 0 || key_x(in[i - 1]) != x) xs[c] = static_cast<int32_t>(i);
+  if (i == n - 1 || key_x(in[i + 1]) != x) xe[c] = static_cast<int32_t>(i + 1);
+}
+
+// Column x of `in` from the table: true with [c, e) if the table holds it.
+template <typename CT>
+__device__ __forceinline__ bool xt_column(const CT *__restrict__ in, int64_t n, const int32_t *__restrict__ xs,
+                                          const int32_t *__restrict__ xe, int64_t slot, uint64_t x, int64_t &c,
+                                          int64_t &e) {
+  c = xs[slot];
+  e = xe[slot];
+  if (c < 0 || c >= n || e <= c || e > n) return false;
+  if (key_x(in[c]) != x || (c > 0 && key_x(in[c - 1]) == x)) return false;
+  return key_x(in[e - 1]) == x && (e == n || key_x(in[e]) != x);
+}
+
+// First position in [lo, hi) whose key is >= v, for two ranges at once
+// (their loads overlap).  With GALLOP the probes first step from lo in
+// doubling strides (the answer is expected near lo: a row's end from its
+// start), then bisect once a probe reaches v; the answer stays in
+// [lo, lo + len] and len shrinks every round.
+template <typename CT, bool GALLOP>
+__device__ __forceinline__ void lower_bound2(const CT *__restrict__ a, int64_t (&lo)[2], const int64_t (&hi)[2],
+                                             const CT (&v)[2]) {
+  int64_t len[2] = {hi[0] - lo[0], hi[1] - lo[1]};
+  int64_t step[2] = {GALLOP ? 1 : 0, GALLOP ? 1 : 0};  // 0: bisecting
+  while (len[0] > 0 || len[1] > 0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (len[t] > 0) {
+        const int64_t h = step[t] > 0 ? (step[t] < len[t] ? step[t] : len[t]) - 1 : len[t] >> 1;
+        if (a[lo[t] + h] < v[t]) {
+          lo[t] += h + 1;
+          len[t] -= h + 1;
+          step[t] <<= 1;
+        } else {
+          len[t] = h;
+          step[t] = 0;
+        }
+      }
+    }
+  }
+}
+
+// Per row q of a run [rs[q], re[q]) (masked keys non-decreasing): the
+// number of keys ordered before masked key k of row `own` (ties go to the
+// earlier row), all four rows' galloping searches side by side.
+template <typename CT>
+__device__ __forceinline__ int64_t masked_counts4(const CT *__restrict__ a, const int64_t (&rs)[4],
+                                                  const int64_t (&re)[4], int own, CT mask, CT k) {
+  int64_t lo[4], len[4], step[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    lo[q] = rs[q];
+    len[q] = q == own ? 0 : re[q] - rs[q];
+    step[q] = 1;
+  }
+  while (len[0] > 0 || len[1] > 0 || len[2] > 0 || len[3] > 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (len[q] > 0) {
+        const int64_t h = step[q] > 0 ? (step[q] < len[q] ? step[q] : len[q]) - 1 : len[q] >> 1;
+        const CT w = a[lo[q] + h] & mask;
+        if (q < own ? (w <= k) : (w < k)) {
+          lo[q] += h + 1;
+          len[q] -= h + 1;
+          step[q] <<= 1;
+        } else {
+          len[q] = h;
+          step[q] = 0;
+        }
+      }
+    }
+  }
+  int64_t c = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) c += q == own ? 0 : lo[q] - rs[q];
+  return c;
+}
+
+// Level merge for x and y ratios of 2 (the networks' chains): the run's four
+// rows are found inside their columns, which the x-table gives, with the two
+// columns searched side by side; a key whose columns lie past the table
+// takes the whole-input searches.
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_merge2_kernel(const CT *__restrict__ in, const uint32_t *__restrict__ n_dev,
+                                                           int64_t n_cap, CT mask, uint32_t ax, uint32_t ay,
+                                                           const int32_t *__restrict__ xs,
+                                                           const int32_t *__restrict__ xe, CT *__restrict__ merged,
+                                                           uint32_t *__restrict__ unsorted) {
+  constexpr int RX = 2, RY = 2;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  if (i >= n) return;
+  const CT key = in[i];
+  if (unsorted && i > 0 && in[i - 1] > key) atomicOr(unsorted, 1u);
+  const CT k = key & mask;
+  const uint64_t x = key_x(key);
+  const uint64_t y = static_cast<uint64_t>((key >> Layout<CT>::YS) & Layout<CT>::YONES);
+  const uint64_t x0 = x & ~(static_cast<uint64_t>(ax) * RX - 1);
+  const uint64_t y0 = y & ~(static_cast<uint64_t>(ay) * RY - 1);
+  const int oxi = static_cast<int>((x - x0) / ax);
+  const int own = oxi * RY + static_cast<int>((y - y0) / ay);
+  const uint64_t xmin = key_x(in[0]);
+  int64_t cs[RX] = {0, 0}, ce[RX] = {0, 0};
+  bool present[RX] = {false, false};
+  bool known = true;
+#pragma unroll
+  for (int ix = 0; ix < RX; ++ix) {
+    const uint64_t xi = x0 + static_cast<uint64_t>(ix) * ax;
+    if (xi < xmin) continue;  // below the first key: absent
+    const int64_t slot = xt_slot(xi, xmin, ax);
+    if (slot < 0) {
+      known = false;
+      continue;
+    }
+    present[ix] = xt_column<CT>(in, n, xs, xe, slot, xi, cs[ix], ce[ix]);
+    if (!present[ix]) cs[ix] = ce[ix] = 0;
+  }
+  int64_t rank;
+  if (!known) {
+    rank = chain_rank_search<CT>(in, n, i, key, mask, ax, ay, RX, RY);
+  } else if (!present[oxi]) {
+    rank = -1;  // the key's own column is not where sorted input puts it
+  } else {
+    int64_t b[RX] = {cs[0], cs[1]};
+    CT v[RX];
+#pragma unroll
+    for (int ix = 0; ix < RX; ++ix)
+      v[ix] = static_cast<CT>(((x0 + static_cast<uint64_t>(ix) * ax) << Layout<CT>::XS) | (y0 << Layout<CT>::YS));
+    lower_bound2<CT, false>(in, b, ce, v);  // absent columns: empty ranges
+    int64_t pos = present[0] ? cs[0] : cs[1];  // keys of columns before x0
+#pragma unroll
+    for (int ix = 0; ix < RX; ++ix) pos += b[ix] - cs[ix];  // keys of column xi with y < y0
+    int64_t rs[RX * RY], re[RX * RY];
+#pragma unroll
+    for (int iy = 0; iy < RY; ++iy) {
+      const uint64_t yn = y0 + static_cast<uint64_t>(iy + 1) * ay;
+#pragma unroll
+      for (int ix = 0; ix < RX; ++ix) {
+        rs[ix * RY + iy] = b[ix];
+        v[ix] = static_cast<CT>(((x0 + static_cast<uint64_t>(ix) * ax) << Layout<CT>::XS) |
+                                ((yn > Layout<CT>::YONES ? 0 : yn) << Layout<CT>::YS));
+      }
+      if (yn > Layout<CT>::YONES) {
+#pragma unroll
+        for (int ix = 0; ix < RX; ++ix) b[ix] = ce[ix];  // the rows run to the column's end
+      } else {
+        lower_bound2<CT, true>(in, b, ce, v);
+      }
+#pragma unroll
+      for (int ix = 0; ix < RX; ++ix) re[ix * RY + iy] = b[ix];
+    }
+    rank = pos + (i - rs[own]) + masked_counts4<CT>(in, rs, re, own, mask, k);
+  }
   if (rank < 0 || rank >= n) {
     if (unsorted) atomicOr(unsorted, 1u);
     return;
@@ -654,15 +859,28 @@ __global__ __launch_bounds__(256) void chain_flag_kernel(const CT *__restrict__ 
   flags[p] = (p < n && (p == 0 || merged[p] != merged[p - 1])) ? 1u : 0u;
 }
 
+// Unique keys to the level's output, and the next level's x-table (stride
+// ax_next) from the merged keys: a column starts at the first unique key of
+// a new x and ends after the last merged key of that x.
 template <typename CT>
 __global__ __launch_bounds__(256) void chain_compact_kernel(const CT *__restrict__ merged,
                                                             const uint32_t *__restrict__ flags,
-                                                            const uint32_t *__restrict__ pos, int64_t n_cap,
-                                                            CT *__restrict__ out, uint32_t *__restrict__ count) {
+                                                            const uint32_t *__restrict__ pos,
+                                                            const uint32_t *__restrict__ n_dev, int64_t n_cap,
+                                                            CT *__restrict__ out, uint32_t *__restrict__ count,
+                                                            uint32_t ax_next, int32_t *__restrict__ xs,
+                                                            int32_t *__restrict__ xe) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n_cap) return;
   if (flags[p]) out[pos[p]] = merged[p];
   if (p == n_cap - 1) *count = pos[p] + flags[p];
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  if (!xs || p >= n) return;
+  const uint64_t x = key_x(merged[p]);
+  const int64_t c = xt_slot(x, key_x(merged[0]), ax_next);
+  if (c < 0) return;
+  if (flags[p] && (p == 0 || key_x(merged[p - 1]) != x)) xs[c] = static_cast<int32_t>(pos[p]);
+  if (p == n - 1 || key_x(merged[p + 1]) != x) xe[c] = static_cast<int32_t>(pos[p] + flags[p]);
 }
 
 static size_t chain_scan_bytes(int64_t n) {
@@ -675,6 +893,7 @@ static size_t chain_scan_bytes(int64_t n) {
 template <typename CT> struct ChainParts {
   CT *merged;
   uint32_t *flags, *pos;
+  int32_t *xs, *xe;  // x-table of the current level's input
   void *temp;
   size_t temp_bytes, total;
 };
@@ -691,6 +910,8 @@ template <typename CT> static ChainParts<CT> chain_parts(int64_t n, void *base) 
   p.merged = reinterpret_cast<CT *>(take(n * sizeof(CT)));
   p.flags = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
   p.pos = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
+  p.xs = reinterpret_cast<int32_t *>(take(kXtCap * sizeof(int32_t)));
+  p.xe = reinterpret_cast<int32_t *>(take(kXtCap * sizeof(int32_t)));
   p.temp_bytes = chain_scan_bytes(n);
   p.temp = take(p.temp_bytes);
   p.total = off;
@@ -729,23 +950,30 @@ static int chain_impl(const CT *keys, int64_t n, int levels, const int32_t *stri
                     "downsample_chain: workspace too small");
   ChainParts<CT> p = chain_parts<CT>(n, ws);
   const dim3 grid(static_cast<unsigned>(div_up(n, 256)));
+  hipLaunchKernelGGL(chain_xtable_kernel<CT>, grid, dim3(256), 0, s, keys, n, p.xs, p.xe);
+  SPIRA_HIP_LAUNCH_CHECK();
   int a[3] = {1, 1, 1};
   for (int l = 0; l < levels; ++l) {
     const int *b = strides + 3 * l;
     const CT *in = l == 0 ? keys : static_cast<const CT *>(outs[l - 1]);
     const uint32_t *n_dev = l == 0 ? nullptr : d_counts + (l - 1);
     const CT mask = stride_mask<CT>(b[0], b[1], b[2]);
-    hipLaunchKernelGGL(chain_merge_kernel<CT>, grid, dim3(256), 0, s, in, n_dev, n, mask,
-                       static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]), b[0] / a[0], b[1] / a[1], p.merged,
-                       l == 0 ? d_unsorted : nullptr);
+    if (b[0] / a[0] == 2 && b[1] / a[1] == 2)
+      hipLaunchKernelGGL(chain_merge2_kernel<CT>, grid, dim3(256), 0, s, in, n_dev, n, mask,
+                         static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]), p.xs, p.xe, p.merged,
+                         l == 0 ? d_unsorted : nullptr);
+    else
+      hipLaunchKernelGGL(chain_merge_kernel<CT>, grid, dim3(256), 0, s, in, n_dev, n, mask,
+                         static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]), b[0] / a[0], b[1] / a[1], p.merged,
+                         l == 0 ? d_unsorted : nullptr);
     SPIRA_HIP_LAUNCH_CHECK();
     hipLaunchKernelGGL(chain_flag_kernel<CT>, grid, dim3(256), 0, s, p.merged, n_dev, n, p.flags);
     SPIRA_HIP_LAUNCH_CHECK();
     size_t tb = p.temp_bytes;
     SPIRA_HIP_TRY(rocprim::exclusive_scan(p.temp, tb, p.flags, p.pos, 0u, static_cast<size_t>(n),
                                           rocprim::plus<uint32_t>(), s));
-    hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.flags, p.pos, n,
-                       static_cast<CT *>(outs[l]), d_counts + l);
+    hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.flags, p.pos, n_dev, n,
+                       static_cast<CT *>(outs[l]), d_counts + l, static_cast<uint32_t>(b[0]), p.xs, p.xe);
     SPIRA_HIP_LAUNCH_CHECK();
     for (int q = 0; q < 3; ++q) a[q] = b[q];
   }
