@@ -578,6 +578,93 @@ __global__ __launch_bounds__(256) void row_mask_kernel(const int32_t *__restrict
   iota[row0 + threadIdx.x] = static_cast<int32_t>(row0 + threadIdx.x);
 }
 
+// ----- row order of maps of at most 8 offsets: a counting sort
+//
+// With K <= 8 the (count, column mask) key has at most 256 values, so the
+// stable sort by (count descending, mask ascending) is one counting pass:
+// per-tile bucket counts, one exclusive scan of them in (bucket, tile)
+// order (rocPRIM), and a stable scatter.  Bucket of mask m = its place in that order
+// (the masks with more columns first).
+constexpr int kSmallRowsPerTile = 1024;  // 256 threads x 4 rows
+
+// bucket of every 8-bit mask, built per block in LDS
+__device__ __forceinline__ void small_bucket_table(uint8_t *rank_s) {
+  const int m = threadIdx.x;  // blockDim.x == 256
+  const int c = __builtin_popcount(m);
+  int r = 0;
+  for (int v = 0; v < 256; ++v) {
+    const int cv = __builtin_popcount(v);
+    r += (cv > c) || (cv == c && v < m);
+  }
+  rank_s[m] = static_cast<uint8_t>(r);
+}
+
+__device__ __forceinline__ int small_mask(const int32_t *__restrict__ map, int64_t row, int K) {
+  int m = 0;
+  for (int j = 0; j < K; ++j) m |= (map[row * K + j] >= 0 ? 1 : 0) << j;
+  return m;
+}
+
+// hist[b * ntiles + tile] = rows of the tile in bucket b
+__global__ __launch_bounds__(256) void small_hist_kernel(const int32_t *__restrict__ map, int64_t T, int K,
+                                                         int64_t ntiles, int32_t *__restrict__ hist) {
+  __shared__ uint8_t rank_s[256];
+  __shared__ int cnt_s[256];
+  small_bucket_table(rank_s);
+  cnt_s[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t tile = blockIdx.x;
+#pragma unroll
+  for (int q = 0; q < kSmallRowsPerTile / 256; ++q) {
+    const int64_t row = tile * kSmallRowsPerTile + q * 256 + threadIdx.x;
+    if (row < T) atomicAdd(&cnt_s[rank_s[small_mask(map, row, K)]], 1);
+  }
+  __syncthreads();
+  hist[static_cast<int64_t>(threadIdx.x) * ntiles + tile] = cnt_s[threadIdx.x];
+}
+
+// sorted[offs[b * ntiles + tile] + (rank of the row among the tile's rows of
+// bucket b)] = row; rows keep their order within a bucket (row quarters in
+// turn, then waves, then lanes)
+__global__ __launch_bounds__(256) void small_scatter_kernel(const int32_t *__restrict__ map, int64_t T, int K,
+                                                            int64_t ntiles, const int32_t *__restrict__ offs,
+                                                            int32_t *__restrict__ sorted) {
+  __shared__ uint8_t rank_s[256];
+  __shared__ int base_s[256];
+  __shared__ int wcnt_s[4][256];
+  small_bucket_table(rank_s);
+  base_s[threadIdx.x] = 0;
+  const int64_t tile = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  for (int q = 0; q < kSmallRowsPerTile / 256; ++q) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) wcnt_s[w][threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t row = tile * kSmallRowsPerTile + q * 256 + threadIdx.x;
+    const bool valid = row < T;
+    const int b = valid ? rank_s[small_mask(map, row, K)] : 0;
+    // lanes of the wave with the same bucket (eight ballots on its bits)
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t m = __ballot(valid && ((b >> bit) & 1));
+      peers &= ((b >> bit) & 1) ? m : ~m;
+    }
+    const int rank = __builtin_popcountll(peers & below);
+    if (valid && (peers >> lane) == 1) wcnt_s[wave][b] = rank + 1;  // the last lane of the group
+    __syncthreads();
+    if (valid) {
+      int pos = offs[static_cast<int64_t>(b) * ntiles + tile] + base_s[b] + rank;
+      for (int w = 0; w < wave; ++w) pos += wcnt_s[w][b];
+      sorted[pos] = static_cast<int32_t>(row);
+    }
+    __syncthreads();
+    base_s[threadIdx.x] += wcnt_s[0][threadIdx.x] + wcnt_s[1][threadIdx.x] + wcnt_s[2][threadIdx.x] +
+                           wcnt_s[3][threadIdx.x];
+  }
+}
+
 // Per group of 128 sorted rows: the 128-bit union of their valid columns
 // (gm[g * 2 + w]) and a sort key that puts the groups with the most columns
 // first (128 - popcount) and keeps a trailing partial group last (255).
@@ -777,7 +864,11 @@ static RowOrderParts row_order_parts(int64_t T, void *base) {
                                   static_cast<uint32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
                                   static_cast<int32_t *>(nullptr), static_cast<size_t>(G), 0, 8);
   RowOrderParts r{};
-  r.tmp_bytes = std::max(std::max(b1, b2), b3);
+  const int64_t small_counts = 256 * ((T + kSmallRowsPerTile - 1) / kSmallRowsPerTile);
+  size_t b4 = 0;
+  (void)rocprim::exclusive_scan(nullptr, b4, static_cast<const int32_t *>(nullptr), static_cast<int32_t *>(nullptr), 0,
+                                static_cast<size_t>(small_counts), rocprim::plus<int32_t>());
+  r.tmp_bytes = std::max(std::max(std::max(b1, b2), b3), b4);
   char *p = static_cast<char *>(base);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -785,8 +876,11 @@ static RowOrderParts row_order_parts(int64_t T, void *base) {
     off += (bytes + 255) / 256 * 256;
     return q;
   };
-  r.keys = reinterpret_cast<uint64_t *>(take(T * sizeof(uint64_t)));
-  r.keys_out = reinterpret_cast<uint64_t *>(take(T * sizeof(uint64_t)));
+  // (also the bucket counts of the counting sort of maps of <= 8 offsets
+  // and their scan: 256 per 1024-row tile)
+  const size_t kb = std::max<size_t>(T * sizeof(uint64_t), small_counts * sizeof(int32_t));
+  r.keys = reinterpret_cast<uint64_t *>(take(kb));
+  r.keys_out = reinterpret_cast<uint64_t *>(take(kb));
   r.iota = reinterpret_cast<int32_t *>(take(T * sizeof(int32_t)));
   r.sorted = reinterpret_cast<int32_t *>(take(T * sizeof(int32_t)));
   r.gm = reinterpret_cast<uint64_t *>(take(G * 2 * sizeof(uint64_t)));
@@ -918,6 +1012,26 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
   SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= row_order_parts(num_targets, nullptr).total,
                     "kmap_row_order: workspace too small");
   RowOrderParts w = row_order_parts(num_targets, workspace);
+  if (num_offsets <= 8) {
+    // counting sort (bucket counts in w.keys, their scan in w.keys_out),
+    // then the rows in that order with their 128-row column unions
+    const int64_t ntiles = div_up(num_targets, kSmallRowsPerTile);
+    int32_t *hist = reinterpret_cast<int32_t *>(w.keys), *offs = reinterpret_cast<int32_t *>(w.keys_out);
+    hipLaunchKernelGGL(small_hist_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(256), 0, stream, out_in_map,
+                       num_targets, num_offsets, ntiles, hist);
+    SPIRA_HIP_LAUNCH_CHECK();
+    size_t stb = w.tmp_bytes;
+    SPIRA_HIP_TRY(rocprim::exclusive_scan(w.tmp, stb, hist, offs, 0, static_cast<size_t>(256 * ntiles),
+                                          rocprim::plus<int32_t>(), stream));
+    hipLaunchKernelGGL(small_scatter_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(256), 0, stream, out_in_map,
+                       num_targets, num_offsets, ntiles, offs, w.sorted);
+    SPIRA_HIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(order_rows_kernel, dim3(div_up(num_targets, 256)), dim3(256), 0, stream, out_in_map, w.sorted,
+                       static_cast<const int32_t *>(nullptr), num_targets, num_offsets, order, ordered_map,
+                       static_cast<const uint64_t *>(nullptr), group_masks);
+    SPIRA_HIP_LAUNCH_CHECK();
+    return kOk;
+  }
   const int rb = num_offsets <= 32 ? 256 : 64;
   SPIRA_HIP_REQUIRE(static_cast<size_t>(rb) * num_offsets * sizeof(int32_t) <= 64 * 1024,
                     "kmap_row_order: at most 256 offsets");

@@ -291,7 +291,9 @@ class SparseConv(Module):
                 y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue, sources2=x2,
                                                     tuning=cfg.get("os_tuning"))
                 if self._os_tuning_data is not None:
-                    mkey = None if self.transposed else (tuple(inputs._stride), tuple(stride), self.kernel_size)
+                    mkey = (tuple(inputs._stride), tuple(stride), self.kernel_size)
+                    if self.transposed:  # the transpose of the forward layer's map (its own row order)
+                        mkey = ("transposed",) + mkey
                     self._os_tuning_data.append((S, T, m[2], x, x2, mkey))
             elif d == 1:
                 y = F.sparse_convolution_forward_ws_merged(S, T, x, self.kernel, m[5], m[6], m[3], m[7], m[8],

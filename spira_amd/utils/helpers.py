@@ -210,12 +210,16 @@ def tune_os(model: Module, kernel_map_cache, sample, reps: int = 10, verbose: bo
 
 
 def _row_order_ms(omap: torch.Tensor, num_targets: int, reps: int = 5) -> float:
-    """Time (ms) to compute a map's row order (on fresh copies: the order is
-    cached per map tensor)."""
+    """GPU time (ms) to compute a map's row order (on fresh copies: the order
+    is cached per map tensor).  The calls are queued behind a short GPU wait,
+    so that the host's work per call (allocations, launches) overlaps the
+    GPU as it does inside a network's map build, and only device time is
+    counted."""
     from ..nn.functional import _native
     copies = [omap.clone() for _ in range(reps)]
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(2_000_000)  # ~1 ms of GPU clock cycles: longer than the host's queueing
     a.record()
     for c in copies:
         _native._C.kmap_row_order(c, int(num_targets))
@@ -226,9 +230,10 @@ def _row_order_ms(omap: torch.Tensor, num_targets: int, reps: int = 5) -> float:
 
 def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
                     verbose: bool = False) -> Dict[Tuple, int]:
-    """Walk each output-stationary map (27..128 offsets, non-transposed
-    layers) in row order or not, whichever is faster for the layers that read
-    it, counting the order's sort once per map.  The launch choices depend on
+    """Walk each output-stationary map (8..128 offsets; a transposed layer's
+    map is a map of its own) in row order or not, whichever is faster for
+    the layers that read it, counting the order's sort once per map.  The
+    launch choices depend on
     the order (a row-ordered walk skips more offsets and prefers other step
     and tile sizes), so each layer's launch is searched again under both
     orders.  Sets every such layer's tuning and the cache's request for the
@@ -246,7 +251,7 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
                 continue
             for call in m._os_tuning_data:
                 omap, key = call[2], call[5]
-                if omap is None or key is None or not (27 <= omap.shape[1] <= 128):
+                if omap is None or key is None or not (8 <= omap.shape[1] <= 128):
                     continue
                 by_map[key].append((m, call))
         requests: Dict[Tuple, int] = {}

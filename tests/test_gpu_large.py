@@ -205,3 +205,61 @@ def test_offset_packing_variants(dev, pack):
                        timeout=150)
     assert r.returncode == 0, r.stderr[-2000:]
     assert float(r.stdout.split("WORST")[-1]) <= 1e-2
+
+
+def _check_small_row_order(m, T, order, masks, omap):
+    """Maps of <= 8 offsets: the order is exactly the stable sort of the rows
+    by (neighbour count descending, column mask ascending), with the map rows
+    and the exact 128-row column unions in that order."""
+    K = m.shape[1]
+    valid = m[:T] >= 0
+    key = ((K - valid.sum(1)) << K) | (valid * (1 << np.arange(K))).sum(1)
+    assert np.array_equal(order, np.argsort(key, kind="stable"))
+    assert np.array_equal(omap, m[order])
+    G = (T + 127) // 128
+    v = np.zeros((G * 128, K), bool)
+    v[:T] = valid[order]
+    union = (v.reshape(G, 128, K).any(1) * (1 << np.arange(K))).sum(1)
+    assert np.array_equal(masks.view(np.uint64).reshape(G, 2)[:, 0], union.astype(np.uint64))
+    assert not masks.view(np.uint64).reshape(G, 2)[:, 1].any()
+
+
+def test_row_order_k2_maps(dev, indoor):
+    """The k = 2 down-sampling map of the config-4 scene and its transpose
+    (one valid entry per row: the counting-sort path)."""
+    from spira_amd.nn.functional._native import _C
+    k = indoor[0]
+    k2 = orc.downsample(k, (2, 2, 2))
+    m = np.ascontiguousarray(orc.build_kmap(k, k2, (2, 2, 2), (1, 1, 1), 0)[2])
+    for mm, T in ((m, len(k2)), (np.ascontiguousarray(orc.convert_transposed_os(m, len(k))), len(k))):
+        order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(mm).to(dev), T))
+        _check_small_row_order(mm, T, order, masks, omap)
+
+
+@pytest.mark.parametrize("T,K", [(1, 8), (1000, 8), (1024, 8), (1025, 4), (5000, 8), (70000, 2)])
+def test_row_order_small_maps(dev, T, K):
+    """Random maps of <= 8 offsets around the 1024-row tiles of the counting sort."""
+    from spira_amd.nn.functional._native import _C
+    rng = np.random.default_rng(T + K)
+    m = np.where(rng.random((T, K)) < 0.4, rng.integers(0, 1000, (T, K)), -1).astype(np.int32)
+    order, masks, omap = (np_(t) for t in _C.kmap_row_order(torch.from_numpy(m).to(dev), T))
+    _check_small_row_order(m, T, order, masks, omap)
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_ordered_k2_layer(dev, indoor, transposed):
+    """A k = 2 stride-2 layer and its transpose walked in row order (the
+    layer's tuning asks for it) against the oracle."""
+    k = indoor[0]
+    k2 = orc.downsample(k, (2, 2, 2))
+    m = orc.build_kmap(k, k2, (2, 2, 2), (1, 1, 1), 0)[2]
+    S, T = len(k), len(k2)
+    if transposed:
+        m, S, T = orc.convert_transposed_os(m, S), T, S
+    X, W = _case(S, 96, 96, dev, seed=11)
+    W = W[:8].contiguous()
+    md = torch.from_numpy(np.ascontiguousarray(m)).to(dev)
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    for rows in (1, 0):
+        y = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=(0, 0, 0, 0, 0, rows))
+        assert rel_err(np_(y.float()), ref) <= 1e-2, rows
