@@ -701,33 +701,39 @@ __global__ __launch_bounds__(256) void group_union_keys_kernel(const KT *__restr
 
 // Stable counting sort of the G group keys (values < 256): gperm = the
 // group ids by key.  The block stages the keys in LDS and builds their
-// histogram; then one wave scans it and walks chunks of 64 keys in order,
-// each lane placed at its bin's running base plus its rank among the
-// chunk's lanes with the same key (peer masks from eight ballots); the
-// highest lane of each key advances the base.
+// histogram per quarter of the groups; one wave scans it in (key, quarter)
+// order; then each wave walks its quarter in chunks of 64 keys, each lane
+// placed at its bin's running base plus its rank among the chunk's lanes
+// with the same key (peer masks from eight ballots); the highest lane of
+// each key advances the base.
 constexpr int kGroupOrderMax = 49152;
 __global__ __launch_bounds__(256) void group_order_kernel(const uint32_t *__restrict__ gkey, int G,
                                                           int32_t *__restrict__ gperm) {
-  __shared__ int base_s[256];
+  // the four waves rank one contiguous quarter of the groups each; a key's
+  // places start at its base plus its count in the quarters before
+  __shared__ int base_s[4][256];
   __shared__ uint8_t key_s[kGroupOrderMax];
-  base_s[threadIdx.x] = 0;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int qlen = (G + 3) / 4;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) base_s[w][threadIdx.x] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < G; i += 256) {
     const uint32_t k = gkey[i] & 255;
     key_s[i] = static_cast<uint8_t>(k);
-    atomicAdd(&base_s[k], 1);
+    atomicAdd(&base_s[i / qlen][k], 1);
   }
   __syncthreads();
-  if (threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
-  {
-    // exclusive scan: lane l owns bins 4l .. 4l+3
-    int c[4], t = 0;
+  if (wave == 0) {
+    // bases: exclusive scan over (key, quarter); lane l owns keys 4l .. 4l+3
+    int c[4][4], t = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c[q] = base_s[lane * 4 + q];
-      t += c[q];
-    }
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        c[q][w] = base_s[w][lane * 4 + q];
+        t += c[q][w];
+      }
     int incl = t;
     for (int o = 1; o < 64; o <<= 1) {
       const int v = __shfl_up(incl, o, 64);
@@ -735,16 +741,20 @@ __global__ __launch_bounds__(256) void group_order_kernel(const uint32_t *__rest
     }
     int run = incl - t;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      base_s[lane * 4 + q] = run;
-      run += c[q];
-    }
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        base_s[w][lane * 4 + q] = run;
+        run += c[q][w];
+      }
   }
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
   const uint64_t below = (uint64_t(1) << lane) - 1;
-  for (int c0 = 0; c0 < G; c0 += 64) {
+  const int q0 = wave * qlen, q1 = (q0 + qlen) < G ? (q0 + qlen) : G;
+  int *base = base_s[wave];
+  for (int c0 = q0; c0 < q1; c0 += 64) {
     const int i = c0 + lane;
-    const bool valid = i < G;
+    const bool valid = i < q1;
     const int k = valid ? static_cast<int>(key_s[i]) : 0;
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -752,11 +762,11 @@ __global__ __launch_bounds__(256) void group_order_kernel(const uint32_t *__rest
       const uint64_t b = __ballot(valid && ((k >> bit) & 1));
       peers &= ((k >> bit) & 1) ? b : ~b;
     }
-    const int pos = valid ? base_s[k] + __popcll(peers & below) : 0;
+    const int pos = valid ? base[k] + __popcll(peers & below) : 0;
     __builtin_amdgcn_wave_barrier();
     if (valid) {
       gperm[pos] = i;
-      if ((peers >> lane) == 1) base_s[k] += __popcll(peers);  // the highest lane of its key
+      if ((peers >> lane) == 1) base[k] += __popcll(peers);  // the highest lane of its key
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -798,20 +808,33 @@ __global__ __launch_bounds__(256) void order_rows_kernel(const int32_t *__restri
     const int dr = 256 / K, dc = 256 - dr * K;
     int r = static_cast<int>(threadIdx.x) / K, c = static_cast<int>(threadIdx.x) - r * K;
     int32_t *dst = ordered ? ordered + row0 * K : nullptr;
-#pragma unroll 4
-    for (int e = threadIdx.x; e < ni; e += 256) {
-      const int32_t v = map[static_cast<int64_t>(src_s[r]) * K + c];
-      if (ordered) dst[e] = v;
-      if (reduce && v >= 0 && c < 128) {
-        const int gi = r >= 128 ? 1 : 0;
-        if (c < 64) m[gi][0] |= uint64_t(1) << c;
-        else m[gi][1] |= uint64_t(1) << (c - 64);
+    // U elements per round: all U loads are issued before the first store,
+    // so that a thread keeps U row gathers in flight
+    constexpr int U = 8;
+    for (int e0 = threadIdx.x; e0 < ni; e0 += 256 * U) {
+      int32_t v[U];
+      int cu[U], ru[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ru[u] = r;
+        cu[u] = c;
+        v[u] = (e0 + u * 256 < ni) ? map[static_cast<int64_t>(src_s[r]) * K + c] : -1;
+        r += dr;
+        c += dc;
+        if (c >= K) {
+          c -= K;
+          ++r;
+        }
       }
-      r += dr;
-      c += dc;
-      if (c >= K) {
-        c -= K;
-        ++r;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (e0 + u * 256 >= ni) continue;
+        if (ordered) dst[e0 + u * 256] = v[u];
+        if (reduce && v[u] >= 0 && cu[u] < 128) {
+          const int gi = ru[u] >= 128 ? 1 : 0;
+          if (cu[u] < 64) m[gi][0] |= uint64_t(1) << cu[u];
+          else m[gi][1] |= uint64_t(1) << (cu[u] - 64);
+        }
       }
     }
   }
