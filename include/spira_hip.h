@@ -143,6 +143,25 @@ int spira_hip_kmap_search(const void *sources, int64_t num_sources, const void *
                           int key_bits, int kx, int ky, int kz, int sx, int sy, int sz, int layout,
                           const int32_t *row_perm, int32_t *kernel_map, int32_t *tile_counts, hipStream_t stream);
 
+/* One output-stationary search (layout SPIRA_KMAP_OS, no row permutation, no
+ * tile counts) of a batch. */
+typedef struct {
+  const void *sources;
+  int64_t num_sources;
+  const void *targets;
+  int64_t num_targets;
+  int kx, ky, kz, sx, sy, sz;
+  int32_t *kernel_map; /* [round_up(num_targets, 128), kx*ky*kz] */
+} spira_hip_kmap_job_t;
+
+/* The n searches of `jobs` (keys of key_bits bits), each exactly as
+ * spira_hip_kmap_search with layout SPIRA_KMAP_OS: maps of one kernel shape
+ * (2x2x2 or 3x3x3) share a launch, so that the searches of a network's maps
+ * overlap; other shapes run one launch each.  (Replaces the per-layer
+ * BinarySearch_kz_ostationary launches of BinarySearchStreamed<CT>,
+ * torch/cuda_sparse_convolution_mapping.cu:894-1645.) */
+int spira_hip_kmap_search_batch(int n, const spira_hip_kmap_job_t *jobs, int key_bits, hipStream_t stream);
+
 /* Workspace bytes for spira_hip_kmap_scan over num_counts tile counts. */
 int spira_hip_kmap_scan_workspace(int64_t num_counts, size_t *bytes);
 

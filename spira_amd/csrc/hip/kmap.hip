@@ -110,10 +110,12 @@ enum SearchLayout : int {
   kLayoutNoz = 2,  // [Tp, K], column k, full offsets and no z-scan (KZ = 1)
 };
 
-// GS: offsets per dx-group when known at compile time (the dy range of the
-// common kernels), else 0 (runtime p.GS, in chunks of kChunk).
-template <typename CT, int KZ, int GS, int LAYOUT>
-__global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const SearchParams<CT> p) {
+// The search of one 64-target tile (one block).  GS: offsets per dx-group
+// when known at compile time (the dy range of the common kernels), else 0
+// (runtime p.GS, in chunks of kChunk).  P: SearchParams or SearchJob (the
+// fields the tile reads).
+template <typename CT, int KZ, int GS, int LAYOUT, class P>
+__device__ __forceinline__ void search_tile(const P &p, const int64_t tile) {
   constexpr int kChunk = GS > 0 ? GS : 4;
   extern __shared__ __align__(16) char smem[];
   const int g = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // dx-group of this wave
@@ -122,7 +124,6 @@ __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const Searc
   int32_t *stage = reinterpret_cast<int32_t *>(smem + p.G * kWindowCap * sizeof(CT));
 
   const int lane = threadIdx.x & 63;
-  const int64_t tile = blockIdx.x;
   const int64_t t = tile * 64 + lane;
   const bool valid = t < p.T;
   // level-1 samples of the sources (independent of the queries, so this load
@@ -309,6 +310,43 @@ __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const Searc
   }
 }
 
+template <typename CT, int KZ, int GS, int LAYOUT>
+__global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const SearchParams<CT> p) {
+  search_tile<CT, KZ, GS, LAYOUT>(p, blockIdx.x);
+}
+
+// Several output-stationary maps of one kernel shape in one launch: job j
+// owns tiles [tile_start[j], tile_start[j + 1]) of the grid, so that the
+// searches of a network's small maps overlap instead of running back to back.
+constexpr int kJobOffsets = 27;  // kernel volumes up to 3 x 3 x 3
+constexpr int kJobsMax = 8;
+template <typename CT> struct SearchJob {
+  const CT *src;
+  const CT *tgt;
+  int32_t *map;
+  int32_t *tile_counts;  // (unused: the output-stationary layout has none)
+  int64_t S, T, Tp, ntiles;
+  int G, GS, O, K;
+  int use_perm;
+  CT sz;
+  CT off[kJobOffsets];
+};
+template <typename CT> struct SearchBatch {
+  int n;
+  int64_t tile_start[kJobsMax + 1];
+  SearchJob<CT> job[kJobsMax];
+};
+
+static_assert(sizeof(SearchBatch<uint64_t>) <= 4096, "batch parameters must fit the kernel argument block");
+
+template <typename CT, int KZ, int GS>
+__global__ __launch_bounds__(64 * kGroupMax) void kmap_search_batch_kernel(const SearchBatch<CT> b) {
+  const int64_t tile = blockIdx.x;
+  int j = 0;
+  for (int q = 1; q < b.n; ++q) j = tile >= b.tile_start[q] ? q : j;
+  search_tile<CT, KZ, GS, kLayoutOsZ>(b.job[j], tile - b.tile_start[j]);
+}
+
 template <typename CT> static void make_offsets(int kx, int ky, int kz, int sx, int sy, int sz, bool full, CT *out) {
   // offset tables of torch/cuda_sparse_convolution_mapping.cu:10-50 (xy only,
   // z pinned to kz_min*sz) and :114-157 (full): x outer, y, z inner; packed
@@ -418,6 +456,71 @@ static int search_impl(const CT *src, int64_t S, const CT *tgt, int64_t T, int k
   const int lay = layout == SPIRA_KMAP_NOZ ? kLayoutNoz : (p.os_layout ? kLayoutOsZ : kLayoutWs);
   launch_search<CT>(KZ, p.GS, lay, grid, block, lds, stream, p);
   SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+// Batched output-stationary searches: jobs of the kernel shapes that have a
+// batch kernel (2x2x2, 3x3x3) are grouped by shape, at most kJobsMax per
+// launch, in their order; every other job is one search_impl call.
+template <typename CT>
+static int search_batch_impl(int n, const spira_hip_kmap_job_t *jobs, hipStream_t stream) {
+  std::vector<char> done(static_cast<size_t>(n), 0);
+  auto batchable = [](const spira_hip_kmap_job_t &j) {
+    return (j.kx == 2 && j.ky == 2 && j.kz == 2) || (j.kx == 3 && j.ky == 3 && j.kz == 3);
+  };
+  for (int a = 0; a < n; ++a) {
+    if (done[a]) continue;
+    const spira_hip_kmap_job_t &ja = jobs[a];
+    if (!batchable(ja)) {
+      done[a] = 1;
+      const int rc = search_impl<CT>(static_cast<const CT *>(ja.sources), ja.num_sources,
+                                     static_cast<const CT *>(ja.targets), ja.num_targets, ja.kx, ja.ky, ja.kz, ja.sx,
+                                     ja.sy, ja.sz, SPIRA_KMAP_OS, nullptr, ja.kernel_map, nullptr, stream);
+      if (rc) return rc;
+      continue;
+    }
+    SearchBatch<CT> b{};
+    int64_t tiles = 0;
+    for (int c = a; c < n && b.n < kJobsMax; ++c) {
+      const spira_hip_kmap_job_t &jc = jobs[c];
+      if (done[c] || jc.kx != ja.kx || jc.ky != ja.ky || jc.kz != ja.kz) continue;
+      SPIRA_HIP_REQUIRE(jc.num_sources >= 0 && jc.num_targets >= 0 && jc.num_sources < (int64_t(1) << 31) &&
+                            jc.num_targets < (int64_t(1) << 31),
+                        "kmap_search_batch: sizes out of range");
+      SPIRA_HIP_REQUIRE(jc.kernel_map != nullptr && (jc.num_targets == 0 || jc.targets != nullptr) &&
+                            (jc.num_sources == 0 || jc.sources != nullptr),
+                        "kmap_search_batch: missing array");
+      done[c] = 1;
+      SearchJob<CT> &p = b.job[b.n];
+      p.src = static_cast<const CT *>(jc.sources);
+      p.tgt = static_cast<const CT *>(jc.targets);
+      p.map = jc.kernel_map;
+      p.tile_counts = nullptr;
+      p.S = jc.num_sources;
+      p.T = jc.num_targets;
+      p.Tp = round_up(p.T, 128);
+      p.ntiles = p.Tp / 64;
+      p.K = jc.kx * jc.ky * jc.kz;
+      p.G = jc.kx;
+      p.GS = jc.ky;
+      p.O = jc.kx * jc.ky;
+      p.use_perm = 0;
+      p.sz = static_cast<CT>(static_cast<uint32_t>(jc.sz));
+      make_offsets<CT>(jc.kx, jc.ky, jc.kz, jc.sx, jc.sy, jc.sz, false, p.off);
+      b.tile_start[b.n] = tiles;
+      tiles += p.ntiles;
+      ++b.n;
+    }
+    b.tile_start[b.n] = tiles;
+    if (tiles == 0) continue;
+    SPIRA_HIP_REQUIRE(tiles < (int64_t(1) << 31), "kmap_search_batch: too many tiles");
+    const int K = ja.kx * ja.ky * ja.kz;
+    const size_t lds = ja.kx * kWindowCap * sizeof(CT) + 64 * K * sizeof(int32_t);
+    const dim3 grid(static_cast<unsigned>(tiles)), block(64 * ja.kx);
+    if (ja.kz == 2) hipLaunchKernelGGL((kmap_search_batch_kernel<CT, 2, 2>), grid, block, lds, stream, b);
+    else hipLaunchKernelGGL((kmap_search_batch_kernel<CT, 3, 3>), grid, block, lds, stream, b);
+    SPIRA_HIP_LAUNCH_CHECK();
+  }
   return kOk;
 }
 
@@ -940,6 +1043,13 @@ int spira_hip_kmap_search(const void *sources, int64_t num_sources, const void *
   return search_impl<uint32_t>(static_cast<const uint32_t *>(sources), num_sources,
                                static_cast<const uint32_t *>(targets), num_targets, kx, ky, kz, sx, sy, sz, layout,
                                row_perm, kernel_map, tile_counts, stream);
+}
+
+int spira_hip_kmap_search_batch(int n, const spira_hip_kmap_job_t *jobs, int key_bits, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "kmap_search_batch: key_bits must be 32 or 64");
+  SPIRA_HIP_REQUIRE(n >= 0 && (n == 0 || jobs != nullptr), "kmap_search_batch: bad job list");
+  if (key_bits == 64) return search_batch_impl<uint64_t>(n, jobs, stream);
+  return search_batch_impl<uint32_t>(n, jobs, stream);
 }
 
 int spira_hip_kmap_scan_workspace(int64_t num_counts, size_t *bytes) {

@@ -52,8 +52,11 @@ static void check_keys(const torch::Tensor &src, const torch::Tensor &tgt) {
 }
 
 // half: -1 = automatic (S == T and K odd), 0 = never, 1 = when K odd
+// `job` (dataflow 0 only, may be null): the search is not launched but
+// described there, for a caller that batches the searches of several maps.
 static PendingMap stage_map(const torch::Tensor &src, const torch::Tensor &tgt, const Int3 &ksize,
-                            const Int3 &sstride, int dataflow, int half, hipStream_t stream) {
+                            const Int3 &sstride, int dataflow, int half, hipStream_t stream,
+                            spira_hip_kmap_job_t *job = nullptr) {
   check_keys(src, tgt);
   SPIRA_CHECK_ARG(dataflow >= 0 && dataflow <= 8, "dataflow must be in [0, 8]");
   const auto dev = src.device();
@@ -71,6 +74,11 @@ static PendingMap stage_map(const torch::Tensor &src, const torch::Tensor &tgt, 
 
   if (dataflow == 0) {
     pm.map = empty_i32({pm.Tp, K}, dev);
+    if (job) {
+      *job = spira_hip_kmap_job_t{src.data_ptr(), pm.S, tgt.data_ptr(), pm.T, kx, ky, kz, sx, sy, sz,
+                                  pm.map.data_ptr<int32_t>()};
+      return pm;
+    }
     check_rc(spira_hip_kmap_search(src.data_ptr(), pm.S, tgt.data_ptr(), pm.T, bits, kx, ky, kz, sx, sy, sz,
                                    SPIRA_KMAP_OS, nullptr, pm.map.data_ptr<int32_t>(), nullptr, stream),
              "binary_search");
@@ -206,18 +214,27 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
   auto stream_of = [&](size_t i) {
     return (concurrent_maps() || dataflow[i] != 0) ? fan[side_of[i]] : cur;
   };
+  // output-stationary maps on the current stream: their searches are
+  // batched into one launch per kernel shape, after every map is allocated
+  std::vector<spira_hip_kmap_job_t> jobs;
   for (size_t i = 0; i < n; ++i) {
     // half maps: dataflow 2 uses the position in the list (mapping.cu:1129),
     // the other dataflows compare the set sizes (mapping.cu:955)
     const int half = (dataflow[i] == 2) ? (i % 2 == 0 ? 1 : 0) : -1;
+    const bool batched = dataflow[i] == 0 && !concurrent_maps();
+    spira_hip_kmap_job_t job{};
     pending[i] = stage_map(voxels[i / 2], voxels[(i + 1) / 2], kernel_sizes[i], source_strides[i], dataflow[i],
-                           half, stream_of(i));
+                           half, stream_of(i), batched ? &job : nullptr);
+    if (batched) jobs.push_back(job);
     if (dataflow[i] % 2 == 1) {
       SPIRA_CHECK_ARG(hipMemcpyAsync(sizes_host.data_ptr<int32_t>() + 2 * i, pending[i].sizes.data_ptr<int32_t>(),
                                      2 * sizeof(int32_t), hipMemcpyDeviceToHost, stream_of(i)) == hipSuccess,
                       "size read-back failed");
     }
   }
+  if (!jobs.empty())
+    check_rc(spira_hip_kmap_search_batch(static_cast<int>(jobs.size()), jobs.data(), key_bits_of(voxels[0]), cur),
+             "binary_search_streamed");
   // Odd dataflows need their pair counts on the host; hybrid dataflows above
   // 4 transpose their dense part on the current stream in finish_map, so the
   // side stream that wrote the map must be complete first.
