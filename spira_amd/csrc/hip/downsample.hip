@@ -547,7 +547,8 @@ static int downsample_impl(const CT *keys, int64_t n, int sx, int sy, int sz, CT
 // runs) plus its index in its own row plus, per other row of the run, the
 // number of that row's keys ordered before it (ties go to the earlier row);
 // all by binary searches over the sorted input.  Duplicates are then
-// adjacent: a flag + scan + compaction leaves the sorted unique keys.
+// adjacent: a scan of the run starts (computed from the merged keys as the
+// scan reads them) and a compaction leave the sorted unique keys.
 // ---------------------------------------------------------------------------
 constexpr int kChainMaxRows = 16;  // input rows per output run and level
 
@@ -850,21 +851,26 @@ __global__ __launch_bounds__(256) void chain_merge2_kernel(const CT *__restrict_
   merged[rank] = k;
 }
 
+// Merged key p starts a run of equal keys (the unique keys of the level):
+// read by the scan straight from the merged keys and again by the
+// compaction, so no flag array is written.
+template <typename CT> struct ChainFirst {
+  const CT *merged;
+  const uint32_t *n_dev;
+  int64_t n_cap;
+  __host__ __device__ uint32_t operator()(int64_t p) const {
+    const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+    return (p < n && (p == 0 || merged[p] != merged[p - 1])) ? 1u : 0u;
+  }
+};
 template <typename CT>
-__global__ __launch_bounds__(256) void chain_flag_kernel(const CT *__restrict__ merged, const uint32_t *__restrict__ n_dev,
-                                                         int64_t n_cap, uint32_t *__restrict__ flags) {
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (p >= n_cap) return;
-  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
-  flags[p] = (p < n && (p == 0 || merged[p] != merged[p - 1])) ? 1u : 0u;
-}
+using ChainFlags = rocprim::transform_iterator<rocprim::counting_iterator<int64_t>, ChainFirst<CT>, uint32_t>;
 
 // Unique keys to the level's output, and the next level's x-table (stride
 // ax_next) from the merged keys: a column starts at the first unique key of
 // a new x and ends after the last merged key of that x.
 template <typename CT>
 __global__ __launch_bounds__(256) void chain_compact_kernel(const CT *__restrict__ merged,
-                                                            const uint32_t *__restrict__ flags,
                                                             const uint32_t *__restrict__ pos,
                                                             const uint32_t *__restrict__ n_dev, int64_t n_cap,
                                                             CT *__restrict__ out, uint32_t *__restrict__ count,
@@ -872,27 +878,29 @@ __global__ __launch_bounds__(256) void chain_compact_kernel(const CT *__restrict
                                                             int32_t *__restrict__ xe) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n_cap) return;
-  if (flags[p]) out[pos[p]] = merged[p];
-  if (p == n_cap - 1) *count = pos[p] + flags[p];
+  const uint32_t flag = ChainFirst<CT>{merged, n_dev, n_cap}(p);
+  if (flag) out[pos[p]] = merged[p];
+  if (p == n_cap - 1) *count = pos[p] + flag;
   const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
   if (!xs || p >= n) return;
   const uint64_t x = key_x(merged[p]);
   const int64_t c = xt_slot(x, key_x(merged[0]), ax_next);
   if (c < 0) return;
-  if (flags[p] && (p == 0 || key_x(merged[p - 1]) != x)) xs[c] = static_cast<int32_t>(pos[p]);
-  if (p == n - 1 || key_x(merged[p + 1]) != x) xe[c] = static_cast<int32_t>(pos[p] + flags[p]);
+  if (flag && (p == 0 || key_x(merged[p - 1]) != x)) xs[c] = static_cast<int32_t>(pos[p]);
+  if (p == n - 1 || key_x(merged[p + 1]) != x) xe[c] = static_cast<int32_t>(pos[p] + flag);
 }
 
-static size_t chain_scan_bytes(int64_t n) {
+template <typename CT> static size_t chain_scan_bytes(int64_t n) {
   size_t b = 0;
-  (void)rocprim::exclusive_scan(nullptr, b, static_cast<const uint32_t *>(nullptr), static_cast<uint32_t *>(nullptr),
-                                0u, static_cast<size_t>(n), rocprim::plus<uint32_t>());
+  const ChainFlags<CT> flags(rocprim::counting_iterator<int64_t>(0), ChainFirst<CT>{nullptr, nullptr, n});
+  (void)rocprim::exclusive_scan(nullptr, b, flags, static_cast<uint32_t *>(nullptr), 0u, static_cast<size_t>(n),
+                                rocprim::plus<uint32_t>());
   return b;
 }
 
 template <typename CT> struct ChainParts {
   CT *merged;
-  uint32_t *flags, *pos;
+  uint32_t *pos;
   int32_t *xs, *xe;  // x-table of the current level's input
   void *temp;
   size_t temp_bytes, total;
@@ -908,11 +916,10 @@ template <typename CT> static ChainParts<CT> chain_parts(int64_t n, void *base) 
     return q;
   };
   p.merged = reinterpret_cast<CT *>(take(n * sizeof(CT)));
-  p.flags = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
   p.pos = reinterpret_cast<uint32_t *>(take(n * sizeof(uint32_t)));
   p.xs = reinterpret_cast<int32_t *>(take(kXtCap * sizeof(int32_t)));
   p.xe = reinterpret_cast<int32_t *>(take(kXtCap * sizeof(int32_t)));
-  p.temp_bytes = chain_scan_bytes(n);
+  p.temp_bytes = chain_scan_bytes<CT>(n);
   p.temp = take(p.temp_bytes);
   p.total = off;
   return p;
@@ -967,12 +974,11 @@ static int chain_impl(const CT *keys, int64_t n, int levels, const int32_t *stri
                          static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]), b[0] / a[0], b[1] / a[1], p.merged,
                          l == 0 ? d_unsorted : nullptr);
     SPIRA_HIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(chain_flag_kernel<CT>, grid, dim3(256), 0, s, p.merged, n_dev, n, p.flags);
-    SPIRA_HIP_LAUNCH_CHECK();
     size_t tb = p.temp_bytes;
-    SPIRA_HIP_TRY(rocprim::exclusive_scan(p.temp, tb, p.flags, p.pos, 0u, static_cast<size_t>(n),
+    const ChainFlags<CT> flags(rocprim::counting_iterator<int64_t>(0), ChainFirst<CT>{p.merged, n_dev, n});
+    SPIRA_HIP_TRY(rocprim::exclusive_scan(p.temp, tb, flags, p.pos, 0u, static_cast<size_t>(n),
                                           rocprim::plus<uint32_t>(), s));
-    hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.flags, p.pos, n_dev, n,
+    hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.pos, n_dev, n,
                        static_cast<CT *>(outs[l]), d_counts + l, static_cast<uint32_t>(b[0]), p.xs, p.xe);
     SPIRA_HIP_LAUNCH_CHECK();
     for (int q = 0; q < 3; ++q) a[q] = b[q];
