@@ -487,8 +487,8 @@ static int search_batch_impl(int n, const spira_hip_kmap_job_t *jobs, hipStream_
       SPIRA_HIP_REQUIRE(jc.num_sources >= 0 && jc.num_targets >= 0 && jc.num_sources < (int64_t(1) << 31) &&
                             jc.num_targets < (int64_t(1) << 31),
                         "kmap_search_batch: sizes out of range");
-      SPIRA_HIP_REQUIRE(jc.kernel_map != nullptr && (jc.num_targets == 0 || jc.targets != nullptr) &&
-                            (jc.num_sources == 0 || jc.sources != nullptr),
+      SPIRA_HIP_REQUIRE(jc.num_targets == 0 || (jc.kernel_map != nullptr && jc.targets != nullptr &&
+                                                 (jc.num_sources == 0 || jc.sources != nullptr)),
                         "kmap_search_batch: missing array");
       done[c] = 1;
       SearchJob<CT> &p = b.job[b.n];
