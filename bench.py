@@ -186,8 +186,8 @@ class E2E:
 
         with tempfile.TemporaryDirectory() as tmp:
             d = self.tune_dir or tmp
-            self.model, groups = spira_amd.tune(self.model, [sample() for _ in range(6)], self.cache,
-                                                map_dataflow_options=[0, 1, 2], test_force_os=False, n_samples=5,
+            self.model, groups = spira_amd.tune(self.model, [sample() for _ in range(11)], self.cache,
+                                                map_dataflow_options=[0, 1, 2], test_force_os=False, n_samples=10,
                                                 save_dir=d, tune_tag=self.net, force_retune=self.tune_dir is None,
                                                 allow_gs_tuning=False, return_dataflows=True)
         self.dataflows = [groups.get(g, d) for g, d in zip(layer_groups(self.net), self.dataflows)]

@@ -156,7 +156,7 @@ typedef struct {
 
 /* The n searches of `jobs` (keys of key_bits bits), each exactly as
  * spira_hip_kmap_search with layout SPIRA_KMAP_OS: maps of one kernel shape
- * (2x2x2 or 3x3x3) share a launch, so that the searches of a network's maps
+ * (2x2x2, 3x3x3 or 5x5x5) share a launch, so that the searches of a network's maps
  * overlap; other shapes run one launch each.  (Replaces the per-layer
  * BinarySearch_kz_ostationary launches of BinarySearchStreamed<CT>,
  * torch/cuda_sparse_convolution_mapping.cu:894-1645.) */

@@ -318,7 +318,7 @@ __global__ __launch_bounds__(64 * kGroupMax) void kmap_search_kernel(const Searc
 // Several output-stationary maps of one kernel shape in one launch: job j
 // owns tiles [tile_start[j], tile_start[j + 1]) of the grid, so that the
 // searches of a network's small maps overlap instead of running back to back.
-constexpr int kJobOffsets = 27;  // kernel volumes up to 3 x 3 x 3
+constexpr int kJobOffsets = 27;  // xy offsets (kx * ky; the z-scan covers z): up to 5 x 5
 constexpr int kJobsMax = 8;
 template <typename CT> struct SearchJob {
   const CT *src;
@@ -460,13 +460,14 @@ static int search_impl(const CT *src, int64_t S, const CT *tgt, int64_t T, int k
 }
 
 // Batched output-stationary searches: jobs of the kernel shapes that have a
-// batch kernel (2x2x2, 3x3x3) are grouped by shape, at most kJobsMax per
+// batch kernel (2x2x2, 3x3x3, 5x5x5) are grouped by shape, at most kJobsMax per
 // launch, in their order; every other job is one search_impl call.
 template <typename CT>
 static int search_batch_impl(int n, const spira_hip_kmap_job_t *jobs, hipStream_t stream) {
   std::vector<char> done(static_cast<size_t>(n), 0);
   auto batchable = [](const spira_hip_kmap_job_t &j) {
-    return (j.kx == 2 && j.ky == 2 && j.kz == 2) || (j.kx == 3 && j.ky == 3 && j.kz == 3);
+    return (j.kx == 2 && j.ky == 2 && j.kz == 2) || (j.kx == 3 && j.ky == 3 && j.kz == 3) ||
+           (j.kx == 5 && j.ky == 5 && j.kz == 5);
   };
   for (int a = 0; a < n; ++a) {
     if (done[a]) continue;
@@ -518,7 +519,8 @@ static int search_batch_impl(int n, const spira_hip_kmap_job_t *jobs, hipStream_
     const size_t lds = ja.kx * kWindowCap * sizeof(CT) + 64 * K * sizeof(int32_t);
     const dim3 grid(static_cast<unsigned>(tiles)), block(64 * ja.kx);
     if (ja.kz == 2) hipLaunchKernelGGL((kmap_search_batch_kernel<CT, 2, 2>), grid, block, lds, stream, b);
-    else hipLaunchKernelGGL((kmap_search_batch_kernel<CT, 3, 3>), grid, block, lds, stream, b);
+    else if (ja.kz == 3) hipLaunchKernelGGL((kmap_search_batch_kernel<CT, 3, 3>), grid, block, lds, stream, b);
+    else hipLaunchKernelGGL((kmap_search_batch_kernel<CT, 5, 5>), grid, block, lds, stream, b);
     SPIRA_HIP_LAUNCH_CHECK();
   }
   return kOk;

@@ -121,6 +121,12 @@ def _sparse_conv_cls():
     return SparseConv
 
 
+#: relative margin by which a dataflow other than the first candidate must
+#: beat it to be chosen (a deviation from the reference, which takes the
+#: minimum)
+DATAFLOW_MARGIN = 0.03
+
+
 def tune_dataflows(model: Module, data_loader: Iterable, group_to_name: Dict[Tuple, List[str]],
                    config_options: List[DataflowConfig], kernel_map_cache, n_samples: int = 10,
                    verbose: bool = True) -> Dict[Tuple, DataflowConfig]:
@@ -164,8 +170,17 @@ def tune_dataflows(model: Module, data_loader: Iterable, group_to_name: Dict[Tup
         measured = [c for c in candidates if times[str(c)].get_trial_count() > 0]
         if not measured:
             measured = candidates[:1]
-        best[group_id] = min(measured, key=lambda c: times[str(c)].get_time() if times[str(c)].get_trial_count()
-                             else float("inf"))
+        t_of = lambda c: times[str(c)].get_time() if times[str(c)].get_trial_count() else float("inf")
+        pick = min(measured, key=t_of)
+        # another dataflow than the first candidate (the output-stationary
+        # one) must win by DATAFLOW_MARGIN: the timings are wall times of a
+        # few forward passes whose maps are built layer by layer, and noise of
+        # that size flipped groups to weight-stationary maps that cost more
+        # inside a network-wide map build than here
+        first = measured[0]
+        if pick is not first and t_of(pick) > (1.0 - DATAFLOW_MARGIN) * t_of(first):
+            pick = first
+        best[group_id] = pick
         if verbose:
             print(f"  -> {group_id}: {best[group_id]}")
     for name, params in gs_params.items():

@@ -1,6 +1,6 @@
 """spira_hip_kmap_search_batch through the C ABI: a batch of output-
-stationary searches (3x3x3 and 2x2x2 maps share launches, other shapes run
-alone, more than eight jobs of one shape split over launches, jobs with no
+stationary searches (3x3x3, 2x2x2 and 5x5x5 maps share launches, other
+shapes run alone, more than eight jobs of one shape split over launches, jobs with no
 targets) gives every map bit-exact equal to the oracle's search."""
 import ctypes
 import os
@@ -36,10 +36,10 @@ def test_batched_searches(dev, bits):
     for s in (2, 4, 8):
         levels[s] = orc.downsample(k1, (s, s, s))
     # (sources stride, targets stride, kernel): submanifold k3, downsampling
-    # k2, one k5 and one anisotropic map (unbatched shapes), nine k3 jobs in
+    # k2, two k5 and one anisotropic map (unbatched shape), eleven k3 jobs in
     # all (two launches of that shape) and one job without targets
     specs = [(1, 1, 3), (1, 2, 2), (2, 2, 3), (2, 4, 2), (4, 4, 3), (4, 8, 2), (8, 8, 3), (1, 1, 5),
-             (2, 2, (1, 1, 3)), (1, 1, 3), (2, 2, 3), (4, 4, 3), (8, 8, 3), (1, 1, 3), (1, 1, 3), (8, 0, 3)]
+             (2, 2, (1, 1, 3)), (2, 2, 5), (1, 1, 3), (2, 2, 3), (4, 4, 3), (8, 8, 3), (1, 1, 3), (1, 1, 3), (8, 0, 3)]
     dt = torch.int64 if bits == 64 else torch.int32
     keep, jobs, refs = [], [], []
     for ss, ts, k in specs:
