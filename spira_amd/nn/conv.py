@@ -359,6 +359,10 @@ def time_os_calls(layer: "SparseConv", calls, tuning: tuple, reps: int) -> float
     return total
 
 
+#: relative gain a launch choice must bring to replace the current one
+OS_TUNING_MARGIN = 0.01
+
+
 def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Optional[int] = None,
                      with_time: bool = False):
     """Coordinate search over the launch fields of ``os_candidates``: each
@@ -388,7 +392,7 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Opti
                 trial = list(best)
                 trial[i] = v
                 t = cost(trial)
-                if t < best_t:
+                if t < (1.0 - OS_TUNING_MARGIN) * best_t:  # noise-sized gains do not move the search
                     best, best_t = trial, t
     tuning = tuple(best) + (row_order,)
     return (tuning, best_t) if with_time else tuning

@@ -121,6 +121,10 @@ def _sparse_conv_cls():
     return SparseConv
 
 
+#: relative margin by which a map's row order must beat index order (the
+#: order's sort and the layers' lost L2 locality are not worth a tie)
+ROW_ORDER_MARGIN = 0.02
+
 #: relative margin by which a dataflow other than the first candidate must
 #: beat it to be chosen (a deviation from the reference, which takes the
 #: minimum)
@@ -277,7 +281,7 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
                 totals[r] = sum(t for _, t in picks[r])
             omap, T = entries[0][1][2], entries[0][1][1]
             totals[1] += _row_order_ms(omap, T)
-            r = 1 if totals[1] < totals[0] else 0
+            r = 1 if totals[1] < (1.0 - ROW_ORDER_MARGIN) * totals[0] else 0
             requests[key] = r
             if verbose:
                 print(f"[Spira] map {key}: {len(entries)} layers, {1e3 * totals[0]:.1f} us in index order, "
