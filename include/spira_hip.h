@@ -281,6 +281,9 @@ typedef struct {
   int offset_splits;
   int offset_pack;
   int block_order;
+  int row_walk; /* 1: each target walks its own valid offsets on the vector ALU (fp16,
+                   c_in <= 16, no row order or concatenation, storage-dtype output;
+                   otherwise ignored): for few channels and large, sparse kernels */
 } spira_hip_os_tuning_t;
 
 /* Workspace bytes of spira_hip_conv_os: an fp32 [num_targets, c_out]

@@ -47,6 +47,8 @@
 namespace spira_hip {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t uint32x4 __attribute__((ext_vector_type(4)));
@@ -1175,6 +1177,127 @@ __global__ __launch_bounds__(256) void scatter_kernel(const OffsetTable ot, int6
 }
 
 // ---------------------------------------------------------------------------
+// Per-target walk for few input channels (fp16, C_in <= 16): with a large,
+// sparse kernel (125 offsets, ~10 valid per target) the MMA tiles spend
+// most of their steps on missing neighbours; here every target sums only
+// its valid (offset, source) pairs, on the vector ALU (v_dot2_f32_f16).
+//
+// Block: 256 threads, a slice of 16 output columns (gridDim.y slices).  The
+// slice's weights [K][16][CIN] (C_in zero-padded to CIN) sit in LDS for the
+// whole block, which then walks 16-target chunks (persistent grid).  Wave w
+// takes targets 4w .. 4w+3 of a chunk; the 16 lanes of a target take the
+// offsets j = lane, lane + 16, ... (coalesced 64-byte map loads), sum their
+// pairs into 16 fp32 column sums, and a 16-lane butterfly adds the lanes'
+// sums; lane q then writes column q (with the epilogue).
+// ---------------------------------------------------------------------------
+constexpr int kWalkOffsetsMax = 128;
+template <int CIN> struct WalkShape {
+  static constexpr int ROW = 16 * CIN + 8;  // halves per offset in LDS (+16 bytes: bank spread)
+  static constexpr int JPL = kWalkOffsetsMax / 16;  // offsets per lane
+};
+
+template <int CIN>
+__global__ __launch_bounds__(256) void os_walk_kernel(const int32_t *__restrict__ map, int64_t T, int K,
+                                                      const _Float16 *__restrict__ X, int Cin,
+                                                      const _Float16 *__restrict__ W, int Cout,
+                                                      _Float16 *__restrict__ Y, Epilogue epi) {
+  using Sh = WalkShape<CIN>;
+  __shared__ __align__(16) _Float16 wl[kWalkOffsetsMax * Sh::ROW];
+  const int n0 = blockIdx.y * 16;
+  // weights of the slice: wl[k][o][c] = W[k][c][n0 + o] (zero past C_in / C_out)
+  for (int e = threadIdx.x; e < K * 16 * CIN; e += 256) {
+    const int k = e / (16 * CIN), r = e - k * 16 * CIN, o = r / CIN, c = r - o * CIN;
+    const int col = n0 + o;
+    wl[k * Sh::ROW + o * CIN + c] =
+        (c < Cin && col < Cout) ? W[(static_cast<int64_t>(k) * Cin + c) * Cout + col] : static_cast<_Float16>(0.f);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane & 15;
+  const int col = n0 + q;
+  float sc = 1.f, sh = 0.f;
+  if (col < Cout) {
+    if (epi.scale) sc = epi.scale[col];
+    if (epi.shift) sh = epi.shift[col];
+  }
+  const int64_t nchunks = (T + 15) / 16;
+  for (int64_t chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
+    const int64_t t = chunk * 16 + wave * 4 + (lane >> 4);
+    const bool live = t < T;
+    int32_t s[Sh::JPL];
+#pragma unroll
+    for (int i = 0; i < Sh::JPL; ++i) {
+      const int j = q + 16 * i;
+      s[i] = (live && j < K) ? map[t * K + j] : -1;
+    }
+    // every source row of the lane first (their loads overlap), then the sums
+    _Float16 x[Sh::JPL][CIN];
+#pragma unroll
+    for (int i = 0; i < Sh::JPL; ++i) {
+      const _Float16 *xr = X + static_cast<int64_t>(s[i] < 0 ? 0 : s[i]) * Cin;
+      if (Cin == CIN && (CIN % 8) == 0) {
+#pragma unroll
+        for (int c = 0; c < CIN; c += 8) {
+          half8 v = {};
+          if (s[i] >= 0) v = *reinterpret_cast<const half8 *>(xr + c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[i][c + e] = v[e];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CIN; ++c) x[i][c] = (s[i] >= 0 && c < Cin) ? xr[c] : static_cast<_Float16>(0.f);
+      }
+    }
+    float acc[16];
+#pragma unroll
+    for (int o = 0; o < 16; ++o) acc[o] = 0.f;
+#pragma unroll
+    for (int i = 0; i < Sh::JPL; ++i) {
+      if (s[i] < 0) continue;
+      const _Float16 *w = wl + (q + 16 * i) * Sh::ROW;
+#pragma unroll
+      for (int o = 0; o < 16; ++o) {
+        // the column's CIN weights: 16-byte LDS reads (8-byte ones for CIN = 4)
+#pragma unroll
+        for (int c0 = 0; c0 < CIN; c0 += (CIN >= 8 ? 8 : 4)) {
+          _Float16 wv[8];
+          if constexpr (CIN >= 8) {
+            const half8 v = *reinterpret_cast<const half8 *>(w + o * CIN + c0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wv[e] = v[e];
+          } else {
+            const half4 v = *reinterpret_cast<const half4 *>(w + o * CIN + c0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wv[e] = v[e];
+          }
+#pragma unroll
+          for (int c = 0; c < (CIN >= 8 ? 8 : 4); c += 2) {
+            const half2 a = {x[i][c0 + c], x[i][c0 + c + 1]};
+            const half2 b = {wv[c], wv[c + 1]};
+            acc[o] = __builtin_amdgcn_fdot2(a, b, acc[o], false);
+          }
+        }
+      }
+    }
+    // add the 16 lanes' sums of every column (butterfly inside the 16-lane group)
+#pragma unroll
+    for (int o = 0; o < 16; ++o)
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) acc[o] += __shfl_xor(acc[o], m, 64);
+    float v = 0.f;
+#pragma unroll
+    for (int o = 0; o < 16; ++o) v = (o == q) ? acc[o] : v;
+    if (live && col < Cout) {
+      v = v * sc + sh;
+      const int64_t at = t * Cout + col;
+      if (epi.residual) v += static_cast<float>(static_cast<const _Float16 *>(epi.residual)[at]);
+      if (epi.relu) v = v > 0.f ? v : 0.f;
+      Y[at] = static_cast<_Float16>(v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 static inline bool mfma_path(int dtype) { return dtype == SPIRA_F16; }
@@ -1310,6 +1433,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
   SPIRA_HIP_REQUIRE(t.offset_pack == 0 || t.offset_pack == 1 || t.offset_pack == 2 || t.offset_pack == 4,
                     "conv_os tuning: offset_pack must be 0, 1, 2 or 4");
   SPIRA_HIP_REQUIRE(t.block_order == 0 || t.block_order == 1, "conv_os tuning: block_order must be 0 or 1");
+  SPIRA_HIP_REQUIRE(t.row_walk == 0 || t.row_walk == 1, "conv_os tuning: row_walk must be 0 or 1");
   return kOk;
 }
 
@@ -1529,6 +1653,27 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
                     "conv_os: without a map (identity) there must be one offset and as many sources as targets");
   if (num_targets <= 0) return kOk;
   const Epilogue epi = make_epi(scale, shift, residual, relu);
+  if (tn.row_walk == 1 && dtype == SPIRA_F16 && c_in2 == 0 && c_in <= 16 && out_mode == SPIRA_OUT_STORE &&
+      out_in_map != nullptr && row_order == nullptr && num_offsets <= kWalkOffsetsMax) {
+    SPIRA_HIP_REQUIRE(weights != nullptr, "conv_os: the row walk reads the weights [K, c_in, c_out]");
+    SPIRA_HIP_REQUIRE(num_targets * num_offsets < (int64_t(1) << 31), "conv_os: kernel map above 2 GiB");
+    const int64_t nchunks = div_up(num_targets, 16);
+    const dim3 grid(static_cast<unsigned>(nchunks < 1024 ? nchunks : 1024), static_cast<unsigned>(div_up(c_out, 16)));
+    const auto *X = static_cast<const _Float16 *>(sources);
+    const auto *W = static_cast<const _Float16 *>(weights);
+    auto *Y = static_cast<_Float16 *>(targets);
+    if (c_in <= 4)
+      hipLaunchKernelGGL(os_walk_kernel<4>, grid, dim3(256), 0, stream, out_in_map, num_targets, num_offsets, X, c_in,
+                         W, c_out, Y, epi);
+    else if (c_in <= 8)
+      hipLaunchKernelGGL(os_walk_kernel<8>, grid, dim3(256), 0, stream, out_in_map, num_targets, num_offsets, X, c_in,
+                         W, c_out, Y, epi);
+    else
+      hipLaunchKernelGGL(os_walk_kernel<16>, grid, dim3(256), 0, stream, out_in_map, num_targets, num_offsets, X,
+                         c_in, W, c_out, Y, epi);
+    SPIRA_HIP_LAUNCH_CHECK();
+    return kOk;
+  }
   if (mfma_path(dtype)) {
     SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
     const int cin_all = c_in + c_in2;

@@ -257,17 +257,19 @@ struct OsTune {
   spira_hip_os_tuning_t k{};
   int row_order = -1;
 };
-using TuneArg = std::optional<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t>>;
+using TuneArg = std::optional<std::vector<int64_t>>;
 static OsTune tune_of(const TuneArg &t) {
   OsTune r;
   if (!t.has_value()) return r;
-  auto [a, b, c, d, o, e] = *t;
-  r.k.col_tile = static_cast<int>(a);
-  r.k.step_channels = static_cast<int>(b);
-  r.k.offset_splits = static_cast<int>(c);
-  r.k.offset_pack = static_cast<int>(d);
-  r.k.block_order = static_cast<int>(o);
-  r.row_order = static_cast<int>(e);
+  const auto &v = *t;
+  SPIRA_CHECK_ARG(v.size() == 6 || v.size() == 7, "tuning must have 6 or 7 fields");
+  r.k.col_tile = static_cast<int>(v[0]);
+  r.k.step_channels = static_cast<int>(v[1]);
+  r.k.offset_splits = static_cast<int>(v[2]);
+  r.k.offset_pack = static_cast<int>(v[3]);
+  r.k.block_order = static_cast<int>(v[4]);
+  r.row_order = static_cast<int>(v[5]);
+  r.k.row_walk = v.size() > 6 ? static_cast<int>(v[6]) : 0;
   SPIRA_CHECK_ARG(r.row_order >= -1 && r.row_order <= 1, "row_order must be -1, 0 or 1");
   return r;
 }
@@ -294,6 +296,9 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
     // no map: the identity map (targets[t] reads sources[t], one offset)
     SPIRA_CHECK_ARG(S == T && K == 1, "the identity map needs as many sources as targets and one offset");
   }
+  // the row walk (few input channels): the map as it is and the rows unpadded
+  const bool walk = tn.k.row_walk == 1 && map && dtype == SPIRA_F16 && !X2 && W.size(1) <= 16 &&
+                    mode == SPIRA_OUT_STORE && K <= 128;
   auto P = prepared_weights(W);
   size_t wsb = 0;
   const int64_t cin_run =
@@ -302,7 +307,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && row_order_applies(T, K, tn.row_order)) {
+  if (map && dtype == SPIRA_F16 && !walk && row_order_applies(T, K, tn.row_order)) {
     const OrderEntry &oe = row_order_of(*map, T);
     order = oe.order.data_ptr<int32_t>();
     masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
@@ -320,7 +325,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
              "sparse_convolution_forward_os");
     return;
   }
-  const int64_t cin = cin_run;
+  const int64_t cin = walk ? W.size(1) : cin_run;
   torch::Tensor Xp = X;
   if (cin != W.size(1)) Xp = torch::constant_pad_nd(X.narrow(0, 0, S), {0, cin - W.size(1)});
   check_rc(spira_hip_conv_os(T, K, mp, order, masks, Xp.data_ptr(), S, cin, wrow_ptr(W, w0), prow_ptr(P, W, w0), W.size(2),

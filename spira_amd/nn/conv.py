@@ -336,13 +336,15 @@ def os_candidates(c_in: int, c_out: int, volume: int) -> List[List[int]]:
     """Values tried per output-stationary launch field (0 = automatic):
     column tiles up to the output width, step channels up to the padded input
     width, offset splits, offset packing where it applies (16-, 32- and
-    64-channel inputs of kernels above 27 offsets), and the block order."""
+    64-channel inputs of kernels above 27 offsets), the block order, and the
+    row walk (inputs of at most 16 channels with a map)."""
     cin_p = (c_in + 15) // 16 * 16
     cols = [0] + [c for c in (32, 64, 96, 128) if c <= (c_out + 31) // 32 * 32]
     steps = [0, 32] + ([64] if cin_p >= 64 else []) + ([128] if cin_p >= 96 else [])
     splits = [0, 1, 2, 4] if volume > 1 else [0]
     packs = [0, 1, 2, 4] if (volume > 27 and cin_p in (16, 32, 64)) else [0]
-    return [cols, steps, splits, packs, [0, 1]]
+    walks = [0, 1] if (c_in <= 16 and volume > 1) else [0]
+    return [cols, steps, splits, packs, [0, 1], walks]
 
 
 def time_os_calls(layer: "SparseConv", calls, tuning: tuple, reps: int) -> float:
@@ -374,11 +376,14 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Opti
         cur = layer._tunable_config.get("os_tuning")
         row_order = -1 if cur is None else int(cur[5])
     cands = os_candidates(layer.in_channels, layer.out_channels, int(np.prod(layer.kernel_size)))
-    best = [0, 0, 0, 0, 0]
+    best = [0] * len(cands)
+
+    def full(fields):  # (launch fields, row order, row walk)
+        return tuple(fields[:5]) + (row_order,) + tuple(fields[5:])
 
     def cost(fields):
         try:
-            return time_os_calls(layer, calls, tuple(fields) + (row_order,), reps)
+            return time_os_calls(layer, calls, full(fields), reps)
         except RuntimeError:
             F.cuda_reset_error()
             return float("inf")
@@ -394,5 +399,5 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Opti
                 t = cost(trial)
                 if t < (1.0 - OS_TUNING_MARGIN) * best_t:  # noise-sized gains do not move the search
                     best, best_t = trial, t
-    tuning = tuple(best) + (row_order,)
+    tuning = full(best)
     return (tuning, best_t) if with_time else tuning

@@ -112,14 +112,16 @@ def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sou
 
 
 def _tuning(tuning) -> Optional[tuple]:
-    """An output-stationary launch choice: None (automatic) or a 6-tuple
+    """An output-stationary launch choice: None (automatic) or a tuple
     (col_tile, step_channels, offset_splits, offset_pack, block_order,
-    row_order); 0 (and -1 for row_order) in a field = automatic."""
+    row_order[, row_walk]); 0 (and -1 for row_order) in a field = automatic;
+    row_walk 1 sums each target's valid pairs on the vector ALU (fp16 layers
+    of at most 16 input channels)."""
     if tuning is None:
         return None
     t = tuple(int(v) for v in tuning)
-    if len(t) != 6:
-        raise ValueError(f"an output-stationary tuning has 6 fields, got {len(t)}")
+    if len(t) not in (6, 7):
+        raise ValueError(f"an output-stationary tuning has 6 or 7 fields, got {len(t)}")
     return t
 
 

@@ -263,3 +263,28 @@ def test_ordered_k2_layer(dev, indoor, transposed):
     for rows in (1, 0):
         y = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=(0, 0, 0, 0, 0, rows))
         assert rel_err(np_(y.float()), ref) <= 1e-2, rows
+
+
+@pytest.mark.parametrize("ks,cin,cout", [(3, 3, 32), (3, 8, 24), (3, 16, 16), (5, 4, 16), (5, 16, 16), (5, 16, 32),
+                                         (5, 11, 40)])
+def test_row_walk(dev, indoor, scene_k5, ks, cin, cout):
+    """The per-target row walk (tuning row_walk = 1: few input channels on
+    the vector ALU) against the oracle, with the fused epilogue, on the
+    config-4 k=3 map and a k=5 map; C_in up to 16, any C_out."""
+    k, m = indoor if ks == 3 else scene_k5
+    S = T = len(k)
+    K = ks ** 3
+    g = torch.Generator().manual_seed(cin * 100 + cout)
+    X = torch.randn(S, cin, generator=g).half()
+    W = (torch.randn(K, cin, cout, generator=g) / np.sqrt(K * cin)).half()
+    scale = 0.5 + torch.rand(cout, generator=g)
+    shift = 0.1 * torch.randn(cout, generator=g)
+    res = torch.randn(T, cout, generator=g).half()
+    md = torch.from_numpy(m).to(dev)
+    conv = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    y = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=(0, 0, 0, 0, 0, -1, 1))
+    assert rel_err(np_(y.float()), conv) <= 1e-2
+    ye = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=(0, 0, 0, 0, 0, -1, 1),
+                                         epilogue=(scale.to(dev), shift.to(dev), res.to(dev), True))
+    ref = np.maximum(conv * scale.double().numpy() + shift.double().numpy() + res.double().numpy(), 0)
+    assert rel_err(np_(ye.float()), ref) <= 1e-2

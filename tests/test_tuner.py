@@ -96,11 +96,12 @@ def test_os_tuning_changes_the_launch():
 
 def test_os_candidates():
     from spira_amd.nn.conv import os_candidates
-    cols, steps, splits, packs, orders = os_candidates(256, 256, 27)
+    cols, steps, splits, packs, orders, walks = os_candidates(256, 256, 27)
     assert cols == [0, 32, 64, 96, 128] and steps == [0, 32, 64, 128] and packs == [0] and orders == [0, 1]
-    cols, steps, splits, packs, orders = os_candidates(16, 16, 125)
-    assert cols == [0, 32] and steps == [0, 32] and packs == [0, 1, 2, 4]
-    assert os_candidates(3, 32, 1)[2] == [0]
+    assert walks == [0]  # the row walk is for inputs of at most 16 channels
+    cols, steps, splits, packs, orders, walks = os_candidates(16, 16, 125)
+    assert cols == [0, 32] and steps == [0, 32] and packs == [0, 1, 2, 4] and walks == [0, 1]
+    assert os_candidates(3, 32, 1)[2] == [0] and os_candidates(3, 32, 1)[5] == [0]  # no map: no walk
 
 
 @pytest.mark.gpu
@@ -195,7 +196,7 @@ def test_os_tuning_keeps_results(dev, tmp_path):
                    n_samples=2, save_dir=str(tmp_path), tune_tag="os", allow_gs_tuning=False)
     tuned = [m for m in model.modules() if isinstance(m, spira_amd.nn.SparseConv)
              and m._tunable_config["os_tuning"] is not None]
-    assert len(tuned) >= 20 and all(len(m._tunable_config["os_tuning"]) == 6 for m in tuned)
+    assert len(tuned) >= 20 and all(len(m._tunable_config["os_tuning"]) == 7 for m in tuned)
     after = run()
     for a, b in zip(before, after):
         rms = float(a.pow(2).mean().sqrt()) or 1.0
