@@ -280,16 +280,20 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
                 picks[r] = [choose_os_tuning(m, [call], reps, row_order=r, with_time=True) for m, call in entries]
                 totals[r] = sum(t for _, t in picks[r])
             omap, T = entries[0][1][2], entries[0][1][1]
-            totals[1] += _row_order_ms(omap, T)
+            # with the order computed, each layer still walks whichever is
+            # faster for it: the map's order pays if the layers' best walks
+            # plus the sort beat index order everywhere
+            best1 = [min(t0, t1) for (_, t0), (_, t1) in zip(picks[0], picks[1])]
+            totals[1] = sum(best1) + _row_order_ms(omap, T)
             r = 1 if totals[1] < (1.0 - ROW_ORDER_MARGIN) * totals[0] else 0
             requests[key] = r
             if verbose:
                 print(f"[Spira] map {key}: {len(entries)} layers, {1e3 * totals[0]:.1f} us in index order, "
-                      f"{1e3 * totals[1]:.1f} us in row order (sort included) -> row order {r}")
+                      f"{1e3 * totals[1]:.1f} us with the order (each layer its faster walk, sort included) -> row order {r}")
                 for (m, _), (t0, ms0), (t1, ms1) in zip(entries, picks[0], picks[1]):
                     print(f"    {m.in_channels}->{m.out_channels}: {t0} {1e3 * ms0:.1f} us | {t1} {1e3 * ms1:.1f} us")
-            for (m, _), (tuning, _) in zip(entries, picks[r]):
-                m._tunable_config["os_tuning"] = tuning
+            for (m, _), (tn0, t0), (tn1, t1) in zip(entries, picks[0], picks[1]):
+                m._tunable_config["os_tuning"] = tn1 if (r == 1 and t1 < t0) else tn0
         if kernel_map_cache is not None:
             kernel_map_cache.row_order_requests.update(requests)
         return requests
