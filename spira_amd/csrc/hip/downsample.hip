@@ -890,6 +890,107 @@ __global__ __launch_bounds__(256) void chain_compact_kernel(const CT *__restrict
   if (p == n - 1 || key_x(merged[p + 1]) != x) xe[c] = static_cast<int32_t>(pos[p] + flag);
 }
 
+// Compaction without a device-wide scan (inputs of at most kCompactMaxTiles
+// tiles): chain_count_kernel counts the run starts of each 2048-key tile;
+// chain_compact2_kernel sums the counts of the tiles before its own (at most
+// a few per thread), scans its tile in the block, and writes what
+// chain_compact_kernel writes.
+constexpr int kCompactTile = 2048;
+constexpr int kCompactItems = kCompactTile / 256;
+constexpr int64_t kCompactMaxTiles = 1024;
+
+// merged[p0 - 1 .. p0 + kCompactItems] (entries outside [0, n_cap): 0)
+template <typename CT>
+__device__ __forceinline__ void load_run(const CT *__restrict__ merged, int64_t n_cap, int64_t p0,
+                                         CT (&m)[kCompactItems + 2]) {
+#pragma unroll
+  for (int r = 0; r < kCompactItems + 2; ++r) {
+    const int64_t p = p0 - 1 + r;
+    const bool in = p >= 0 && p < n_cap;
+    const CT v = merged[in ? p : 0];
+    m[r] = in ? v : CT(0);
+  }
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_count_kernel(const CT *__restrict__ merged,
+                                                          const uint32_t *__restrict__ n_dev, int64_t n_cap,
+                                                          uint32_t *__restrict__ tile_counts) {
+  __shared__ uint32_t red[4];
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kCompactTile + threadIdx.x * kCompactItems;
+  CT m[kCompactItems + 2];
+  load_run<CT>(merged, n_cap, p0, m);
+  uint32_t c = 0;
+#pragma unroll
+  for (int r = 0; r < kCompactItems; ++r) {
+    const int64_t p = p0 + r;
+    c += (p < n && (p == 0 || m[r + 1] != m[r])) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) c += __shfl_xor(c, d, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) tile_counts[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void chain_compact2_kernel(const CT *__restrict__ merged,
+                                                             const uint32_t *__restrict__ tile_counts,
+                                                             const uint32_t *__restrict__ n_dev, int64_t n_cap,
+                                                             CT *__restrict__ out, uint32_t *__restrict__ count,
+                                                             uint32_t ax_next, int32_t *__restrict__ xs,
+                                                             int32_t *__restrict__ xe) {
+  __shared__ uint32_t before[4], wtot[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t n = n_dev ? static_cast<int64_t>(*n_dev) : n_cap;
+  // run starts of the tiles before this one
+  uint32_t b = 0;
+  for (int t = tid; t < static_cast<int>(blockIdx.x); t += 256) b += tile_counts[t];
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) b += __shfl_xor(b, d, 64);
+  // this thread's keys and run starts
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kCompactTile + tid * kCompactItems;
+  CT m[kCompactItems + 2];
+  load_run<CT>(merged, n_cap, p0, m);
+  bool f[kCompactItems];
+  uint32_t c = 0;
+#pragma unroll
+  for (int r = 0; r < kCompactItems; ++r) {
+    const int64_t p = p0 + r;
+    f[r] = p < n && (p == 0 || m[r + 1] != m[r]);
+    c += f[r] ? 1u : 0u;
+  }
+  // exclusive prefix of c over the block
+  uint32_t incl = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wtot[w] = incl;
+  if (lane == 0) before[w] = b;
+  __syncthreads();
+  uint32_t pos = before[0] + before[1] + before[2] + before[3] + incl - c;
+  for (int q = 0; q < w; ++q) pos += wtot[q];
+  const uint64_t xmin = key_x(merged[0]);
+#pragma unroll
+  for (int r = 0; r < kCompactItems; ++r) {
+    const int64_t p = p0 + r;
+    if (f[r]) out[pos] = m[r + 1];
+    if (p == n_cap - 1) *count = pos + (f[r] ? 1u : 0u);
+    if (xs && p < n) {
+      const uint64_t x = key_x(m[r + 1]);
+      const int64_t cx = xt_slot(x, xmin, ax_next);
+      if (cx >= 0) {
+        if (f[r] && (p == 0 || key_x(m[r]) != x)) xs[cx] = static_cast<int32_t>(pos);
+        if (p == n - 1 || key_x(m[r + 2]) != x) xe[cx] = static_cast<int32_t>(pos + (f[r] ? 1u : 0u));
+      }
+    }
+    pos += f[r] ? 1u : 0u;
+  }
+}
+
 template <typename CT> static size_t chain_scan_bytes(int64_t n) {
   size_t b = 0;
   const ChainFlags<CT> flags(rocprim::counting_iterator<int64_t>(0), ChainFirst<CT>{nullptr, nullptr, n});
@@ -974,13 +1075,25 @@ static int chain_impl(const CT *keys, int64_t n, int levels, const int32_t *stri
                          static_cast<uint32_t>(a[0]), static_cast<uint32_t>(a[1]), b[0] / a[0], b[1] / a[1], p.merged,
                          l == 0 ? d_unsorted : nullptr);
     SPIRA_HIP_LAUNCH_CHECK();
-    size_t tb = p.temp_bytes;
-    const ChainFlags<CT> flags(rocprim::counting_iterator<int64_t>(0), ChainFirst<CT>{p.merged, n_dev, n});
-    SPIRA_HIP_TRY(rocprim::exclusive_scan(p.temp, tb, flags, p.pos, 0u, static_cast<size_t>(n),
-                                          rocprim::plus<uint32_t>(), s));
-    hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.pos, n_dev, n,
-                       static_cast<CT *>(outs[l]), d_counts + l, static_cast<uint32_t>(b[0]), p.xs, p.xe);
-    SPIRA_HIP_LAUNCH_CHECK();
+    const int64_t ctiles = div_up(n, kCompactTile);
+    if (ctiles <= kCompactMaxTiles) {
+      // (the tile counts take the front of the positions array)
+      hipLaunchKernelGGL(chain_count_kernel<CT>, dim3(static_cast<unsigned>(ctiles)), dim3(256), 0, s, p.merged,
+                         n_dev, n, p.pos);
+      SPIRA_HIP_LAUNCH_CHECK();
+      hipLaunchKernelGGL(chain_compact2_kernel<CT>, dim3(static_cast<unsigned>(ctiles)), dim3(256), 0, s, p.merged,
+                         p.pos, n_dev, n, static_cast<CT *>(outs[l]), d_counts + l, static_cast<uint32_t>(b[0]), p.xs,
+                         p.xe);
+      SPIRA_HIP_LAUNCH_CHECK();
+    } else {
+      size_t tb = p.temp_bytes;
+      const ChainFlags<CT> flags(rocprim::counting_iterator<int64_t>(0), ChainFirst<CT>{p.merged, n_dev, n});
+      SPIRA_HIP_TRY(rocprim::exclusive_scan(p.temp, tb, flags, p.pos, 0u, static_cast<size_t>(n),
+                                            rocprim::plus<uint32_t>(), s));
+      hipLaunchKernelGGL(chain_compact_kernel<CT>, grid, dim3(256), 0, s, p.merged, p.pos, n_dev, n,
+                         static_cast<CT *>(outs[l]), d_counts + l, static_cast<uint32_t>(b[0]), p.xs, p.xe);
+      SPIRA_HIP_LAUNCH_CHECK();
+    }
     for (int q = 0; q < 3; ++q) a[q] = b[q];
   }
   return kOk;
