@@ -80,6 +80,42 @@ static bool chainable(const std::vector<Int3> &strides) {
   return true;
 }
 
+// The chained downsample queued on the current stream with no host read:
+// the outputs at full capacity (n keys each), then a device int32 tensor of
+// B + 1 entries, the level counts and the unsorted-input flag.  Empty if the
+// strides do not chain or there are no keys (the caller then takes
+// streamed_output_generate).
+std::vector<torch::Tensor> downsample_chain_launch(const torch::Tensor &keys, const std::vector<Int3> &strides) {
+  SPIRA_CHECK_ARG(keys.dim() == 1, "coordinates should be already flattened");
+  require_device(keys, "keys");
+  const int bits = key_bits_of(keys);
+  const auto dev = keys.device();
+  const int64_t n = keys.size(0);
+  const size_t B = strides.size();
+  std::vector<torch::Tensor> outs;
+  if (n == 0 || B == 0 || !chainable(strides)) return outs;
+  std::vector<int32_t> st;
+  for (auto &t : strides) {
+    auto [sx, sy, sz] = t;
+    st.insert(st.end(), {sx, sy, sz});
+  }
+  std::vector<void *> ptrs;
+  for (size_t i = 0; i < B; ++i) {
+    outs.push_back(torch::empty_like(keys));
+    ptrs.push_back(outs.back().data_ptr());
+  }
+  auto cnt = torch::zeros({static_cast<int64_t>(B + 1)}, torch::TensorOptions(dev).dtype(torch::kInt32));
+  size_t cwb = 0;
+  check_rc(spira_hip_downsample_chain_workspace(n, bits, &cwb), "downsample_chain_launch");
+  auto cws = workspace(cwb, dev);
+  uint32_t *c = reinterpret_cast<uint32_t *>(cnt.data_ptr<int32_t>());
+  check_rc(spira_hip_downsample_chain(keys.data_ptr(), n, bits, static_cast<int>(B), st.data(), ptrs.data(), c, c + B,
+                                      cws.data_ptr(), cwb, current_stream()),
+           "downsample_chain_launch");
+  outs.push_back(cnt);
+  return outs;
+}
+
 // One downsample per target stride: every plan on the current stream, one
 // host read of all plans, then each execution on its own pool stream, and
 // one host read of all counts at the end (reference:
@@ -94,31 +130,13 @@ std::vector<torch::Tensor> streamed_output_generate(const torch::Tensor &keys, c
   // Nested power-of-two strides (2, 4, 8, 16 ...): every level from the
   // previous one, no host read until the counts (spira_hip_downsample_chain);
   // keys that turn out unsorted fall through to the per-stride path below.
-  if (n > 0 && B > 0 && chainable(strides)) {
-    std::vector<int32_t> st;
-    for (auto &t : strides) {
-      auto [sx, sy, sz] = t;
-      st.insert(st.end(), {sx, sy, sz});
-    }
-    std::vector<torch::Tensor> outs;
-    std::vector<void *> ptrs;
-    for (size_t i = 0; i < B; ++i) {
-      outs.push_back(torch::empty_like(keys));
-      ptrs.push_back(outs.back().data_ptr());
-    }
-    auto cnt = torch::zeros({static_cast<int64_t>(B + 1)}, torch::TensorOptions(dev).dtype(torch::kInt32));
-    size_t cwb = 0;
-    check_rc(spira_hip_downsample_chain_workspace(n, bits, &cwb), "streamed_output_generate");
-    auto cws = workspace(cwb, dev);
-    uint32_t *c = reinterpret_cast<uint32_t *>(cnt.data_ptr<int32_t>());
-    check_rc(spira_hip_downsample_chain(keys.data_ptr(), n, bits, static_cast<int>(B), st.data(), ptrs.data(), c,
-                                        c + B, cws.data_ptr(), cwb, current_stream()),
-             "streamed_output_generate");
+  if (auto launched = downsample_chain_launch(keys, strides); !launched.empty()) {
+    auto cnt = launched.back();
     auto h = cnt.cpu();
     const int32_t *hc = h.data_ptr<int32_t>();
     if (hc[B] == 0) {
       std::vector<torch::Tensor> res;
-      for (size_t i = 0; i < B; ++i) res.push_back(outs[i].slice(0, 0, hc[i]));
+      for (size_t i = 0; i < B; ++i) res.push_back(launched[i].slice(0, 0, hc[i]));
       return res;
     }
   }
@@ -196,6 +214,7 @@ void register_coords(pybind11::module_ &m) {
   m.def("cuda_unflatten", &unflatten);
   m.def("cuda_downsample", &downsample);
   m.def("cuda_streamed_output_generate", &streamed_output_generate);
+  m.def("cuda_downsample_chain_launch", &downsample_chain_launch);
 }
 
 }  // namespace spira_host

@@ -188,12 +188,14 @@ void set_concurrent_maps(bool on) { concurrent_maps() = on; }
 std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &voxels,
                                               const std::vector<Int3> &kernel_sizes,
                                               const std::vector<Int3> &source_strides,
-                                              const std::vector<int> &dataflow) {
+                                              const std::vector<int> &dataflow, int64_t begin) {
   const size_t n = kernel_sizes.size();
+  SPIRA_CHECK_ARG(begin >= 0 && static_cast<size_t>(begin) <= n, "begin out of range");
+  const size_t b0 = static_cast<size_t>(begin);
   SPIRA_CHECK_ARG(source_strides.size() == n && dataflow.size() == n,
                   "All argument lists must have the same length in build_kmap_streamed");
   SPIRA_CHECK_ARG(!voxels.empty(), "voxels must not be empty");
-  for (size_t i = 0; i < n; ++i)
+  for (size_t i = b0; i < n; ++i)
     SPIRA_CHECK_ARG((i + 1) / 2 < voxels.size(), "not enough voxel sets for ", n, " maps");
   const auto dev = voxels[0].device();
   std::vector<PendingMap> pending(n);
@@ -207,7 +209,7 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
   // streams.  The current stream waits for all of them.
   std::vector<size_t> side_of(n, 0);
   size_t nside = 0;
-  for (size_t i = 0; i < n; ++i)
+  for (size_t i = b0; i < n; ++i)
     if (concurrent_maps() || dataflow[i] != 0) side_of[i] = nside++;
   StreamFan fan(dev, nside);
   const hipStream_t cur = current_stream();
@@ -217,7 +219,7 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
   // output-stationary maps on the current stream: their searches are
   // batched into one launch per kernel shape, after every map is allocated
   std::vector<spira_hip_kmap_job_t> jobs;
-  for (size_t i = 0; i < n; ++i) {
+  for (size_t i = b0; i < n; ++i) {
     // half maps: dataflow 2 uses the position in the list (mapping.cu:1129),
     // the other dataflows compare the set sizes (mapping.cu:955)
     const int half = (dataflow[i] == 2) ? (i % 2 == 0 ? 1 : 0) : -1;
@@ -238,10 +240,10 @@ std::vector<KmapTuple> binary_search_streamed(const std::vector<torch::Tensor> &
   // Odd dataflows need their pair counts on the host; hybrid dataflows above
   // 4 transpose their dense part on the current stream in finish_map, so the
   // side stream that wrote the map must be complete first.
-  for (size_t i = 0; i < n; ++i)
+  for (size_t i = b0; i < n; ++i)
     if (dataflow[i] % 2 == 1 || dataflow[i] > 4)
       SPIRA_CHECK_ARG(hipStreamSynchronize(stream_of(i)) == hipSuccess, "stream synchronisation failed");
-  for (size_t i = 0; i < n; ++i) {
+  for (size_t i = b0; i < n; ++i) {
     const int32_t *h = sizes_host.data_ptr<int32_t>() + 2 * i;
     out.push_back(finish_map(pending[i], dataflow[i] % 2 == 1 ? h[0] : 0, dataflow[i] % 2 == 1 ? h[1] : 0,
                              stream_of(i)));
@@ -316,7 +318,8 @@ void register_mapping(pybind11::module_ &m) {
   m.def("time_kmap_search", &time_kmap_search);
   m.def("set_concurrent_maps", &set_concurrent_maps);
   m.def("cuda_binary_search", &binary_search);
-  m.def("cuda_binary_search_streamed", &binary_search_streamed);
+  m.def("cuda_binary_search_streamed", &binary_search_streamed, pybind11::arg("voxels"), pybind11::arg("kernel_sizes"),
+        pybind11::arg("source_strides"), pybind11::arg("dataflow"), pybind11::arg("begin") = 0);
   m.def("cuda_binary_search_no_small_z", &binary_search_no_small_z);
   m.def("cuda_convert_transposed_os", &convert_transposed_os);
 }

@@ -103,21 +103,46 @@ class KernelMapCache:
         """Network-wide precompute: all downsampled coordinate sets, then every
         layer map concurrently (map i: sources voxels[i//2], targets
         voxels[(i+1)//2])."""
-        outputs = F.streamed_output_generate(source_coordinates, target_strides)
-        voxels = [source_coordinates] + list(outputs)
+        src_strides = list(source_strides)[:-1]
         s_stride = as_tuple(init_stride, size=3)
+        map_keys = []
+        s_prev = s_stride
+        for i in range(len(kernel_sizes)):
+            t_stride = as_tuple(source_strides[i + 1], size=3)
+            map_keys.append((s_prev, t_stride, as_tuple(kernel_sizes[i], size=3)))
+            s_prev = t_stride
+
+        def row_order(i, kmap):
+            if self.prepare_row_orders and dataflow[i] == 0:
+                F.prepare_row_order(kmap[2], kmap[1], self.row_order_requests.get(map_keys[i], -1))
+
+        # Map 0 (voxels[0] to voxels[0]) needs no downsampled level: it is
+        # queued between the chained downsample and the host read of the
+        # level counts, so that the GPU works on it while the host waits.
+        kmaps, outputs = [], None
+        launched = F.downsample_chain_launch(source_coordinates, target_strides) if kernel_sizes else None
+        if launched is not None:
+            levels, counts = launched
+            host = torch.empty(counts.numel(), dtype=torch.int32, pin_memory=True)
+            host.copy_(counts, non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record()
+            kmaps = F.build_kmap_streamed([source_coordinates], kernel_sizes[:1], src_strides[:1], dataflow[:1])
+            row_order(0, kmaps[0])
+            ready.synchronize()
+            n = host.tolist()
+            if n[-1] == 0:
+                outputs = [lv[:c] for lv, c in zip(levels, n[:-1])]
+        if outputs is None:  # strides that do not chain, or unsorted keys
+            outputs = F.streamed_output_generate(source_coordinates, target_strides)
+        voxels = [source_coordinates] + list(outputs)
         self._coordinates_cache[s_stride] = voxels[0]
         for i, ts in enumerate(target_strides):
             self._coordinates_cache[as_tuple(ts, size=3)] = voxels[i + 1]
-        kmaps = F.build_kmap_streamed(voxels, kernel_sizes, list(source_strides)[:-1], dataflow)
-        if self.prepare_row_orders:
-            s_prev = as_tuple(init_stride, size=3)
-            for i, d in enumerate(dataflow):
-                t_stride = as_tuple(source_strides[i + 1], size=3)
-                key = (s_prev, t_stride, as_tuple(kernel_sizes[i], size=3))
-                s_prev = t_stride
-                if d == 0:
-                    F.prepare_row_order(kmaps[i][2], kmaps[i][1], self.row_order_requests.get(key, -1))
+        first = len(kmaps)
+        kmaps += F.build_kmap_streamed(voxels, kernel_sizes, src_strides, dataflow, begin=first)
+        for i in range(first, len(kernel_sizes)):
+            row_order(i, kmaps[i])
         for i in range(len(kernel_sizes)):
             t_stride = as_tuple(source_strides[i + 1], size=3)
             self._kernel_maps_cache[(s_stride, t_stride, as_tuple(kernel_sizes[i], size=3))] = [False, *kmaps[i]]

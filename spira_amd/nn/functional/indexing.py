@@ -16,7 +16,7 @@ from ._native import _C
 
 __all__ = [
     "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os",
-    "build_kmap_streamed", "streamed_output_generate", "build_kmap_no_small_z", "sparse_quantize",
+    "build_kmap_streamed", "streamed_output_generate", "downsample_chain_launch", "build_kmap_no_small_z", "sparse_quantize",
     "prepare_row_order",
 ]
 
@@ -57,14 +57,28 @@ def streamed_output_generate(coordinates: torch.Tensor, target_strides: List[Tup
     return _C.cuda_streamed_output_generate(coordinates, [as_tuple(s, size=3) for s in target_strides])
 
 
+def downsample_chain_launch(coordinates: torch.Tensor, target_strides: List[Tuple[int, int, int]]):
+    """Queue the chained downsample of sorted keys on the current stream
+    without reading anything back: ``(outputs, counts)``, the outputs at full
+    capacity and ``counts`` a device int32 tensor of the level counts followed
+    by the unsorted-input flag; ``None`` when the strides do not chain (or no
+    keys), for which :func:`streamed_output_generate` is the call."""
+    coordinates = coordinates.contiguous()
+    _require_gpu(coordinates)
+    r = _C.cuda_downsample_chain_launch(coordinates, [as_tuple(s, size=3) for s in target_strides])
+    if not r:
+        return None
+    return list(r[:-1]), r[-1]
+
+
 def build_kmap_streamed(voxels: List[torch.Tensor], kernel_sizes: List[ScalarOrTuple[int]],
-                        source_strides: List[ScalarOrTuple[int]], dataflow: List[int]):
+                        source_strides: List[ScalarOrTuple[int]], dataflow: List[int], begin: int = 0):
     voxels = [v.contiguous() for v in voxels]
     kernel_sizes = [as_tuple(k, size=3, name="kernel_size") for k in kernel_sizes]
     source_strides = [as_tuple(s, size=3, name="kernel_stride") for s in source_strides]
     if not (len(kernel_sizes) == len(source_strides) == len(dataflow)):
         raise ValueError("All argument lists must have the same length in build_kmap_streamed")
-    return _C.cuda_binary_search_streamed(voxels, kernel_sizes, source_strides, list(dataflow))
+    return _C.cuda_binary_search_streamed(voxels, kernel_sizes, source_strides, list(dataflow), int(begin))
 
 
 def prepare_row_order(kmap: torch.Tensor, num_targets: int, request: int = -1) -> List[torch.Tensor]:
