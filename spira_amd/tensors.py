@@ -83,9 +83,13 @@ class SparseTensor:
 
     def order(self) -> "SparseTensor":
         """Pack and sort the coordinates; features follow the sort."""
-        from .nn.functional.indexing import flat_sort
+        from .nn.functional._native import _C
+        from .nn.functional.indexing import _require_gpu
 
-        keys, index = flat_sort(self._coordinates, self._double)
-        self._coordinates = keys.contiguous()
-        self._features = self._features[index].contiguous()
+        coordinates = self._coordinates.contiguous()
+        _require_gpu(coordinates)
+        # (the int32 permutation indexes directly: no int64 copy of it)
+        keys, index = _C.cuda_flatten_sort(coordinates, self._double)
+        self._coordinates = keys
+        self._features = self._features.index_select(0, index)
         return self
