@@ -201,6 +201,17 @@ int spira_hip_kmap_emit_masks(const int32_t *kernel_map, int64_t num_sources, in
 int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_targets, int num_offsets,
                                     int64_t aligned_sources, int32_t *out, hipStream_t stream);
 
+/* spira_hip_convert_transposed_os for a map whose entries partition the
+ * sources [0, num_sources): every source in exactly one entry, as in a
+ * down-sampling map whose kernel equals its stride (the networks' k = 2,
+ * stride-2 maps).  One pass writes whole rows: no fill, then scatter.  Any
+ * other map gives wrong rows here; take spira_hip_convert_transposed_os.
+ * (No counterpart in the reference: a special case of
+ * cuda_convert_transposed_os, torch/cuda_sparse_convolution_mapping.cu:1809-1830.) */
+int spira_hip_convert_transposed_os_partition(const int32_t *out_in_map, int64_t aligned_targets, int num_offsets,
+                                              int64_t num_sources, int64_t aligned_sources, int32_t *out,
+                                              hipStream_t stream);
+
 /* Workspace bytes for spira_hip_kmap_row_order. */
 int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes);
 

@@ -634,6 +634,27 @@ __global__ void convert_transposed_kernel(const int32_t *__restrict__ map, int64
   out[static_cast<int64_t>(s) * K + i % K] = static_cast<int32_t>(i / K);
 }
 
+// The inverse of a map whose entries partition the sources (every source in
+// exactly one entry: a down-sampling map whose kernel is its stride), in one
+// pass: the entry (t, k) of source s writes all of row s (t at column k, -1
+// elsewhere), and the padding rows [S, Sp) are -1.  Threads [0, n) take
+// entries, [n, n + pad) padding words.
+__global__ void convert_transposed_partition_kernel(const int32_t *__restrict__ map, int64_t n, int K, int64_t S,
+                                                    int64_t Sp, int32_t *__restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) {
+    const int64_t w = S * K + (i - n);
+    if (w < Sp * K) out[w] = -1;
+    return;
+  }
+  const int32_t s = map[i];
+  if (s < 0 || s >= S) return;
+  const int k = static_cast<int>(i % K);
+  const int32_t t = static_cast<int32_t>(i / K);
+  int32_t *row = out + static_cast<int64_t>(s) * K;
+  for (int j = 0; j < K; ++j) row[j] = j == k ? t : -1;
+}
+
 // Row-order key of an output-stationary map row: the bitmask of its valid
 // columns (the first 63 columns, with bit 63 flagging any valid column past
 // them), so that sorting groups rows with identical neighbour patterns.
@@ -1130,6 +1151,19 @@ int spira_hip_convert_transposed_os(const int32_t *out_in_map, int64_t aligned_t
 
 int spira_hip_fill_i32(int32_t *ptr, int64_t n, int32_t value, hipStream_t stream) {
   return fill_i32(ptr, n, value, stream);
+}
+
+int spira_hip_convert_transposed_os_partition(const int32_t *out_in_map, int64_t aligned_targets, int num_offsets,
+                                              int64_t num_sources, int64_t aligned_sources, int32_t *out,
+                                              hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(num_offsets >= 1 && num_sources >= 0 && aligned_sources >= num_sources,
+                    "convert_transposed_os_partition: bad sizes");
+  const int64_t n = aligned_targets * num_offsets, pad = (aligned_sources - num_sources) * num_offsets;
+  if (n + pad == 0) return kOk;
+  hipLaunchKernelGGL(convert_transposed_partition_kernel, dim3(div_up(n + pad, 256)), dim3(256), 0, stream,
+                     out_in_map, n, num_offsets, num_sources, aligned_sources, out);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
 }
 
 int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes) {

@@ -268,16 +268,24 @@ KmapTuple binary_search_no_small_z(const torch::Tensor &sources, const torch::Te
 }
 
 // (reference: CUDAConvertTransposedOs, mapping.cu:1809-1830)
-torch::Tensor convert_transposed_os(const torch::Tensor &out_in_map, int64_t num_sources) {
+// partition: the map's entries partition the sources (a down-sampling map
+// whose kernel is its stride), which one pass inverts
+torch::Tensor convert_transposed_os(const torch::Tensor &out_in_map, int64_t num_sources, bool partition) {
   SPIRA_CHECK_ARG(out_in_map.dim() == 2 && out_in_map.scalar_type() == torch::kInt32,
                   "out_in_map must be a 2-D int32 tensor");
   require_device(out_in_map, "out_in_map");
   const int64_t Sp = round128(num_sources);
   auto out = empty_i32({Sp, out_in_map.size(1)}, out_in_map.device());
-  check_rc(spira_hip_convert_transposed_os(out_in_map.data_ptr<int32_t>(), out_in_map.size(0),
-                                           static_cast<int>(out_in_map.size(1)), Sp, out.data_ptr<int32_t>(),
-                                           current_stream()),
-           "convert_transposed_os");
+  if (partition)
+    check_rc(spira_hip_convert_transposed_os_partition(out_in_map.data_ptr<int32_t>(), out_in_map.size(0),
+                                                       static_cast<int>(out_in_map.size(1)), num_sources, Sp,
+                                                       out.data_ptr<int32_t>(), current_stream()),
+             "convert_transposed_os");
+  else
+    check_rc(spira_hip_convert_transposed_os(out_in_map.data_ptr<int32_t>(), out_in_map.size(0),
+                                             static_cast<int>(out_in_map.size(1)), Sp, out.data_ptr<int32_t>(),
+                                             current_stream()),
+             "convert_transposed_os");
   return out;
 }
 
@@ -321,7 +329,8 @@ void register_mapping(pybind11::module_ &m) {
   m.def("cuda_binary_search_streamed", &binary_search_streamed, pybind11::arg("voxels"), pybind11::arg("kernel_sizes"),
         pybind11::arg("source_strides"), pybind11::arg("dataflow"), pybind11::arg("begin") = 0);
   m.def("cuda_binary_search_no_small_z", &binary_search_no_small_z);
-  m.def("cuda_convert_transposed_os", &convert_transposed_os);
+  m.def("cuda_convert_transposed_os", &convert_transposed_os, pybind11::arg("out_in_map"), pybind11::arg("num_sources"),
+        pybind11::arg("partition") = false);
 }
 
 }  // namespace spira_host

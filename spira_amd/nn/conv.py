@@ -82,7 +82,13 @@ class KernelMapCache:
                 entry[0] = True
             if (map_dataflow == 0 or force_os) and transposed:
                 out = list(entry[1:])
-                out[2] = F.convert_transposed_os(entry[3], entry[1])
+                # The forward map's sources are at target_stride (fine), its
+                # targets at source_stride (coarse, the down-sampled
+                # sources).  With a kernel of 2 (offsets 0 and 1) or 1 per
+                # axis equal to the stride ratio, each fine voxel lies in
+                # exactly one entry, that of its own coarse cell.
+                part = all(k in (1, 2) and c == k * f for f, c, k in zip(target_stride, source_stride, kernel_size))
+                out[2] = F.convert_transposed_os(entry[3], entry[1], partition=part)
                 return out
             return entry[1:]
 

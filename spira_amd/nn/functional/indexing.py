@@ -115,8 +115,11 @@ def build_kmap(sources: torch.Tensor, targets: torch.Tensor, kernel_size: Scalar
                                  as_tuple(source_stride, size=3, name="kernel_stride"), dataflow)
 
 
-def convert_transposed_os(out_in_map: torch.Tensor, input_size: int) -> torch.Tensor:
-    return _C.cuda_convert_transposed_os(out_in_map.contiguous(), input_size)
+def convert_transposed_os(out_in_map: torch.Tensor, input_size: int, partition: bool = False) -> torch.Tensor:
+    """``partition``: every source is in exactly one map entry (a
+    down-sampling map whose kernel equals its stride), so one pass writes
+    whole rows; any other map needs the default."""
+    return _C.cuda_convert_transposed_os(out_in_map.contiguous(), input_size, partition)
 
 
 def build_kmap_no_small_z(sources: torch.Tensor, targets: torch.Tensor, kernel_size: ScalarOrTuple[int],

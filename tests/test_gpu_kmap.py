@@ -300,3 +300,19 @@ def test_network_wide_cache_build(dev, prepare, df):
             order, masks, omap = _native._C.kmap_row_order(m, T)
             o2, m2, om2 = _native._C.kmap_row_order(m.clone(), T)  # computed afresh
             assert torch.equal(order, o2) and torch.equal(masks, m2) and torch.equal(omap, om2)
+
+
+@pytest.mark.parametrize("ks", [(2, 2, 2), (1, 2, 2)])
+def test_convert_transposed_partition(dev, ks):
+    """The one-pass inverse of a down-sampling map whose kernel is its stride
+    (every source in exactly one entry) equals the general inverse, padding
+    rows included: the config-4 scene and a small ragged one."""
+    for c in (scenes.indoor(), scenes.spheres_planes(n=3001, grid=40, seed=2)):
+        k, _ = orc.flatten_sort(c, True)
+        kd = orc.downsample(k, ks)
+        m = orc.build_kmap(k, kd, ks, (1, 1, 1), 0)[2]
+        ref = orc.convert_transposed_os(m, len(k))
+        md = torch.from_numpy(np.ascontiguousarray(m)).to(dev)
+        got = F.convert_transposed_os(md, len(k), partition=True)
+        assert np.array_equal(np_(got), ref)
+        assert np.array_equal(np_(F.convert_transposed_os(md, len(k))), ref)
