@@ -652,7 +652,15 @@ __global__ void convert_transposed_partition_kernel(const int32_t *__restrict__ 
   const int k = static_cast<int>(i % K);
   const int32_t t = static_cast<int32_t>(i / K);
   int32_t *row = out + static_cast<int64_t>(s) * K;
-  for (int j = 0; j < K; ++j) row[j] = j == k ? t : -1;
+  if (K % 4 == 0) {  // 16-byte row chunks (rows start 16-byte aligned)
+    int4 *row4 = reinterpret_cast<int4 *>(row);
+    for (int q = 0; q < K / 4; ++q) {
+      const int b = 4 * q;
+      row4[q] = make_int4(b == k ? t : -1, b + 1 == k ? t : -1, b + 2 == k ? t : -1, b + 3 == k ? t : -1);
+    }
+  } else {
+    for (int j = 0; j < K; ++j) row[j] = j == k ? t : -1;
+  }
 }
 
 // Row-order key of an output-stationary map row: the bitmask of its valid
