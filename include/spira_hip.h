@@ -212,6 +212,22 @@ int spira_hip_convert_transposed_os_partition(const int32_t *out_in_map, int64_t
                                               int64_t num_sources, int64_t aligned_sources, int32_t *out,
                                               hipStream_t stream);
 
+/* Workspace bytes for spira_hip_convert_transposed_os_partition_order. */
+int spira_hip_convert_transposed_os_partition_order_workspace(int64_t num_coarse, int num_offsets, size_t *bytes);
+
+/* spira_hip_convert_transposed_os_partition (out [aligned_sources, K]), and
+ * with it, without a sort, the inverse's row order as spira_hip_kmap_row_order
+ * gives it: order [num_sources], ordered_map [num_sources, K] and
+ * group_masks [ceil(num_sources / 128) * 2].  The inverse has one valid entry
+ * per row, so that order is the rows grouped by column in source order.
+ * out_in_map holds num_coarse rows; K <= 8 and K * ceil(num_coarse / 256) <=
+ * 16384.  (No counterpart in the reference: the row order is this
+ * library's own.) */
+int spira_hip_convert_transposed_os_partition_order(const int32_t *out_in_map, int64_t num_coarse, int num_offsets,
+                                                    int64_t num_sources, int64_t aligned_sources, int32_t *out,
+                                                    int32_t *order, int32_t *ordered_map, uint64_t *group_masks,
+                                                    void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Workspace bytes for spira_hip_kmap_row_order. */
 int spira_hip_kmap_row_order_workspace(int64_t num_targets, size_t *bytes);
 

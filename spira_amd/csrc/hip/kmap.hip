@@ -663,6 +663,140 @@ __global__ void convert_transposed_partition_kernel(const int32_t *__restrict__ 
   }
 }
 
+// ---- row order of a partition map's inverse, without a sort.  The inverse
+// of a map whose entries partition the sources has one valid entry per row
+// (column k, the entry's offset), so its stable (count, mask) row order is
+// the rows grouped by k, each group in source order, which is coarse-row
+// order.  Three launches over 256-row tiles of the coarse map:
+//   tp_count_kernel  per (k, tile) valid counts (and the inverse's padding
+//                    rows, -1);
+//   tp_scan_kernel   one block: the counts' exclusive scan in k-major order
+//                    and every 128-row group's column union (from the k
+//                    bucket bounds);
+//   tp_emit_kernel   each entry's position (bucket base + rank in the tile):
+//                    the order, the ordered map row and the inverse row.
+constexpr int kTpTile = 256;
+constexpr int kTpMaxK = 8;
+constexpr int kTpScanThreads = 1024;
+constexpr int kTpScanPer = 16;  // counts per scan thread: K * ntiles <= 16384
+
+// the row of a partition inverse: t at column k, -1 elsewhere
+__device__ __forceinline__ void tp_row(int32_t *row, int K, int k, int32_t t) {
+  if (K % 4 == 0) {
+    int4 *row4 = reinterpret_cast<int4 *>(row);
+    for (int q = 0; q < K / 4; ++q) {
+      const int b = 4 * q;
+      row4[q] = make_int4(b == k ? t : -1, b + 1 == k ? t : -1, b + 2 == k ? t : -1, b + 3 == k ? t : -1);
+    }
+  } else {
+    for (int j = 0; j < K; ++j) row[j] = j == k ? t : -1;
+  }
+}
+
+__global__ __launch_bounds__(kTpTile) void tp_count_kernel(const int32_t *__restrict__ map, int64_t Tc, int K,
+                                                           int ntiles, int32_t *__restrict__ cnt, int64_t S,
+                                                           int64_t Sp, int32_t *__restrict__ inverse) {
+  __shared__ int32_t part[kTpTile / 64][kTpMaxK];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTpTile + tid;
+  for (int k = 0; k < K; ++k) {
+    const bool v = t < Tc && map[t * K + k] >= 0;
+    const uint64_t m = ballot(v);
+    if (lane == 0) part[w][k] = __builtin_popcountll(m);
+  }
+  __syncthreads();
+  if (tid < K) {
+    int c = 0;
+    for (int q = 0; q < kTpTile / 64; ++q) c += part[q][tid];
+    cnt[tid * ntiles + blockIdx.x] = c;
+  }
+  const int64_t pad = (Sp - S) * K;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kTpTile + tid; i < pad;
+       i += static_cast<int64_t>(gridDim.x) * kTpTile)
+    inverse[S * K + i] = -1;
+}
+
+__global__ __launch_bounds__(kTpScanThreads) void tp_scan_kernel(const int32_t *__restrict__ cnt, int K, int ntiles,
+                                                                 int32_t *__restrict__ offs, int64_t S,
+                                                                 uint64_t *__restrict__ masks) {
+  __shared__ int32_t wsum[kTpScanThreads / 64];
+  __shared__ int32_t base[kTpMaxK + 1];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n = K * ntiles;
+  const int i0 = tid * kTpScanPer;
+  int v[kTpScanPer];
+  int sum = 0;
+#pragma unroll
+  for (int r = 0; r < kTpScanPer; ++r) {
+    v[r] = i0 + r < n ? cnt[i0 + r] : 0;
+    sum += v[r];
+  }
+  int incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int run = incl - sum;
+  for (int q = 0; q < w; ++q) run += wsum[q];
+#pragma unroll
+  for (int r = 0; r < kTpScanPer; ++r) {
+    const int i = i0 + r;
+    if (i < n) {
+      offs[i] = run;
+      if (i % ntiles == 0) base[i / ntiles] = run;  // bucket k starts here
+    }
+    run += v[r];
+  }
+  if (tid == kTpScanThreads - 1) base[K] = run;  // the total
+  __syncthreads();
+  // column unions of the 128-row groups of the ordered rows
+  const int64_t total = base[K];
+  const int64_t G = (S + 127) / 128;
+  for (int64_t g = tid; g < G; g += kTpScanThreads) {
+    const int64_t lo = g * 128, hi = lo + 128 < total ? lo + 128 : total;
+    uint64_t bits = 0;
+    for (int k = 0; k < K; ++k)
+      if (base[k + 1] > base[k] && base[k] < hi && base[k + 1] > lo) bits |= uint64_t(1) << k;
+    masks[2 * g] = bits;
+    masks[2 * g + 1] = 0;
+  }
+}
+
+__global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restrict__ map, int64_t Tc, int K,
+                                                          int ntiles, const int32_t *__restrict__ offs, int64_t S,
+                                                          int32_t *__restrict__ order,
+                                                          int32_t *__restrict__ ordered_map,
+                                                          int32_t *__restrict__ inverse) {
+  __shared__ int32_t part[kTpTile / 64][kTpMaxK];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTpTile + tid;
+  // (loops over the compile-time maximum, so that src / rank stay in registers)
+  int32_t src[kTpMaxK];
+  int rank[kTpMaxK];
+#pragma unroll
+  for (int k = 0; k < kTpMaxK; ++k) {
+    src[k] = (k < K && t < Tc) ? map[t * K + k] : -1;
+    const uint64_t m = ballot(src[k] >= 0);
+    rank[k] = lane_prefix(m);
+    if (lane == 0 && k < K) part[w][k] = __builtin_popcountll(m);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kTpMaxK; ++k) {
+    const int32_t s = src[k];
+    if (s < 0 || s >= S) continue;
+    int pos = offs[k * ntiles + blockIdx.x] + rank[k];
+    for (int q = 0; q < w; ++q) pos += part[q][k];
+    if (pos >= S) continue;  // (only if the entries do not partition the sources)
+    order[pos] = s;
+    tp_row(ordered_map + static_cast<int64_t>(pos) * K, K, k, static_cast<int32_t>(t));
+    tp_row(inverse + static_cast<int64_t>(s) * K, K, k, static_cast<int32_t>(t));
+  }
+}
+
 // Row-order key of an output-stationary map row: the bitmask of its valid
 // columns (the first 63 columns, with bit 63 flagging any valid column past
 // them), so that sorting groups rows with identical neighbour patterns.
@@ -1170,6 +1304,40 @@ int spira_hip_convert_transposed_os_partition(const int32_t *out_in_map, int64_t
   if (n + pad == 0) return kOk;
   hipLaunchKernelGGL(convert_transposed_partition_kernel, dim3(div_up(n + pad, 256)), dim3(256), 0, stream,
                      out_in_map, n, num_offsets, num_sources, aligned_sources, out);
+  SPIRA_HIP_LAUNCH_CHECK();
+  return kOk;
+}
+
+int spira_hip_convert_transposed_os_partition_order_workspace(int64_t num_coarse, int num_offsets, size_t *bytes) {
+  const int64_t ntiles = div_up(std::max<int64_t>(num_coarse, 1), kTpTile);
+  *bytes = static_cast<size_t>(2 * num_offsets * ntiles) * sizeof(int32_t);
+  return kOk;
+}
+
+int spira_hip_convert_transposed_os_partition_order(const int32_t *out_in_map, int64_t num_coarse, int num_offsets,
+                                                    int64_t num_sources, int64_t aligned_sources, int32_t *out,
+                                                    int32_t *order, int32_t *ordered_map, uint64_t *group_masks,
+                                                    void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  const int K = num_offsets;
+  SPIRA_HIP_REQUIRE(K >= 1 && K <= kTpMaxK, "convert_transposed_os_partition_order: at most 8 offsets");
+  SPIRA_HIP_REQUIRE(num_coarse >= 0 && num_sources >= 0 && aligned_sources >= num_sources &&
+                        num_sources < (int64_t(1) << 31),
+                    "convert_transposed_os_partition_order: bad sizes");
+  const int64_t ntiles = div_up(std::max<int64_t>(num_coarse, 1), kTpTile);
+  SPIRA_HIP_REQUIRE(K * ntiles <= int64_t(kTpScanThreads) * kTpScanPer,
+                    "convert_transposed_os_partition_order: too many coarse rows");
+  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= static_cast<size_t>(2 * K * ntiles) * sizeof(int32_t),
+                    "convert_transposed_os_partition_order: workspace too small");
+  if (num_sources == 0 && aligned_sources == 0) return kOk;
+  int32_t *cnt = static_cast<int32_t *>(workspace), *offs = cnt + K * ntiles;
+  hipLaunchKernelGGL(tp_count_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTpTile), 0, stream, out_in_map,
+                     num_coarse, K, static_cast<int>(ntiles), cnt, num_sources, aligned_sources, out);
+  SPIRA_HIP_LAUNCH_CHECK();
+  hipLaunchKernelGGL(tp_scan_kernel, dim3(1), dim3(kTpScanThreads), 0, stream, cnt, K, static_cast<int>(ntiles), offs,
+                     num_sources, group_masks);
+  SPIRA_HIP_LAUNCH_CHECK();
+  hipLaunchKernelGGL(tp_emit_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTpTile), 0, stream, out_in_map,
+                     num_coarse, K, static_cast<int>(ntiles), offs, num_sources, order, ordered_map, out);
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }

@@ -87,6 +87,7 @@ struct OrderEntry {
   const void *data = nullptr;
   uint32_t version = 0;
   int64_t T = 0;
+  bool free = false;  // made with the map at no sorting cost (convert_transposed_os_ordered)
   torch::Tensor order, masks, ordered_map;
 };
 
@@ -148,6 +149,61 @@ static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
                                     e.ordered_map.data_ptr<int32_t>(), ws.data_ptr(), wsb, current_stream()),
            "row_order");
   return cache.emplace(key, std::move(e)).first->second;
+}
+
+// The order cached for `map` (same tensor, unchanged, same T), or null.
+static const OrderEntry *cached_order(const torch::Tensor &map, int64_t T) {
+  auto &cache = order_cache();
+  auto it = cache.find(map.unsafeGetTensorImpl());
+  if (it == cache.end()) return nullptr;
+  const OrderEntry &e = it->second;
+  if (e.impl.expired() || e.data != map.data_ptr() || e.version != map._version() || e.T != T) return nullptr;
+  return &e;
+}
+
+// The inverse of a map whose entries partition its sources (a k = 2 or 1
+// down-sampling map with its stride) for a transposed layer, with the
+// inverse's row order made in the same pass (no sort) and cached for it:
+// the fp16 kernel then walks the inverse grouped by column, one offset per
+// 128-row group but at the group boundaries, instead of visiting every
+// offset with one row in K valid.  No reference counterpart (a special case
+// of cuda_convert_transposed_os, torch/cuda_sparse_convolution_mapping.cu:1809-1830).
+torch::Tensor convert_transposed_os_ordered(const torch::Tensor &map, int64_t num_coarse, int64_t num_sources) {
+  SPIRA_CHECK_ARG(map.dim() == 2 && map.scalar_type() == torch::kInt32, "out_in_map must be a 2-D int32 tensor");
+  require_device(map, "out_in_map");
+  SPIRA_CHECK_ARG(num_coarse >= 0 && num_coarse <= map.size(0) && num_sources >= 0, "bad map sizes");
+  const int64_t K = map.size(1);
+  const int64_t Sp = (num_sources + 127) / 128 * 128;
+  auto inverse = empty_i32({Sp, K}, map.device());
+  const int64_t ntiles = (std::max<int64_t>(num_coarse, 1) + 255) / 256;
+  if (!row_order_enabled() || K > 8 || K * ntiles > 16384 || num_sources == 0) {
+    check_rc(spira_hip_convert_transposed_os_partition(map.data_ptr<int32_t>(), map.size(0), static_cast<int>(K),
+                                                       num_sources, Sp, inverse.data_ptr<int32_t>(),
+                                                       current_stream()),
+             "convert_transposed_os_ordered");
+    return inverse;
+  }
+  OrderEntry e(inverse);
+  e.data = inverse.data_ptr();
+  e.version = inverse._version();
+  e.T = num_sources;
+  e.free = true;
+  e.order = empty_i32({num_sources}, map.device());
+  e.masks = torch::empty({(num_sources + 127) / 128 * 2}, torch::TensorOptions(map.device()).dtype(torch::kInt64));
+  e.ordered_map = empty_i32({num_sources, K}, map.device());
+  size_t wsb = 0;
+  check_rc(spira_hip_convert_transposed_os_partition_order_workspace(num_coarse, static_cast<int>(K), &wsb),
+           "convert_transposed_os_ordered");
+  auto ws = workspace(wsb, map.device());
+  check_rc(spira_hip_convert_transposed_os_partition_order(
+               map.data_ptr<int32_t>(), num_coarse, static_cast<int>(K), num_sources, Sp, inverse.data_ptr<int32_t>(),
+               e.order.data_ptr<int32_t>(), e.ordered_map.data_ptr<int32_t>(),
+               reinterpret_cast<uint64_t *>(e.masks.data_ptr<int64_t>()), ws.data_ptr(), wsb, current_stream()),
+           "convert_transposed_os_ordered");
+  auto &cache = order_cache();
+  cache.erase(inverse.unsafeGetTensorImpl());
+  cache.emplace(inverse.unsafeGetTensorImpl(), std::move(e));
+  return inverse;
 }
 
 // Queue the row order of an output-stationary map now, on the current
@@ -307,11 +363,21 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
   auto ws = zeroed_workspace(wsb, dev);
   const int32_t *order = nullptr;
   const uint64_t *masks = nullptr;
-  if (map && dtype == SPIRA_F16 && !walk && row_order_applies(T, K, tn.row_order)) {
-    const OrderEntry &oe = row_order_of(*map, T);
-    order = oe.order.data_ptr<int32_t>();
-    masks = oe.masks.defined() ? reinterpret_cast<const uint64_t *>(oe.masks.data_ptr<int64_t>()) : nullptr;
-    mp = oe.ordered_map.data_ptr<int32_t>();
+  if (map && dtype == SPIRA_F16 && !walk) {
+    // the library's rule (or the tuning's request) for a sorted order; an
+    // order made at no cost with the map (convert_transposed_os_ordered)
+    // is taken unless the tuning asks against it
+    const OrderEntry *oe = nullptr;
+    if (row_order_applies(T, K, tn.row_order)) oe = &row_order_of(*map, T);
+    else if (tn.row_order != 0 && row_order_enabled()) {
+      oe = cached_order(*map, T);
+      if (oe && !oe->free) oe = nullptr;  // (a sorted order only by the rule or on request)
+    }
+    if (oe) {
+      order = oe->order.data_ptr<int32_t>();
+      masks = oe->masks.defined() ? reinterpret_cast<const uint64_t *>(oe->masks.data_ptr<int64_t>()) : nullptr;
+      mp = oe->ordered_map.data_ptr<int32_t>();
+    }
   }
   // fp16 rows whose width is not a multiple of 8 channels (the 3-channel
   // stem) are padded with zero channels to 16-byte rows, which the MMA
@@ -701,6 +767,13 @@ void register_conv(pybind11::module_ &m) {
   m.def("cuda_reset_error", &reset_error);
   m.def("set_os_row_order", &set_row_order);
   m.def("kmap_row_order", &kmap_row_order);
+  // an order made with the map (no sort), as a partition inverse carries one
+  m.def("has_free_row_order", [](const torch::Tensor &map, int64_t T) {
+    const OrderEntry *e = cached_order(map, T);
+    return e != nullptr && e->free;
+  });
+  m.def("convert_transposed_os_ordered", &convert_transposed_os_ordered, pybind11::arg("out_in_map"),
+        pybind11::arg("num_coarse"), pybind11::arg("num_sources"));
   m.def("conv_os_plan", &conv_os_plan, pybind11::arg("T"), pybind11::arg("K"), pybind11::arg("cin"),
         pybind11::arg("cin2"), pybind11::arg("cout"), pybind11::arg("has_map"),
         pybind11::arg("tuning") = pybind11::none());

@@ -88,7 +88,11 @@ class KernelMapCache:
                 # axis equal to the stride ratio, each fine voxel lies in
                 # exactly one entry, that of its own coarse cell.
                 part = all(k in (1, 2) and c == k * f for f, c, k in zip(target_stride, source_stride, kernel_size))
-                out[2] = F.convert_transposed_os(entry[3], entry[1], partition=part)
+                if part:
+                    # (with its row order, made in the same pass)
+                    out[2] = F.convert_transposed_os_ordered(entry[3], entry[2], entry[1])
+                else:
+                    out[2] = F.convert_transposed_os(entry[3], entry[1])
                 return out
             return entry[1:]
 

@@ -15,7 +15,7 @@ from ...utils.typing import ScalarOrTuple
 from ._native import _C
 
 __all__ = [
-    "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os",
+    "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os", "convert_transposed_os_ordered",
     "build_kmap_streamed", "streamed_output_generate", "downsample_chain_launch", "build_kmap_no_small_z", "sparse_quantize",
     "prepare_row_order",
 ]
@@ -113,6 +113,14 @@ def build_kmap(sources: torch.Tensor, targets: torch.Tensor, kernel_size: Scalar
     targets = targets.contiguous()
     return _C.cuda_binary_search(sources, targets, as_tuple(kernel_size, size=3, name="kernel_size"),
                                  as_tuple(source_stride, size=3, name="kernel_stride"), dataflow)
+
+
+def convert_transposed_os_ordered(out_in_map: torch.Tensor, num_coarse: int, input_size: int) -> torch.Tensor:
+    """:func:`convert_transposed_os` with ``partition=True`` (``out_in_map``
+    has ``num_coarse`` rows of targets), and the inverse's row order made in
+    the same pass and kept for the fp16 convolution that walks it."""
+    _require_gpu(out_in_map)
+    return _C.convert_transposed_os_ordered(out_in_map.contiguous(), int(num_coarse), int(input_size))
 
 
 def convert_transposed_os(out_in_map: torch.Tensor, input_size: int, partition: bool = False) -> torch.Tensor:

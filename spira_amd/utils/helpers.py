@@ -284,7 +284,11 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
             # faster for it: the map's order pays if the layers' best walks
             # plus the sort beat index order everywhere
             best1 = [min(t0, t1) for (_, t0), (_, t1) in zip(picks[0], picks[1])]
-            totals[1] = sum(best1) + _row_order_ms(omap, T)
+            # (an order made with the map, as a transposed layer's
+            # partition inverse carries one, costs no sort)
+            from ..nn.functional import _native
+            sort_ms = 0.0 if _native._C.has_free_row_order(omap, int(T)) else _row_order_ms(omap, T)
+            totals[1] = sum(best1) + sort_ms
             r = 1 if totals[1] < (1.0 - ROW_ORDER_MARGIN) * totals[0] else 0
             requests[key] = r
             if verbose:

@@ -9,7 +9,7 @@ from oracle import oracle as orc
 from spira_amd import scenes
 from spira_amd.nn import functional as F
 
-from helpers import assert_tuple_equal, np_
+from helpers import assert_tuple_equal, np_, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -316,3 +316,34 @@ def test_convert_transposed_partition(dev, ks):
         got = F.convert_transposed_os(md, len(k), partition=True)
         assert np.array_equal(np_(got), ref)
         assert np.array_equal(np_(F.convert_transposed_os(md, len(k))), ref)
+
+
+@pytest.mark.parametrize("ks", [(2, 2, 2), (1, 2, 2)])
+def test_convert_transposed_partition_order(dev, ks):
+    """The inverse of a partition map with its row order made in the same
+    pass: the inverse equals the oracle's, and the cached order, group masks
+    and ordered map equal the general row order of the same inverse (computed
+    on a copy, sorted); a transposed fp16 layer walking it matches the oracle."""
+    from spira_amd.nn.functional._native import _C
+    for c in (scenes.indoor(), scenes.spheres_planes(n=3001, grid=40, seed=2)):
+        k, _ = orc.flatten_sort(c, True)
+        for s in (1, 2, 4):
+            kf = k if s == 1 else orc.downsample(k, (s,) * 3)
+            st = tuple(s * q for q in ks)
+            kc = orc.downsample(k, st)
+            m = orc.build_kmap(kf, kc, ks, (s,) * 3, 0)[2]
+            S, T = len(kf), len(kc)
+            print(f"[partition order] S={S} T={T} ks={ks} stride={s}", flush=True)
+            md = torch.from_numpy(np.ascontiguousarray(m)).to(dev)
+            inv = F.convert_transposed_os_ordered(md, T, S)
+            assert np.array_equal(np_(inv), orc.convert_transposed_os(m, S))
+            got = [np_(t) for t in _C.kmap_row_order(inv, S)]
+            ref = [np_(t) for t in _C.kmap_row_order(inv.clone(), S)]
+            for g, r in zip(got, ref):
+                assert np.array_equal(g, r)
+    g = torch.Generator().manual_seed(3)
+    X = torch.randn(T, 64, generator=g).half()
+    W = (torch.randn(m.shape[1], 64, 48, generator=g) / 20).half()
+    invn = orc.convert_transposed_os(m, S)
+    y = F.sparse_convolution_forward_os(T, S, inv, X.to(dev), W.to(dev))
+    assert rel_err(np_(y.float()), orc.conv_os(invn, S, X.double().numpy(), W.double().numpy())) <= 1e-2
