@@ -347,3 +347,17 @@ def test_convert_transposed_partition_order(dev, ks):
     invn = orc.convert_transposed_os(m, S)
     y = F.sparse_convolution_forward_os(T, S, inv, X.to(dev), W.to(dev))
     assert rel_err(np_(y.float()), orc.conv_os(invn, S, X.double().numpy(), W.double().numpy())) <= 1e-2
+
+
+def test_downsample_chain_large(dev):
+    """An input above 1024 compaction tiles (2.3M keys): the chained
+    downsample takes the device-wide scan at every level (the levels are
+    sized by the input); every level against the oracle."""
+    rng = np.random.default_rng(31)
+    c = np.unique(rng.integers(0, 600, size=(2_300_000, 3)), axis=0).astype(np.int32)
+    assert len(c) > 2048 * 1024
+    rk, _ = orc.flatten_sort(c, True)
+    strides = [(2, 2, 2), (4, 4, 4), (8, 8, 8), (16, 16, 16)]
+    outs = F.streamed_output_generate(torch.from_numpy(rk).to(dev), strides)
+    for o, s in zip(outs, strides):
+        assert np.array_equal(np_(o), orc.downsample(rk, s)), s
