@@ -667,18 +667,17 @@ __global__ void convert_transposed_partition_kernel(const int32_t *__restrict__ 
 // of a map whose entries partition the sources has one valid entry per row
 // (column k, the entry's offset), so its stable (count, mask) row order is
 // the rows grouped by k, each group in source order, which is coarse-row
-// order.  Three launches over 256-row tiles of the coarse map:
+// order.  Two launches over 256-row tiles of the coarse map:
 //   tp_count_kernel  per (k, tile) valid counts (and the inverse's padding
 //                    rows, -1);
-//   tp_scan_kernel   one block: the counts' exclusive scan in k-major order
-//                    and every 128-row group's column union (from the k
-//                    bucket bounds);
-//   tp_emit_kernel   each entry's position (bucket base + rank in the tile):
-//                    the order, the ordered map row and the inverse row.
+//   tp_emit_kernel   each block sums the counts (its tile's base in each
+//                    bucket, the bucket totals), then each entry's position
+//                    (bucket base + rank in the tile): the order, the ordered
+//                    map row and the inverse row; block 0 also writes every
+//                    128-row group's column union (from the bucket bounds).
 constexpr int kTpTile = 256;
 constexpr int kTpMaxK = 8;
-constexpr int kTpScanThreads = 1024;
-constexpr int kTpScanPer = 16;  // counts per scan thread: K * ntiles <= 16384
+constexpr int kTpMaxCounts = 16384;  // K * ntiles: each emit block sums them all
 
 // the row of a partition inverse: t at column k, -1 elsewhere
 __device__ __forceinline__ void tp_row(int32_t *row, int K, int k, int32_t t) {
@@ -716,63 +715,73 @@ __global__ __launch_bounds__(kTpTile) void tp_count_kernel(const int32_t *__rest
     inverse[S * K + i] = -1;
 }
 
-__global__ __launch_bounds__(kTpScanThreads) void tp_scan_kernel(const int32_t *__restrict__ cnt, int K, int ntiles,
-                                                                 int32_t *__restrict__ offs, int64_t S,
-                                                                 uint64_t *__restrict__ masks) {
-  __shared__ int32_t wsum[kTpScanThreads / 64];
-  __shared__ int32_t base[kTpMaxK + 1];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int n = K * ntiles;
-  const int i0 = tid * kTpScanPer;
-  int v[kTpScanPer];
-  int sum = 0;
-#pragma unroll
-  for (int r = 0; r < kTpScanPer; ++r) {
-    v[r] = i0 + r < n ? cnt[i0 + r] : 0;
-    sum += v[r];
-  }
-  int incl = sum;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
-  if (lane == 63) wsum[w] = incl;
-  __syncthreads();
-  int run = incl - sum;
-  for (int q = 0; q < w; ++q) run += wsum[q];
-#pragma unroll
-  for (int r = 0; r < kTpScanPer; ++r) {
-    const int i = i0 + r;
-    if (i < n) {
-      offs[i] = run;
-      if (i % ntiles == 0) base[i / ntiles] = run;  // bucket k starts here
-    }
-    run += v[r];
-  }
-  if (tid == kTpScanThreads - 1) base[K] = run;  // the total
-  __syncthreads();
-  // column unions of the 128-row groups of the ordered rows
-  const int64_t total = base[K];
-  const int64_t G = (S + 127) / 128;
-  for (int64_t g = tid; g < G; g += kTpScanThreads) {
-    const int64_t lo = g * 128, hi = lo + 128 < total ? lo + 128 : total;
-    uint64_t bits = 0;
-    for (int k = 0; k < K; ++k)
-      if (base[k + 1] > base[k] && base[k] < hi && base[k + 1] > lo) bits |= uint64_t(1) << k;
-    masks[2 * g] = bits;
-    masks[2 * g + 1] = 0;
-  }
-}
-
 __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restrict__ map, int64_t Tc, int K,
-                                                          int ntiles, const int32_t *__restrict__ offs, int64_t S,
+                                                          int ntiles, const int32_t *__restrict__ cnt, int64_t S,
                                                           int32_t *__restrict__ order,
                                                           int32_t *__restrict__ ordered_map,
-                                                          int32_t *__restrict__ inverse) {
+                                                          int32_t *__restrict__ inverse,
+                                                          uint64_t *__restrict__ masks) {
   __shared__ int32_t part[kTpTile / 64][kTpMaxK];
+  __shared__ int32_t red[kTpTile / 64][2 * kTpMaxK];
+  __shared__ int32_t base[kTpMaxK + 1], tile_base[kTpMaxK];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kTpTile + tid;
+  // this tile's position in each bucket: the counts of the tiles before it,
+  // and the buckets' totals (every block sums the K * ntiles counts itself)
+  {
+    int before[kTpMaxK], total[kTpMaxK];
+#pragma unroll
+    for (int k = 0; k < kTpMaxK; ++k) before[k] = total[k] = 0;
+    for (int q = tid; q < ntiles; q += kTpTile) {
+#pragma unroll
+      for (int k = 0; k < kTpMaxK; ++k) {
+        const int c = k < K ? cnt[k * ntiles + q] : 0;
+        total[k] += c;
+        before[k] += q < static_cast<int>(blockIdx.x) ? c : 0;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kTpMaxK; ++k) {
+      for (int d = 32; d > 0; d >>= 1) {
+        before[k] += __shfl_xor(before[k], d, 64);
+        total[k] += __shfl_xor(total[k], d, 64);
+      }
+      if (lane == 0) {
+        red[w][k] = before[k];
+        red[w][kTpMaxK + k] = total[k];
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int run = 0;
+      for (int k = 0; k < K; ++k) {
+        int b = 0, tot = 0;
+        for (int q = 0; q < kTpTile / 64; ++q) {
+          b += red[q][k];
+          tot += red[q][kTpMaxK + k];
+        }
+        base[k] = run;
+        tile_base[k] = run + b;
+        run += tot;
+      }
+      base[K] = run;
+    }
+    __syncthreads();
+  }
+  // block 0: the column union of every 128-row group of the ordered rows
+  // (from the k bucket bounds)
+  if (blockIdx.x == 0) {
+    const int64_t total = base[K];
+    const int64_t G = (S + 127) / 128;
+    for (int64_t g = tid; g < G; g += kTpTile) {
+      const int64_t lo = g * 128, hi = lo + 128 < total ? lo + 128 : total;
+      uint64_t bits = 0;
+      for (int k = 0; k < K; ++k)
+        if (base[k + 1] > base[k] && base[k] < hi && base[k + 1] > lo) bits |= uint64_t(1) << k;
+      masks[2 * g] = bits;
+      masks[2 * g + 1] = 0;
+    }
+  }
   // (loops over the compile-time maximum, so that src / rank stay in registers)
   int32_t src[kTpMaxK];
   int rank[kTpMaxK];
@@ -788,7 +797,7 @@ __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restr
   for (int k = 0; k < kTpMaxK; ++k) {
     const int32_t s = src[k];
     if (s < 0 || s >= S) continue;
-    int pos = offs[k * ntiles + blockIdx.x] + rank[k];
+    int pos = tile_base[k] + rank[k];
     for (int q = 0; q < w; ++q) pos += part[q][k];
     if (pos >= S) continue;  // (only if the entries do not partition the sources)
     order[pos] = s;
@@ -1310,7 +1319,7 @@ int spira_hip_convert_transposed_os_partition(const int32_t *out_in_map, int64_t
 
 int spira_hip_convert_transposed_os_partition_order_workspace(int64_t num_coarse, int num_offsets, size_t *bytes) {
   const int64_t ntiles = div_up(std::max<int64_t>(num_coarse, 1), kTpTile);
-  *bytes = static_cast<size_t>(2 * num_offsets * ntiles) * sizeof(int32_t);
+  *bytes = static_cast<size_t>(num_offsets * ntiles) * sizeof(int32_t);
   return kOk;
 }
 
@@ -1324,20 +1333,16 @@ int spira_hip_convert_transposed_os_partition_order(const int32_t *out_in_map, i
                         num_sources < (int64_t(1) << 31),
                     "convert_transposed_os_partition_order: bad sizes");
   const int64_t ntiles = div_up(std::max<int64_t>(num_coarse, 1), kTpTile);
-  SPIRA_HIP_REQUIRE(K * ntiles <= int64_t(kTpScanThreads) * kTpScanPer,
-                    "convert_transposed_os_partition_order: too many coarse rows");
-  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= static_cast<size_t>(2 * K * ntiles) * sizeof(int32_t),
+  SPIRA_HIP_REQUIRE(K * ntiles <= kTpMaxCounts, "convert_transposed_os_partition_order: too many coarse rows");
+  SPIRA_HIP_REQUIRE(workspace != nullptr && workspace_bytes >= static_cast<size_t>(K * ntiles) * sizeof(int32_t),
                     "convert_transposed_os_partition_order: workspace too small");
   if (num_sources == 0 && aligned_sources == 0) return kOk;
-  int32_t *cnt = static_cast<int32_t *>(workspace), *offs = cnt + K * ntiles;
+  int32_t *cnt = static_cast<int32_t *>(workspace);
   hipLaunchKernelGGL(tp_count_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTpTile), 0, stream, out_in_map,
                      num_coarse, K, static_cast<int>(ntiles), cnt, num_sources, aligned_sources, out);
   SPIRA_HIP_LAUNCH_CHECK();
-  hipLaunchKernelGGL(tp_scan_kernel, dim3(1), dim3(kTpScanThreads), 0, stream, cnt, K, static_cast<int>(ntiles), offs,
-                     num_sources, group_masks);
-  SPIRA_HIP_LAUNCH_CHECK();
   hipLaunchKernelGGL(tp_emit_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTpTile), 0, stream, out_in_map,
-                     num_coarse, K, static_cast<int>(ntiles), offs, num_sources, order, ordered_map, out);
+                     num_coarse, K, static_cast<int>(ntiles), cnt, num_sources, order, ordered_map, out, group_masks);
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
 }
