@@ -135,9 +135,12 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
 // kernels are latency-bound: more resident waves beat larger wave tiles),
 // the ring depth, and the waves per SIMD the register budget targets: 4 for
 // up to 96 columns (<= 128 VGPRs, four 40 KiB blocks per CU), 3 for 128.
-template <int WN, int NKS = 2> struct TileOf {
+// DS = 1: one more ring stage for 64-channel steps of wide tiles (chosen
+// where the larger blocks still fit the grid in one round, os_deep_ring).
+template <int WN, int NKS = 2, int DS = 0> struct TileOf {
   static constexpr int MT = 1;
-  static constexpr int NS = NKS == 2 ? (WN >= 3 ? 3 : 4) : (NKS == 8 || WN >= 3 ? 2 : 3);
+  static_assert(DS == 0 || NKS == 4, "the extra ring stage is for 64-channel steps");
+  static constexpr int NS = (NKS == 2 ? (WN >= 3 ? 3 : 4) : (NKS == 8 || WN >= 3 ? 2 : 3)) + DS;
   static constexpr int WAVES = WN <= 3 ? 4 : 3;
   using C = Cfg<WN, MT, NS, NKS>;
 };
@@ -662,12 +665,12 @@ __device__ __forceinline__ void xcd_block(int64_t &bx, int &by, int &bz) {
 // logical row i is target order[i] and `map` holds the rows in logical order;
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
-template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
+template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP, int DS = 0>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS, DS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
                                                     Operands op, void *Y, Epilogue epi, int xcd_order) {
-  using C = typename ring::TileOf<WN, NKS>::C;
+  using C = typename ring::TileOf<WN, NKS, DS>::C;
   constexpr int MT = C::BM / 128, NS = C::NS;
   __shared__ __align__(1024) char ring_lds[C::LDS];
   // map entries of a later step, per stage and packed offset (untiled maps;
@@ -1368,14 +1371,19 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
     default: CALL(4); break;      \
   }
 
-template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1>
+template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1, int DS = 0>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                       void *Y, const Epilogue &epi, int xcd = 0) {
 #define SPIRA_OS_CALL(W)                                                                                             \
-  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP>), grid, dim3(256), 0, s, map, order, rowmask, T, Kc, \
-                     jper, op, Y, epi, xcd)
-  SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS>), grid, dim3(256), 0, s, map, order, rowmask, T,  \
+                     Kc, jper, op, Y, epi, xcd)
+  if constexpr (DS == 1) {  // (96- and 128-column tiles only)
+    if (wn == 3) SPIRA_OS_CALL(3);
+    else SPIRA_OS_CALL(4);
+  } else {
+    SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
+  }
 #undef SPIRA_OS_CALL
 }
 
@@ -1417,6 +1425,22 @@ static int os_wn(int64_t num_targets, int c_out, int cus, int col_tile) {
   return wn;
 }
 
+// A third ring stage for 64-channel steps of 96- and 128-column tiles (two
+// steps of gathers in flight instead of one) where the grid, at the larger
+// block's LDS, still runs in one round of resident blocks.  (Measured on the
+// config-4 layers, untuned: the stride-8 256 -> 256 transposed layer 49.2 ->
+// 33.1 us, the stride-8 384 -> 256 1x1 layer 28.3 -> 22.1 us; the 529-block
+// stride-4 128 -> 128 layers, two blocks per CU at 62 KiB, went 82.9 ->
+// 96.2 us with the tail round, so they keep two stages.)
+static bool os_deep_ring(int wn, int nks, int64_t blocks, int cus) {
+  if (nks != 4 || wn < 3) return false;
+  constexpr int kLdsPerCu = 160 * 1024;
+  const int lds = wn == 3 ? ring::TileOf<3, 4, 1>::C::LDS : ring::TileOf<4, 4, 1>::C::LDS;
+  const int waves = wn == 3 ? ring::TileOf<3, 4, 1>::WAVES : ring::TileOf<4, 4, 1>::WAVES;
+  const int per_cu = std::min(kLdsPerCu / lds, waves);
+  return blocks <= static_cast<int64_t>(per_cu) * cus;
+}
+
 static spira_hip_os_tuning_t tuning_of(const spira_hip_os_tuning_t *t) {
   spira_hip_os_tuning_t r{};
   if (t) r = *t;
@@ -1441,7 +1465,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
 // block, offsets per split (jper), 16-channel slices per step (nks), kernel
 // offsets per step (pack: 1, 2 or 4) and the grid.
 struct OsPlan {
-  int wn, bm, jper, splits, nks, pack, xcd;
+  int wn, bm, jper, splits, nks, pack, xcd, deep;
   bool aligned;
   int64_t gx, gy;
 };
@@ -1480,6 +1504,7 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
     pl.pack = 2;
     pl.nks = 8;
   }
+  pl.deep = pl.pack == 1 && os_deep_ring(pl.wn, pl.nks, pl.gx * pl.gy * pl.splits, cus) ? 1 : 0;
   return pl;
 }
 
@@ -1507,10 +1532,14 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
     // channel concatenations: storage-dtype outputs (split or not)
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
       if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 4 && pl.deep)
+        launch_os<MODE, true, 4, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
     }
   } else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else if (nks == 4 && pl.deep)
+    launch_os<MODE, true, 4, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
 }
