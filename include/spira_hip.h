@@ -297,8 +297,12 @@ int spira_hip_prepare_weights(const void *weights, int num_offsets, int c_in, in
  *                  inputs of kernels above 27 offsets: 1 (none), 2 or 4;
  *   block_order    1: the blocks that the hardware sends to one XCD (one
  *                  of 8 L2 slices) take one contiguous range of row tiles,
- *                  so that each L2 serves a slab of the map; 0 (default):
- *                  row tiles in dispatch order.
+ *                  so that each L2 serves a slab of the map; 2, 3, 4: runs
+ *                  of 4, 8, 16 consecutive blocks per XCD, dealt to the
+ *                  XCDs in turn (neighbouring row tiles share an L2, every
+ *                  XCD gets its share of the long blocks that a row-ordered
+ *                  map puts first); 0 (default): row tiles in dispatch
+ *                  order.
  * (No reference counterpart: these are the selector's CDNA4 parameters; the
  * reference selector sweeps gather / scatter tile sizes instead,
  * source/spira/nn/conv.py:217-307.) */

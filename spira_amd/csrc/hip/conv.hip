@@ -646,12 +646,30 @@ __device__ __forceinline__ void store_tile_vec(const floatx4 (&acc)[2][2 * WN], 
 // contiguous range of the logical (row tile, column tile, split) order,
 // column tiles innermost, so that the XCD's L2 serves one slab of rows (and
 // the column tiles of a row tile run on one XCD, close in time).
-__device__ __forceinline__ void xcd_block(int64_t &bx, int &by, int &bz) {
+// order >= 2: runs of c = 2^order consecutive blocks per XCD, dealt to the
+// XCDs in turn.  Hardware ids [8cs, 8c(s + 1)) (round s) give each XCD c
+// blocks; XCD x's k-th block of round s is logical block 8cs + cx + k.  The
+// last, partial round keeps its ids.  Consecutive blocks (a row tile's
+// column tiles, then neighbouring row tiles) share an L2 while every XCD
+// still gets its share of each part of the grid (row-ordered maps put the
+// longest blocks first, so one contiguous range per XCD is unbalanced).
+__device__ __forceinline__ void xcd_block(int64_t &bx, int &by, int &bz, int order) {
   constexpr int64_t kXcds = 8;
   const int64_t X = gridDim.x, Y = gridDim.y, Z = gridDim.z, G = X * Y * Z;
   const int64_t w = blockIdx.x + X * (blockIdx.y + Y * static_cast<int64_t>(blockIdx.z));
-  const int64_t q = G / kXcds, r = G % kXcds, x = w % kXcds, i = w / kXcds;
-  const int64_t L = x * q + (x < r ? x : r) + i;  // a bijection of [0, G)
+  int64_t L;
+  if (order == 1) {
+    const int64_t q = G / kXcds, r = G % kXcds, x = w % kXcds, i = w / kXcds;
+    L = x * q + (x < r ? x : r) + i;  // a bijection of [0, G)
+  } else {
+    const int64_t c = int64_t(1) << order, round = kXcds * c;
+    if (w < G / round * round) {
+      const int64_t x = w % kXcds, i = w / kXcds;
+      L = (i / c) * round + x * c + i % c;
+    } else {
+      L = w;
+    }
+  }
   bz = static_cast<int>(L / (X * Y));
   const int64_t rem = L % (X * Y);
   bx = rem / Y;
@@ -686,7 +704,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   const int r = lane & 31, kh = lane >> 5;
   int64_t bx = blockIdx.x;
   int by = blockIdx.y, bz = blockIdx.z;
-  if (xcd_order) xcd_block(bx, by, bz);
+  if (xcd_order) xcd_block(bx, by, bz, xcd_order);
   const int64_t row0 = bx * C::BM;
   const int n0 = by * C::BN;
   const int j0 = bz * jper;
@@ -1456,7 +1474,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
   SPIRA_HIP_REQUIRE(t.offset_splits >= 0 && t.offset_splits <= 128, "conv_os tuning: offset_splits must be 0..128");
   SPIRA_HIP_REQUIRE(t.offset_pack == 0 || t.offset_pack == 1 || t.offset_pack == 2 || t.offset_pack == 4,
                     "conv_os tuning: offset_pack must be 0, 1, 2 or 4");
-  SPIRA_HIP_REQUIRE(t.block_order == 0 || t.block_order == 1, "conv_os tuning: block_order must be 0 or 1");
+  SPIRA_HIP_REQUIRE(t.block_order >= 0 && t.block_order <= 4, "conv_os tuning: block_order must be 0..4");
   SPIRA_HIP_REQUIRE(t.row_walk == 0 || t.row_walk == 1, "conv_os tuning: row_walk must be 0 or 1");
   return kOk;
 }

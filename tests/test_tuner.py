@@ -97,7 +97,7 @@ def test_os_tuning_changes_the_launch():
 def test_os_candidates():
     from spira_amd.nn.conv import os_candidates
     cols, steps, splits, packs, orders, walks = os_candidates(256, 256, 27)
-    assert cols == [0, 32, 64, 96, 128] and steps == [0, 32, 64, 128] and packs == [0] and orders == [0, 1]
+    assert cols == [0, 32, 64, 96, 128] and steps == [0, 32, 64, 128] and packs == [0] and orders == [0, 1, 2, 3, 4]
     assert walks == [0]  # the row walk is for inputs of at most 16 channels
     cols, steps, splits, packs, orders, walks = os_candidates(16, 16, 125)
     assert cols == [0, 32] and steps == [0, 32] and packs == [0, 1, 2, 4] and walks == [0, 1]
