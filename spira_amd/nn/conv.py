@@ -403,9 +403,10 @@ OS_TUNING_MARGIN = 0.01
 
 def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Optional[int] = None,
                      with_time: bool = False):
-    """Coordinate search over the launch fields of ``os_candidates``: each
-    field in turn takes its fastest value with the others fixed, twice
-    over; a value the library rejects is skipped.  The row-order field is
+    """Search over the launch fields of ``os_candidates``, twice over: the
+    column tile and step channels as a pair over their whole grid, then each
+    field in turn takes its fastest value with the others fixed; a value the
+    library rejects is skipped.  The row-order field is
     held at `row_order` (default: the layer's current one, else -1, the
     library's rule).  Returns the tuning (and its time with `with_time`)."""
     if row_order is None:
@@ -425,7 +426,24 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Opti
             return float("inf")
 
     best_t = cost(best)
-    for _ in range(2):
+
+    def pair_grid():
+        # the column tile and the step channels jointly (their best pair is
+        # often not reached one field at a time: a narrower tile pays only
+        # with shorter steps, which need the deeper ring)
+        nonlocal best, best_t
+        for col in cands[0]:
+            for step in cands[1]:
+                if (col, step) == (best[0], best[1]):
+                    continue
+                trial = list(best)
+                trial[0], trial[1] = col, step
+                t = cost(trial)
+                if t < (1.0 - OS_TUNING_MARGIN) * best_t:
+                    best, best_t = trial, t
+
+    def each_field():
+        nonlocal best, best_t
         for i, values in enumerate(cands):
             for v in values:
                 if v == best[i]:
@@ -435,5 +453,12 @@ def choose_os_tuning(layer: "SparseConv", calls, reps: int = 10, row_order: Opti
                 t = cost(trial)
                 if t < (1.0 - OS_TUNING_MARGIN) * best_t:  # noise-sized gains do not move the search
                     best, best_t = trial, t
+
+    # pair grid, fields, pair grid again (with the block order and splits
+    # now chosen), fields
+    pair_grid()
+    each_field()
+    pair_grid()
+    each_field()
     tuning = full(best)
     return (tuning, best_t) if with_time else tuning

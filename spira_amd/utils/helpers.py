@@ -247,6 +247,29 @@ def _row_order_ms(omap: torch.Tensor, num_targets: int, reps: int = 5) -> float:
     return a.elapsed_time(b) / reps
 
 
+def _share_sibling_tunings(entries, picks, reps: int) -> None:
+    """Layers of the same shape on the same map (a res block's repeated
+    convolutions) are the same launch problem: each also tries the tunings
+    its siblings found, and keeps the fastest (the searches start from the
+    same point, but timing noise can send them to different optima)."""
+    from ..nn.conv import time_os_calls, OS_TUNING_MARGIN
+    for i, (m, call) in enumerate(entries):
+        for j, (m2, _) in enumerate(entries):
+            if j == i or (m2.in_channels, m2.out_channels, m2.kernel.shape) != (m.in_channels, m.out_channels,
+                                                                                 m.kernel.shape):
+                continue
+            if picks[j][0] == picks[i][0]:
+                continue
+            try:
+                t = time_os_calls(m, [call], picks[j][0], reps)
+            except RuntimeError:  # a launch this layer cannot take
+                from ..nn import functional as F
+                F.cuda_reset_error()
+                continue
+            if t < (1.0 - OS_TUNING_MARGIN) * picks[i][1]:
+                picks[i] = (picks[j][0], t)
+
+
 def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
                     verbose: bool = False) -> Dict[Tuple, int]:
     """Walk each output-stationary map (8..128 offsets; a transposed layer's
@@ -278,6 +301,7 @@ def tune_row_orders(model: Module, kernel_map_cache, sample, reps: int = 10,
             totals, picks = {}, {}
             for r in (0, 1):
                 picks[r] = [choose_os_tuning(m, [call], reps, row_order=r, with_time=True) for m, call in entries]
+                _share_sibling_tunings(entries, picks[r], reps)
                 totals[r] = sum(t for _, t in picks[r])
             omap, T = entries[0][1][2], entries[0][1][1]
             # with the order computed, each layer still walks whichever is
