@@ -726,6 +726,11 @@ __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restr
   __shared__ int32_t base[kTpMaxK + 1], tile_base[kTpMaxK];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kTpTile + tid;
+  // the thread's map row, loaded first so that it overlaps the counts' loads
+  // (loops over the compile-time maximum, so that src / rank stay in registers)
+  int32_t src[kTpMaxK];
+#pragma unroll
+  for (int k = 0; k < kTpMaxK; ++k) src[k] = (k < K && t < Tc) ? map[t * K + k] : -1;
   // this tile's position in each bucket: the counts of the tiles before it,
   // and the buckets' totals (every block sums the K * ntiles counts itself)
   {
@@ -782,12 +787,9 @@ __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restr
       masks[2 * g + 1] = 0;
     }
   }
-  // (loops over the compile-time maximum, so that src / rank stay in registers)
-  int32_t src[kTpMaxK];
   int rank[kTpMaxK];
 #pragma unroll
   for (int k = 0; k < kTpMaxK; ++k) {
-    src[k] = (k < K && t < Tc) ? map[t * K + k] : -1;
     const uint64_t m = ballot(src[k] >= 0);
     rank[k] = lane_prefix(m);
     if (lane == 0 && k < K) part[w][k] = __builtin_popcountll(m);
