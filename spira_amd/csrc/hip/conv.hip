@@ -40,7 +40,6 @@
 #include "../../../include/spira_hip.h"
 
 #include <algorithm>
-#include <cstdlib>
 #include <utility>
 #include <vector>
 
@@ -139,7 +138,7 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
 // where the larger blocks still fit the grid in one round, os_deep_ring).
 template <int WN, int NKS = 2, int DS = 0> struct TileOf {
   static constexpr int MT = 1;
-  static_assert(DS == 0 || NKS == 4, "the extra ring stage is for 64-channel steps");
+  static_assert(DS == 0 || NKS == 4 || (NKS == 8 && WN <= 2), "no room for an extra ring stage");
   static constexpr int NS = (NKS == 2 ? (WN >= 3 ? 3 : 4) : (NKS == 8 || WN >= 3 ? 2 : 3)) + DS;
   static constexpr int WAVES = WN <= 3 ? 4 : 3;
   using C = Cfg<WN, MT, NS, NKS>;
@@ -1396,9 +1395,12 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
 #define SPIRA_OS_CALL(W)                                                                                             \
   hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS>), grid, dim3(256), 0, s, map, order, rowmask, T,  \
                      Kc, jper, op, Y, epi, xcd)
-  if constexpr (DS == 1) {  // (96- and 128-column tiles only)
+  if constexpr (DS == 1 && NKS == 4) {  // (96- and 128-column tiles only)
     if (wn == 3) SPIRA_OS_CALL(3);
     else SPIRA_OS_CALL(4);
+  } else if constexpr (DS == 1) {  // (32- and 64-column tiles only)
+    if (wn == 1) SPIRA_OS_CALL(1);
+    else SPIRA_OS_CALL(2);
   } else {
     SPIRA_WN_SWITCH(wn, SPIRA_OS_CALL)
   }
@@ -1443,18 +1445,24 @@ static int os_wn(int64_t num_targets, int c_out, int cus, int col_tile) {
   return wn;
 }
 
-// A third ring stage for 64-channel steps of 96- and 128-column tiles (two
-// steps of gathers in flight instead of one) where the grid, at the larger
-// block's LDS, still runs in one round of resident blocks.  (Measured on the
+// A third ring stage (two steps of gathers in flight instead of one) for
+// 64-channel steps of 96- and 128-column tiles and for 128-channel steps of
+// 32- and 64-column tiles, where the grid, at the larger block's LDS, still
+// runs in one round of resident blocks.  (Also measured, kernel only: the
+// stride-16 256 -> 256 layer at 64-column tiles and 128-channel steps 34.4
+// -> 31.5 us, the stride-8 128 -> 128 layer 43.2 -> 38.7 us.)  (Measured on the
 // config-4 layers, untuned: the stride-8 256 -> 256 transposed layer 49.2 ->
 // 33.1 us, the stride-8 384 -> 256 1x1 layer 28.3 -> 22.1 us; the 529-block
 // stride-4 128 -> 128 layers, two blocks per CU at 62 KiB, went 82.9 ->
 // 96.2 us with the tail round, so they keep two stages.)
 static bool os_deep_ring(int wn, int nks, int64_t blocks, int cus) {
-  if (nks != 4 || wn < 3) return false;
+  const bool wide = nks == 4 && wn >= 3, narrow = nks == 8 && wn <= 2;
+  if (!wide && !narrow) return false;
   constexpr int kLdsPerCu = 160 * 1024;
-  const int lds = wn == 3 ? ring::TileOf<3, 4, 1>::C::LDS : ring::TileOf<4, 4, 1>::C::LDS;
-  const int waves = wn == 3 ? ring::TileOf<3, 4, 1>::WAVES : ring::TileOf<4, 4, 1>::WAVES;
+  const int lds = wide ? (wn == 3 ? ring::TileOf<3, 4, 1>::C::LDS : ring::TileOf<4, 4, 1>::C::LDS)
+                       : (wn == 1 ? ring::TileOf<1, 8, 1>::C::LDS : ring::TileOf<2, 8, 1>::C::LDS);
+  const int waves = wide ? (wn == 3 ? ring::TileOf<3, 4, 1>::WAVES : ring::TileOf<4, 4, 1>::WAVES)
+                         : ring::TileOf<2, 8, 1>::WAVES;
   const int per_cu = std::min(kLdsPerCu / lds, waves);
   return blocks <= static_cast<int64_t>(per_cu) * cus;
 }
@@ -1549,13 +1557,17 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
   else if (cat) {
     // channel concatenations: storage-dtype outputs (split or not)
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
-      if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      if (nks == 8 && pl.deep)
+        launch_os<MODE, true, 8, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 4 && pl.deep)
         launch_os<MODE, true, 4, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
     }
-  } else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  } else if (nks == 8 && pl.deep)
+    launch_os<MODE, true, 8, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 4 && pl.deep)
     launch_os<MODE, true, 4, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
