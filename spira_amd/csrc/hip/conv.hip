@@ -476,6 +476,127 @@ __device__ __forceinline__ void run(floatx4 (&acc)[2][C::BN / 16], int nsteps, F
   wait_vm<0>();
 }
 
+// The A loads (gathered rows, slice KS) of a step, as issue_slice issues
+// them (OP = 1).
+template <class C, bool ALIGNED, bool CAT, int KS>
+__device__ __forceinline__ void issue_a(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
+                                        __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t xr2,
+                                        half8 (&a)[1][C::NKS]) {
+  constexpr int rt = KS & 1;
+  const int k0 = st.kb + (KS >> 1) * 32;
+  const int32_t ix = st.idx[rt];
+  const bool rv = st.live & (ix >= 0);
+  if constexpr (!ALIGNED) {
+    const int k = k0 + cx.kh8;
+    const uint32_t off = (rv & (k < op.Cin)) ? (static_cast<uint32_t>(ix) * op.Cin + k) * 2u : kOutOfRange;
+    half8 v;
+    v[0] = __builtin_bit_cast(_Float16, static_cast<unsigned short>(
+                                            __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0)));
+#pragma unroll
+    for (int e = 1; e < 8; ++e)
+      v[e] = (rv && k + e < op.Cin) ? op.X[static_cast<int64_t>(ix) * op.Cin + k + e] : static_cast<_Float16>(0.f);
+    a[0][KS] = v;
+  } else {
+    const bool ok = rv & (cx.kh8 < op.Cin - k0);
+    if constexpr (CAT) {
+      const bool second = k0 >= op.C1;
+      const uint32_t at = second ? static_cast<uint32_t>(ix) * static_cast<uint32_t>((op.Cin - op.C1) * 2) +
+                                       static_cast<uint32_t>((k0 - op.C1) * 2)
+                                 : static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.C1 * 2) +
+                                       static_cast<uint32_t>(k0 * 2);
+      a[0][KS] = __builtin_bit_cast(
+          half8, __builtin_amdgcn_raw_buffer_load_b128(second ? xr2 : xr, ok ? at + cx.kh16 : kOutOfRange, 0, 0));
+    } else {
+      const uint32_t rb1 = static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.C1 * 2);
+      a[0][KS] = __builtin_bit_cast(
+          half8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? rb1 + static_cast<uint32_t>(k0 * 2) + cx.kh16
+                                                              : kOutOfRange,
+                                                       0, 0));
+    }
+  }
+}
+
+// Every weight DMA of a step into ring stage S (OP = 1).
+template <class C, int S>
+__device__ __forceinline__ void issue_b(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
+                                        __amdgpu_buffer_rsrc_t wr) {
+  const uint32_t wstep = static_cast<uint32_t>((st.wrow * op.CoutP * op.CinP + st.kb) * 2);
+  const int wlim = st.live ? op.CinP - st.kb : 0;
+#pragma unroll
+  for (int i = 0; i < C::BVEC; ++i) {
+    const uint32_t off = cx.c8[i] < wlim ? cx.wlane[i] + wstep : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void_t *)(cx.ldsw + S * C::STAGE + i * 4096), 16, off, 0, 0, 0);
+  }
+}
+
+// The step loop with the gathered rows two steps ahead (a ring of three
+// register stages) and the weights one step ahead (the two-stage LDS ring),
+// for maps held in LDS (no index fetches) and one offset per step.  Per
+// step v: wait for the loads of step v (the only younger loads are step
+// v + 1's gathers, issued after step v's weights), barrier, then the
+// weights of step v + 1 and the gathers of step v + 2 are issued between
+// the MFMAs of step v.  The weights' LDS stage (v + 1) % 2 was last read by
+// step v - 1, which every wave finished before the barrier.  resolve() runs
+// for steps 0, 1, 2, ... in order (two steps ahead); a step's weight row and
+// channel offset are kept one step for its weights.  The loop's unrolled
+// period is 6 (stage v % 2, register slot v % 3); steps past nsteps are
+// skipped (block-uniform).
+template <class C, bool ALIGNED, bool CAT, class Resolve>
+__device__ __forceinline__ void run_da(floatx4 (&acc)[2][C::BN / 16], int nsteps, Resolve resolve,
+                                       const Operands &op, int n0, char *ring) {
+  static_assert(C::NS == 2 && C::BM == 128, "two LDS stages, one row tile per wave");
+  constexpr int LA = C::NKS;  // gathered-row loads per wave and step
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
+  const __amdgpu_buffer_rsrc_t xr2 = make_rsrc(op.X2 ? op.X2 : op.X, op.X2 ? op.x2bytes : 0u);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
+  const ReadBase<C::NKS> rb = read_base<C>(ring);
+  const IssueCtx<C> cx = issue_ctx<C, 1>(ring, wave, n0, op);
+  half8 areg[3][1][C::NKS];
+  auto prepare = [&](int u) {
+    StepIn st;
+    st.wrow = 0;
+    st.kb = 0;
+    st.live = u < nsteps;
+    st.idx[0] = st.idx[1] = -1;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      st.livep[q] = false;
+      st.wrowp[q] = 0;
+      st.idxp[q][0] = st.idxp[q][1] = -1;
+    }
+    if (st.live) resolve(u, std::integral_constant<int, 0>{}, st);
+    return st;
+  };
+  // prologue: A(0), B(0), A(1)
+  StepIn st0 = prepare(0);
+  unroll<C::NKS>([&](auto KS) { issue_a<C, ALIGNED, CAT, decltype(KS)::value>(cx, st0, op, xr, xr2, areg[0]); });
+  issue_b<C, 0>(cx, st0, op, wr);
+  StepIn nb = prepare(1);  // step v + 1: its weights are issued in step v
+  // (the map-tile read that resolve(2) takes was issued by resolve(1), with
+  // no compute, and so no LDS wait, in between)
+  lds_wait();
+  unroll<C::NKS>([&](auto KS) { issue_a<C, ALIGNED, CAT, decltype(KS)::value>(cx, nb, op, xr, xr2, areg[1]); });
+  for (int s = 0; s < nsteps; s += 6) {
+    unroll<6>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (s + i < nsteps) {
+        wait_vm<LA>();
+        __builtin_amdgcn_s_barrier();
+        const StepIn na = prepare(s + i + 2);
+        compute<C, i % 2>(acc, rb, areg[i % 3], [&](auto KQ) {
+          constexpr int kq = decltype(KQ)::value;
+          if constexpr (kq == 0) issue_b<C, (i + 1) % 2>(cx, nb, op, wr);
+          issue_a<C, ALIGNED, CAT, 2 * kq>(cx, na, op, xr, xr2, areg[(i + 2) % 3]);
+          issue_a<C, ALIGNED, CAT, 2 * kq + 1>(cx, na, op, xr, xr2, areg[(i + 2) % 3]);
+        });
+        nb = na;
+      }
+    });
+  }
+  wait_vm<0>();
+}
+
 // Scalar iterator over the set bits of a 128-bit offset set, nch channel
 // chunks per offset: step() moves to the next (offset, chunk).
 struct StepIter {
@@ -682,7 +803,7 @@ __device__ __forceinline__ void xcd_block(int64_t &bx, int &by, int &bz, int ord
 // logical row i is target order[i] and `map` holds the rows in logical order;
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
-template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP, int DS = 0>
+template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP, int DS = 0, int DA = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS, DS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
@@ -872,7 +993,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     pit.step(nch);
     if (tiled) read_tile();
   };
-  ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  if constexpr (DA == 1) {
+    // gathered rows two steps ahead (maps held in LDS only)
+    if (tiled) ring::run_da<C, ALIGNED, CAT>(acc, nsteps, resolve, op, n0, ring_lds);
+    else ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  } else {
+    ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+  }
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -1388,12 +1515,12 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
     default: CALL(4); break;      \
   }
 
-template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1, int DS = 0>
+template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1, int DS = 0, int DA = 0>
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                       void *Y, const Epilogue &epi, int xcd = 0) {
 #define SPIRA_OS_CALL(W)                                                                                             \
-  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS>), grid, dim3(256), 0, s, map, order, rowmask, T,  \
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS, DA>), grid, dim3(256), 0, s, map, order, rowmask, T, \
                      Kc, jper, op, Y, epi, xcd)
   if constexpr (DS == 1 && NKS == 4) {  // (96- and 128-column tiles only)
     if (wn == 3) SPIRA_OS_CALL(3);
@@ -1491,7 +1618,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
 // block, offsets per split (jper), 16-channel slices per step (nks), kernel
 // offsets per step (pack: 1, 2 or 4) and the grid.
 struct OsPlan {
-  int wn, bm, jper, splits, nks, pack, xcd, deep;
+  int wn, bm, jper, splits, nks, pack, xcd, deep, da;
   bool aligned;
   int64_t gx, gy;
 };
@@ -1531,6 +1658,15 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
     pl.nks = 8;
   }
   pl.deep = pl.pack == 1 && os_deep_ring(pl.wn, pl.nks, pl.gx * pl.gy * pl.splits, cus) ? 1 : 0;
+  // Gathered rows two steps ahead in registers (run_da): 128-channel steps
+  // of 96- and 128-column tiles (two LDS stages), maps held in LDS.
+  // (Measured, kernel only, config-4 maps: s4 128 -> 128 56.5 -> 50.9 us,
+  // s8 256 -> 256 row-ordered 90.6 -> 78.3 us, s8 384 -> 256 138.7 ->
+  // 123.6 us, s2 96 -> 96 57.4 -> 53.2 us; 64-column tiles, at 158 VGPRs,
+  // went 58.8 -> 65.2 us, so they keep the plain ring.)
+  pl.da = (pl.pack == 1 && !pl.deep && pl.aligned && pl.nks == 8 && pl.wn >= 3 && has_map && Kc <= ring::kMapTileK)
+              ? 1
+              : 0;
   return pl;
 }
 
@@ -1559,6 +1695,8 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
       if (nks == 8 && pl.deep)
         launch_os<MODE, true, 8, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 8 && pl.da)
+        launch_os<MODE, true, 8, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 4 && pl.deep)
         launch_os<MODE, true, 4, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
@@ -1567,6 +1705,8 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
     }
   } else if (nks == 8 && pl.deep)
     launch_os<MODE, true, 8, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else if (nks == 8 && pl.da)
+    launch_os<MODE, true, 8, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 4 && pl.deep)
     launch_os<MODE, true, 4, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
