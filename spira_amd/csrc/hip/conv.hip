@@ -1522,7 +1522,7 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
 #define SPIRA_OS_CALL(W)                                                                                             \
   hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS, DA>), grid, dim3(256), 0, s, map, order, rowmask, T, \
                      Kc, jper, op, Y, epi, xcd)
-  if constexpr (DS == 1 && NKS == 4) {  // (96- and 128-column tiles only)
+  if constexpr ((DS == 1 && NKS == 4) || DA == 1) {  // (96- and 128-column tiles only)
     if (wn == 3) SPIRA_OS_CALL(3);
     else SPIRA_OS_CALL(4);
   } else if constexpr (DS == 1) {  // (32- and 64-column tiles only)
@@ -1658,13 +1658,16 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
     pl.nks = 8;
   }
   pl.deep = pl.pack == 1 && os_deep_ring(pl.wn, pl.nks, pl.gx * pl.gy * pl.splits, cus) ? 1 : 0;
-  // Gathered rows two steps ahead in registers (run_da): 128-channel steps
-  // of 96- and 128-column tiles (two LDS stages), maps held in LDS.
+  // Gathered rows two steps ahead in registers (run_da): 64- and
+  // 128-channel steps of 96- and 128-column tiles with two LDS stages, maps
+  // held in LDS.  (64-channel steps: s1 96 -> 96 52.0 -> 45.2 us, s4 192 ->
+  // 128 99.3 -> 87.3 us.)
   // (Measured, kernel only, config-4 maps: s4 128 -> 128 56.5 -> 50.9 us,
   // s8 256 -> 256 row-ordered 90.6 -> 78.3 us, s8 384 -> 256 138.7 ->
   // 123.6 us, s2 96 -> 96 57.4 -> 53.2 us; 64-column tiles, at 158 VGPRs,
   // went 58.8 -> 65.2 us, so they keep the plain ring.)
-  pl.da = (pl.pack == 1 && !pl.deep && pl.aligned && pl.nks == 8 && pl.wn >= 3 && has_map && Kc <= ring::kMapTileK)
+  pl.da = (pl.pack == 1 && !pl.deep && pl.aligned && (pl.nks == 8 || pl.nks == 4) && pl.wn >= 3 && has_map &&
+           Kc <= ring::kMapTileK)
               ? 1
               : 0;
   return pl;
@@ -1700,6 +1703,8 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
       else if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 4 && pl.deep)
         launch_os<MODE, true, 4, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 4 && pl.da)
+        launch_os<MODE, true, 4, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
     }
@@ -1710,6 +1715,8 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
   else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 4 && pl.deep)
     launch_os<MODE, true, 4, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else if (nks == 4 && pl.da)
+    launch_os<MODE, true, 4, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
 }
