@@ -288,3 +288,38 @@ def test_row_walk(dev, indoor, scene_k5, ks, cin, cout):
                                          epilogue=(scale.to(dev), shift.to(dev), res.to(dev), True))
     ref = np.maximum(conv * scale.double().numpy() + shift.double().numpy() + res.double().numpy(), 0)
     assert rel_err(np_(ye.float()), ref) <= 1e-2
+
+
+# Launches that issue the gathered rows two steps ahead of the weights (64-
+# and 128-channel steps of 96- and 128-column tiles whose grid is too large
+# for a third LDS stage: 200k rows): index and row order, block orders, a
+# channel concatenation, and an output width that leaves a partial column
+# tile.  (tuning: col_tile, step_channels, offset_splits, offset_pack,
+# block_order, row_order)
+@pytest.mark.parametrize("cin,cout,tuning", [
+    (128, 128, (128, 128, 0, 0, 0, 1)),
+    (128, 128, (128, 64, 0, 0, 4, 0)),
+    (96, 96, (96, 128, 0, 0, 1, 1)),
+    (96, 96, (96, 64, 0, 0, 2, 1)),
+    (128, 160, (96, 128, 0, 0, 0, 0)),
+])
+def test_two_step_gathers(dev, indoor, cin, cout, tuning):
+    k, m = indoor
+    S = T = len(k)
+    X, W = _case(S, cin, cout, dev, seed=cin * 7 + cout)
+    md = torch.from_numpy(m).to(dev)
+    y = np_(F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=tuning).float())
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(y, ref) <= 1e-2
+
+
+def test_two_step_gathers_concat(dev, indoor):
+    k, m = indoor
+    S = T = len(k)
+    X, W = _case(S, 192, 128, dev, seed=11)
+    md = torch.from_numpy(m).to(dev)
+    Xd = X.to(dev)
+    y = np_(F.sparse_convolution_forward_os(S, T, md, Xd[:, :128].contiguous(), W.to(dev),
+                                            sources2=Xd[:, 128:].contiguous(), tuning=(128, 128, 0, 0, 0, 1)).float())
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(y, ref) <= 1e-2
