@@ -134,12 +134,14 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
 // kernels are latency-bound: more resident waves beat larger wave tiles),
 // the ring depth, and the waves per SIMD the register budget targets: 4 for
 // up to 96 columns (<= 128 VGPRs, four 40 KiB blocks per CU), 3 for 128.
+// (32-column tiles of 32-channel steps take 3 stages, not 4: measured on the
+// config-4 32 -> 32 layers, s1 18.0 -> 17.4 us, s2 20.2 -> 18.9 us.)
 // DS = 1: one more ring stage for 64-channel steps of wide tiles (chosen
 // where the larger blocks still fit the grid in one round, os_deep_ring).
 template <int WN, int NKS = 2, int DS = 0> struct TileOf {
   static constexpr int MT = 1;
   static_assert(DS == 0 || NKS == 4 || (NKS == 8 && WN <= 2), "no room for an extra ring stage");
-  static constexpr int NS = (NKS == 2 ? (WN >= 3 ? 3 : 4) : (NKS == 8 || WN >= 3 ? 2 : 3)) + DS;
+  static constexpr int NS = (NKS == 2 ? (WN == 2 ? 4 : 3) : (NKS == 8 || WN >= 3 ? 2 : 3)) + DS;
   static constexpr int WAVES = WN <= 3 ? 4 : 3;
   using C = Cfg<WN, MT, NS, NKS>;
 };
