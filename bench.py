@@ -53,23 +53,23 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 # commands, tunings and raw figures are in profiles/os_kernel_traffic.md; a
 # default run re-tunes and can choose other launches, whose traffic differs.
 MEASURED_TRAFFIC = {
-    "s1 3->32 K27": 58955866,  # FETCH 22432.5 KiB, WRITE 12709.2 KiB
-    "s1 32->32 K27": 82384608,  # FETCH 33868.9 KiB, WRITE 12715.9 KiB
-    "s1 96->96 K27": 177937101,  # FETCH 68093.0 KiB, WRITE 37580.7 KiB
-    "s1 128->96 K27": 188672141,  # FETCH 73335.4 KiB, WRITE 37579.3 KiB
-    "s2 32->32 K27": 93101069,  # FETCH 40618.7 KiB, WRITE 9681.6 KiB
-    "s2 96->96 K27": 238373446,  # FETCH 101965.5 KiB, WRITE 28855.5 KiB
-    "s2 128->96 K27": 253492176,  # FETCH 109375.4 KiB, WRITE 28800.1 KiB
-    "s4 32->64 K27": 28899328,  # FETCH 9880.6 KiB, WRITE 8460.9 KiB
-    "s4 64->64 K27": 40941530,  # FETCH 15760.5 KiB, WRITE 8460.9 KiB
-    "s4 128->128 K27": 104293747,  # FETCH 42463.8 KiB, WRITE 16921.8 KiB
-    "s4 192->128 K27": 167001728,  # FETCH 73082.9 KiB, WRITE 16921.8 KiB
-    "s8 64->128 K27": 21468160,  # FETCH 8352.0 KiB, WRITE 4261.0 KiB
-    "s8 128->128 K27": 18822016,  # FETCH 7059.9 KiB, WRITE 4261.0 KiB
-    "s8 256->256 K27": 49884784,  # FETCH 20084.4 KiB, WRITE 8546.9 KiB
-    "s8 384->256 K27": 73468358,  # FETCH 31588.8 KiB, WRITE 8568.9 KiB
-    "s16 128->256 K27": 28908800,  # FETCH 7122.6 KiB, WRITE 13986.0 KiB
-    "s16 256->256 K27": 42386432,  # FETCH 9707.5 KiB, WRITE 21978.0 KiB
+    "s1 3->32 K27": 59147816,  # FETCH 22529.4 KiB, WRITE 12707.2 KiB
+    "s1 32->32 K27": 82594203,  # FETCH 33973.9 KiB, WRITE 12717.2 KiB
+    "s1 96->96 K27": 177703176,  # FETCH 67987.5 KiB, WRITE 37576.5 KiB
+    "s1 128->96 K27": 188732655,  # FETCH 73375.5 KiB, WRITE 37572.4 KiB
+    "s2 32->32 K27": 93550079,  # FETCH 40831.6 KiB, WRITE 9702.2 KiB
+    "s2 96->96 K27": 230775517,  # FETCH 98282.5 KiB, WRITE 28820.8 KiB
+    "s2 128->96 K27": 252398889,  # FETCH 108841.0 KiB, WRITE 28822.3 KiB
+    "s4 32->64 K27": 40333856,  # FETCH 15465.3 KiB, WRITE 8460.9 KiB
+    "s4 64->64 K27": 56965110,  # FETCH 23586.8 KiB, WRITE 8460.9 KiB
+    "s4 128->128 K27": 133386743,  # FETCH 56674.9 KiB, WRITE 16921.8 KiB
+    "s4 192->128 K27": 175078752,  # FETCH 77034.3 KiB, WRITE 16921.8 KiB
+    "s8 64->128 K27": 13367064,  # FETCH 4396.8 KiB, WRITE 4261.0 KiB
+    "s8 128->128 K27": 20248062,  # FETCH 7757.0 KiB, WRITE 4261.0 KiB
+    "s8 256->256 K27": 50210735,  # FETCH 20234.5 KiB, WRITE 8568.8 KiB
+    "s8 384->256 K27": 98760791,  # FETCH 43955.8 KiB, WRITE 8542.9 KiB
+    "s16 128->256 K27": 19567968,  # FETCH 8556.5 KiB, WRITE 1998.0 KiB
+    "s16 256->256 K27": 61090076,  # FETCH 18842.0 KiB, WRITE 21978.0 KiB
 }
 # the same for the config-2 k=3 stride-1 map search (`--only kmap,calib`)
 KMAP_TRAFFIC = 16050790  # FETCH 2558.8 KiB, WRITE 10557.0 KiB
