@@ -306,7 +306,10 @@ __device__ __forceinline__ void search_tile(const P &p, const int64_t tile) {
     const int total = 64 * p.K;  // multiple of 4
     const int4 *s4 = reinterpret_cast<const int4 *>(stage);
     int4 *d4 = reinterpret_cast<int4 *>(dst);
-    for (int i = threadIdx.x; i < total / 4; i += blockDim.x) d4[i] = s4[i];
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i *sv = reinterpret_cast<const v4i *>(s4);
+    v4i *dv = reinterpret_cast<v4i *>(d4);
+    for (int i = threadIdx.x; i < total / 4; i += blockDim.x) __builtin_nontemporal_store(sv[i], dv + i);
   }
 }
 
