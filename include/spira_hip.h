@@ -71,6 +71,14 @@ int spira_hip_radix_sort_workspace(int64_t n, int key_bits, size_t *bytes);
 int spira_hip_radix_sort_pairs(const void *keys_in, const int32_t *vals_in, void *keys_out, int32_t *vals_out,
                                int64_t n, int key_bits, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Status of the last spira_hip_radix_sort_pairs that used `workspace` (same
+ * n and key_bits): waits for `stream` and returns an error if a tile's
+ * look-back wait ran out of its spin bound, in which case that sort's output
+ * is incomplete.  Tiles take tickets in dispatch order and wait only on
+ * earlier tickets, so this is not expected to happen.  (No reference
+ * counterpart: CUB's sort has no bounded waits.) */
+int spira_hip_radix_sort_status(const void *workspace, int64_t n, int key_bits, hipStream_t stream);
+
 /* Workspace bytes for spira_hip_downsample, _plan and _execute. */
 int spira_hip_downsample_workspace(int64_t n, int key_bits, size_t *bytes);
 
@@ -221,7 +229,10 @@ int spira_hip_convert_transposed_os_partition_order_workspace(int64_t num_coarse
  * group_masks [ceil(num_sources / 128) * 2].  The inverse has one valid entry
  * per row, so that order is the rows grouped by column in source order.
  * out_in_map holds num_coarse rows; K <= 8 and K * ceil(num_coarse / 256) <=
- * 16384.  (No counterpart in the reference: the row order is this
+ * 16384.  If the valid entries are fewer than num_sources (some source lies
+ * in no entry), out is still the exact inverse (such rows all -1), order is
+ * the identity, ordered_map equals out and every group mask holds all K
+ * columns.  (No counterpart in the reference: the row order is this
  * library's own.) */
 int spira_hip_convert_transposed_os_partition_order(const int32_t *out_in_map, int64_t num_coarse, int num_offsets,
                                                     int64_t num_sources, int64_t aligned_sources, int32_t *out,

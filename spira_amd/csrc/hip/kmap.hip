@@ -697,7 +697,8 @@ __device__ __forceinline__ void tp_row(int32_t *row, int K, int k, int32_t t) {
 
 __global__ __launch_bounds__(kTpTile) void tp_count_kernel(const int32_t *__restrict__ map, int64_t Tc, int K,
                                                            int ntiles, int32_t *__restrict__ cnt, int64_t S,
-                                                           int64_t Sp, int32_t *__restrict__ inverse) {
+                                                           int64_t Sp, int32_t *__restrict__ inverse,
+                                                           int32_t *__restrict__ ordered_map) {
   __shared__ int32_t part[kTpTile / 64][kTpMaxK];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kTpTile + tid;
@@ -712,10 +713,12 @@ __global__ __launch_bounds__(kTpTile) void tp_count_kernel(const int32_t *__rest
     for (int q = 0; q < kTpTile / 64; ++q) c += part[q][tid];
     cnt[tid * ntiles + blockIdx.x] = c;
   }
-  const int64_t pad = (Sp - S) * K;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kTpTile + tid; i < pad;
-       i += static_cast<int64_t>(gridDim.x) * kTpTile)
-    inverse[S * K + i] = -1;
+  // every inverse and ordered-map word starts at -1: the emit pass rewrites
+  // the row of each source it finds, so a source that lies in no entry (a map
+  // whose entries do not partition its sources) keeps an all -1 row
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kTpTile;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kTpTile + tid; i < Sp * K; i += step) inverse[i] = -1;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kTpTile + tid; i < S * K; i += step) ordered_map[i] = -1;
 }
 
 __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restrict__ map, int64_t Tc, int K,
@@ -776,6 +779,28 @@ __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restr
     }
     __syncthreads();
   }
+  // Entries that do not partition the sources (fewer valid entries than
+  // sources: some source lies in no entry): the order is the identity, the
+  // ordered map is the inverse, every group's union holds all K columns, and
+  // each entry writes only its own word (rows start at -1, count pass).
+  if (base[K] != S) {
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kTpTile;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kTpTile + tid; i < S; i += step)
+      order[i] = static_cast<int32_t>(i);
+    if (blockIdx.x == 0)
+      for (int64_t g = tid; g < (S + 127) / 128; g += kTpTile) {
+        masks[2 * g] = K >= 64 ? ~uint64_t(0) : (uint64_t(1) << K) - 1;
+        masks[2 * g + 1] = 0;
+      }
+#pragma unroll
+    for (int k = 0; k < kTpMaxK; ++k) {
+      const int32_t s = src[k];
+      if (s < 0 || s >= S) continue;
+      inverse[static_cast<int64_t>(s) * K + k] = static_cast<int32_t>(t);
+      ordered_map[static_cast<int64_t>(s) * K + k] = static_cast<int32_t>(t);
+    }
+    return;
+  }
   // block 0: the column union of every 128-row group of the ordered rows
   // (from the k bucket bounds)
   if (blockIdx.x == 0) {
@@ -804,7 +829,7 @@ __global__ __launch_bounds__(kTpTile) void tp_emit_kernel(const int32_t *__restr
     if (s < 0 || s >= S) continue;
     int pos = tile_base[k] + rank[k];
     for (int q = 0; q < w; ++q) pos += part[q][k];
-    if (pos >= S) continue;  // (only if the entries do not partition the sources)
+    if (pos >= S) continue;  // (a source in two entries; then the counts do not sum to S)
     order[pos] = s;
     tp_row(ordered_map + static_cast<int64_t>(pos) * K, K, k, static_cast<int32_t>(t));
     tp_row(inverse + static_cast<int64_t>(s) * K, K, k, static_cast<int32_t>(t));
@@ -1344,7 +1369,7 @@ int spira_hip_convert_transposed_os_partition_order(const int32_t *out_in_map, i
   if (num_sources == 0 && aligned_sources == 0) return kOk;
   int32_t *cnt = static_cast<int32_t *>(workspace);
   hipLaunchKernelGGL(tp_count_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTpTile), 0, stream, out_in_map,
-                     num_coarse, K, static_cast<int>(ntiles), cnt, num_sources, aligned_sources, out);
+                     num_coarse, K, static_cast<int>(ntiles), cnt, num_sources, aligned_sources, out, ordered_map);
   SPIRA_HIP_LAUNCH_CHECK();
   hipLaunchKernelGGL(tp_emit_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTpTile), 0, stream, out_in_map,
                      num_coarse, K, static_cast<int>(ntiles), cnt, num_sources, order, ordered_map, out, group_masks);

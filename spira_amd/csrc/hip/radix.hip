@@ -44,9 +44,6 @@ constexpr uint32_t kFlagAgg = 1u << 30;         // look-back word: tile count on
 constexpr uint32_t kFlagPrefix = 2u << 30;      // look-back word: inclusive prefix
 constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr int kSpinLimit = 1 << 22;
-// grids of at most this many tiles are resident at once on MI355X (256 CUs,
-// 8 blocks of 256 threads each, far below the LDS and register limits)
-constexpr int kResidentTiles = 1024;
 
 // device-side control block of one sort
 struct Ctrl {
@@ -179,13 +176,11 @@ __global__ __launch_bounds__(kThreads) void rs_pass_kernel(int pass, int64_t n, 
   __shared__ int s_tile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Tiles in ticket order, so that every tile a look-back waits on has
-  // started.  Grids that fit the chip at once (every block resident: up to
-  // kResidentTiles) take their block index instead and save the ticket's
-  // round trip.
-  if (ntiles > kResidentTiles && tid == 0) s_tile = static_cast<int>(atomicAdd(&ctrl->ticket[pass], 1u));
+  // started, whatever order the hardware dispatches the blocks in.
+  if (tid == 0) s_tile = static_cast<int>(atomicAdd(&ctrl->ticket[pass], 1u));
   for (int i = tid; i < kWaves * kBins; i += kThreads) (&wcnt[0][0])[i] = 0;
   __syncthreads();
-  const int tile = ntiles > kResidentTiles ? s_tile : static_cast<int>(blockIdx.x);
+  const int tile = s_tile;
   const CT *__restrict__ kin = src == 0 ? b.k0 : (src == 1 ? b.k1 : b.k2);
   const int32_t *__restrict__ vin = src == 0 ? b.v0 : (src == 1 ? b.v1 : b.v2);
   CT *__restrict__ kout = dst == 1 ? b.k1 : b.k2;
@@ -356,6 +351,22 @@ extern "C" {
 int spira_hip_radix_sort_workspace(int64_t n, int key_bits, size_t *bytes) {
   SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "radix_sort: key_bits must be 32 or 64");
   *bytes = n <= 0 ? 0 : (key_bits == 64 ? radix_sort_bytes<uint64_t>(n) : radix_sort_bytes<uint32_t>(n));
+  return kOk;
+}
+
+int spira_hip_radix_sort_status(const void *workspace, int64_t n, int key_bits, hipStream_t stream) {
+  SPIRA_HIP_REQUIRE(key_bits == 32 || key_bits == 64, "radix_sort: key_bits must be 32 or 64");
+  if (n <= 0) return kOk;
+  SPIRA_HIP_REQUIRE(workspace != nullptr, "radix_sort_status: null workspace");
+  const size_t bytes = key_bits == 64 ? radix_sort_bytes<uint64_t>(n) : radix_sort_bytes<uint32_t>(n);
+  const auto *ctrl = reinterpret_cast<const radix::Ctrl *>(static_cast<const char *>(workspace) + bytes -
+                                                           rs_align(sizeof(radix::Ctrl)));
+  uint32_t stalled = 0;
+  SPIRA_HIP_REQUIRE(hipMemcpyAsync(&stalled, &ctrl->stalled, sizeof(stalled), hipMemcpyDeviceToHost, stream) ==
+                            hipSuccess &&
+                        hipStreamSynchronize(stream) == hipSuccess,
+                    "radix_sort_status: read failed");
+  SPIRA_HIP_REQUIRE(stalled == 0, "radix_sort: a look-back wait ran out; the output is incomplete");
   return kOk;
 }
 

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <tuple>
 #include <unordered_map>
 
 namespace spira_host {
@@ -18,6 +19,19 @@ static int dtype_of(const torch::Tensor &t) {
   if (t.scalar_type() == torch::kHalf) return SPIRA_F16;
   if (t.scalar_type() == torch::kFloat) return SPIRA_F32;
   fail("Cannot find implementation for feature dtype ", t.scalar_type());
+}
+
+// Cached device tensors are allocated from the caching allocator's pool of
+// the stream that made them, and go back to that pool when their entry is
+// dropped.  A kernel that reads them on another stream must be recorded on
+// them, or a later allocation on the making stream could reuse the memory
+// while that kernel still reads it (an order overwritten under a running
+// convolution indexes its output rows out of bounds).
+static void record_use(hipStream_t made_on, std::initializer_list<const torch::Tensor *> ts) {
+  const auto cur = c10::hip::getCurrentHIPStream();
+  if (cur.stream() == made_on) return;
+  for (const torch::Tensor *t : ts)
+    if (t->defined()) const_cast<torch::Tensor *>(t)->record_stream(cur);
 }
 
 // Prepared (MFMA-ready) weights, cached per weight tensor.  An entry is valid
@@ -31,6 +45,7 @@ struct PreparedEntry {
   const void *data = nullptr;
   uint32_t version = 0;
   torch::Tensor prepared;
+  hipStream_t stream = nullptr;  // the stream that allocated and wrote `prepared`
 };
 
 static std::unordered_map<const c10::TensorImpl *, PreparedEntry> &prepared_cache() {
@@ -50,17 +65,19 @@ static torch::Tensor prepared_weights(const torch::Tensor &W) {
   if (it != cache.end()) {
     auto &e = it->second;
     if (!e.impl.expired() && e.data == W.data_ptr() && e.version == W._version() &&
-        e.prepared.device() == W.device())
+        e.prepared.device() == W.device()) {
+      record_use(e.stream, {&e.prepared});
       return e.prepared;
+    }
     cache.erase(it);
   }
-  if (cache.size() > 4096) {  // drop entries of freed tensors
-    for (auto i = cache.begin(); i != cache.end();) i = i->second.impl.expired() ? cache.erase(i) : std::next(i);
-  }
+  // drop the entries of freed weight tensors (one entry per live layer)
+  for (auto i = cache.begin(); i != cache.end();) i = i->second.impl.expired() ? cache.erase(i) : std::next(i);
   PreparedEntry e(W);
   e.data = W.data_ptr();
   e.version = W._version();
   e.prepared = workspace(bytes, W.device());
+  e.stream = current_stream();
   check_rc(spira_hip_prepare_weights(W.data_ptr(), W.size(0), W.size(1), W.size(2), dtype, e.prepared.data_ptr(),
                                      current_stream()),
            "prepare_weights");
@@ -89,11 +106,22 @@ struct OrderEntry {
   int64_t T = 0;
   bool free = false;  // made with the map at no sorting cost (convert_transposed_os_ordered)
   torch::Tensor order, masks, ordered_map;
+  hipStream_t stream = nullptr;  // the stream the tensors were allocated and written on
 };
+
 
 static std::unordered_map<const c10::TensorImpl *, OrderEntry> &order_cache() {
   static std::unordered_map<const c10::TensorImpl *, OrderEntry> cache;
   return cache;
+}
+
+// Drops the entries whose map tensor has been freed, so that their device
+// tensors (order, ordered map, masks: ~7 MB for a 200k-row k = 2 inverse) go
+// back to the allocator with the map instead of piling up across steps.  Run
+// on every insert: the cache holds one entry per live map, a few dozen.
+static void purge_expired_orders() {
+  auto &cache = order_cache();
+  for (auto i = cache.begin(); i != cache.end();) i = i->second.impl.expired() ? cache.erase(i) : std::next(i);
 }
 
 static bool &row_order_flag() {
@@ -128,13 +156,12 @@ static const OrderEntry &row_order_of(const torch::Tensor &map, int64_t T) {
     if (!e.impl.expired() && e.data == map.data_ptr() && e.version == map._version() && e.T == T) return e;
     cache.erase(it);
   }
-  if (cache.size() > 1024) {
-    for (auto i = cache.begin(); i != cache.end();) i = i->second.impl.expired() ? cache.erase(i) : std::next(i);
-  }
+  purge_expired_orders();
   OrderEntry e(map);
   e.data = map.data_ptr();
   e.version = map._version();
   e.T = T;
+  e.stream = current_stream();
   const int64_t K = map.size(1);
   e.order = empty_i32({std::max<int64_t>(T, 1)}, map.device());
   // 128-bit valid-column unions per 128 ordered rows (maps of <= 128 offsets)
@@ -177,9 +204,10 @@ torch::Tensor convert_transposed_os_ordered(const torch::Tensor &map, int64_t nu
   auto inverse = empty_i32({Sp, K}, map.device());
   const int64_t ntiles = (std::max<int64_t>(num_coarse, 1) + 255) / 256;
   if (!row_order_enabled() || K > 8 || K * ntiles > 16384 || num_sources == 0) {
-    check_rc(spira_hip_convert_transposed_os_partition(map.data_ptr<int32_t>(), map.size(0), static_cast<int>(K),
-                                                       num_sources, Sp, inverse.data_ptr<int32_t>(),
-                                                       current_stream()),
+    // the general inverse (a -1 fill, then one scatter per entry): it does
+    // not rely on the entries partitioning the sources
+    check_rc(spira_hip_convert_transposed_os(map.data_ptr<int32_t>(), map.size(0), static_cast<int>(K), Sp,
+                                             inverse.data_ptr<int32_t>(), current_stream()),
              "convert_transposed_os_ordered");
     return inverse;
   }
@@ -188,6 +216,7 @@ torch::Tensor convert_transposed_os_ordered(const torch::Tensor &map, int64_t nu
   e.version = inverse._version();
   e.T = num_sources;
   e.free = true;
+  e.stream = current_stream();
   e.order = empty_i32({num_sources}, map.device());
   e.masks = torch::empty({(num_sources + 127) / 128 * 2}, torch::TensorOptions(map.device()).dtype(torch::kInt64));
   e.ordered_map = empty_i32({num_sources, K}, map.device());
@@ -200,6 +229,7 @@ torch::Tensor convert_transposed_os_ordered(const torch::Tensor &map, int64_t nu
                e.order.data_ptr<int32_t>(), e.ordered_map.data_ptr<int32_t>(),
                reinterpret_cast<uint64_t *>(e.masks.data_ptr<int64_t>()), ws.data_ptr(), wsb, current_stream()),
            "convert_transposed_os_ordered");
+  purge_expired_orders();
   auto &cache = order_cache();
   cache.erase(inverse.unsafeGetTensorImpl());
   cache.emplace(inverse.unsafeGetTensorImpl(), std::move(e));
@@ -374,6 +404,7 @@ static void run_os(const torch::Tensor *map, int64_t S, int64_t T, const torch::
       if (oe && !oe->free) oe = nullptr;  // (a sorted order only by the rule or on request)
     }
     if (oe) {
+      record_use(oe->stream, {&oe->order, &oe->masks, &oe->ordered_map});
       order = oe->order.data_ptr<int32_t>();
       masks = oe->masks.defined() ? reinterpret_cast<const uint64_t *>(oe->masks.data_ptr<int64_t>()) : nullptr;
       mp = oe->ordered_map.data_ptr<int32_t>();
@@ -751,15 +782,41 @@ void free_buffers() { c10::hip::HIPCachingAllocator::emptyCache(); }
 void reset_error() { (void)hipGetLastError(); }
 
 void register_conv(pybind11::module_ &m) {
-  m.def("cuda_sparse_convolution_forward_os", &forward_os);
-  m.def("cuda_dense_forward", &forward_dense);
+  // The reference binds these without defaults (cuda_sparse_convolution_forward.cu:130-448) and its
+  // callers pass exactly the reference arguments (nn/functional/convolution.py:78-172); the fused
+  // epilogue and the launch tuning of this build are trailing keyword arguments with neutral defaults,
+  // so a call at the reference's arity runs the plain convolution.
+  namespace py = pybind11;
+  const auto epi_args = [](auto... head) {
+    return std::make_tuple(head..., py::arg("scale") = py::none(), py::arg("shift") = py::none(),
+                           py::arg("residual") = py::none(), py::arg("relu") = false);
+  };
+  const auto def_with = [&](const char *name, auto fn, auto args, auto... extra) {
+    std::apply([&](auto... a) { m.def(name, fn, a..., extra...); }, args);
+  };
+  def_with("cuda_sparse_convolution_forward_os", &forward_os,
+           epi_args(py::arg("S"), py::arg("T"), py::arg("out_in_map"), py::arg("X"), py::arg("W")),
+           py::arg("x2") = py::none(), py::arg("tuning") = py::none());
+  def_with("cuda_dense_forward", &forward_dense, epi_args(py::arg("X"), py::arg("W")), py::arg("x2") = py::none(),
+           py::arg("tuning") = py::none());
   m.def("time_conv_os", &time_conv_os, pybind11::arg("S"), pybind11::arg("T"), pybind11::arg("out_in_map"),
         pybind11::arg("X"), pybind11::arg("W"), pybind11::arg("reps"), pybind11::arg("x2") = pybind11::none(),
         pybind11::arg("tuning") = pybind11::none());
-  m.def("cuda_sparse_convolution_forward_ws", &forward_ws);
-  m.def("cuda_sparse_convolution_forward_ws_merged", &forward_ws_merged);
-  m.def("cuda_sparse_convolution_forward_hs", &forward_hs);
-  m.def("cuda_sparse_convolution_forward_hs_merged", &forward_hs_merged);
+  def_with("cuda_sparse_convolution_forward_ws", &forward_ws,
+           epi_args(py::arg("S"), py::arg("T"), py::arg("gather_tile"), py::arg("scatter_tile"), py::arg("parallel"),
+                    py::arg("threshold"), py::arg("X"), py::arg("W"), py::arg("source_masks"),
+                    py::arg("target_masks"), py::arg("nbsizes")));
+  def_with("cuda_sparse_convolution_forward_ws_merged", &forward_ws_merged,
+           epi_args(py::arg("S"), py::arg("T"), py::arg("X"), py::arg("W"), py::arg("naddrs"), py::arg("qnaddrs"),
+                    py::arg("nbmaps"), py::arg("mapsize"), py::arg("qmapsize"), py::arg("transpose")));
+  def_with("cuda_sparse_convolution_forward_hs", &forward_hs,
+           epi_args(py::arg("S"), py::arg("T"), py::arg("gather_tile"), py::arg("scatter_tile"), py::arg("parallel"),
+                    py::arg("threshold"), py::arg("X"), py::arg("W"), py::arg("source_masks"),
+                    py::arg("target_masks"), py::arg("nbsizes"), py::arg("out_in_map")));
+  def_with("cuda_sparse_convolution_forward_hs_merged", &forward_hs_merged,
+           epi_args(py::arg("S"), py::arg("T"), py::arg("X"), py::arg("W"), py::arg("naddrs"), py::arg("qnaddrs"),
+                    py::arg("nbmaps"), py::arg("out_in_map"), py::arg("mapsize"), py::arg("qmapsize"),
+                    py::arg("transpose")));
   m.def("cuda_time_gemm", &time_gemm);
   m.def("cuda_time_gather", &time_gather);
   m.def("cuda_time_scatter", &time_scatter);
@@ -768,6 +825,8 @@ void register_conv(pybind11::module_ &m) {
   m.def("set_os_row_order", &set_row_order);
   m.def("kmap_row_order", &kmap_row_order);
   // an order made with the map (no sort), as a partition inverse carries one
+  // number of cached row orders (for tests: entries of freed maps are dropped)
+  m.def("row_order_cache_size", [] { return static_cast<int64_t>(order_cache().size()); });
   m.def("has_free_row_order", [](const torch::Tensor &map, int64_t T) {
     const OrderEntry *e = cached_order(map, T);
     return e != nullptr && e->free;

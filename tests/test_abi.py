@@ -58,3 +58,15 @@ def test_spira_alias_resolves_to_spira_amd():
     import spira.nn
     assert spira.nn.SparseConv is spira_amd.nn.SparseConv
     assert hasattr(spira, "SparseTensor") and hasattr(spira, "tune") and hasattr(spira, "set_kernel_map_cache")
+
+
+def test_noalloc_scratch_holds_the_maximum_workspace():
+    """The allocation-free flatten_sort's fixed 32 MiB scratch holds the
+    workspace of its maximum input (1048576 points) for both key widths (a
+    host-side size query: no GPU needed)."""
+    lib = ctypes.CDLL(LIB)
+    lib.spira_hip_flatten_sort_workspace.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]
+    for bits in (32, 64):
+        wsb = ctypes.c_size_t(0)
+        assert lib.spira_hip_flatten_sort_workspace(1 << 20, bits, ctypes.byref(wsb)) == 0
+        assert 0 < wsb.value <= 32 << 20, (bits, wsb.value)

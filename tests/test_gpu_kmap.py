@@ -349,6 +349,34 @@ def test_convert_transposed_partition_order(dev, ks):
     assert rel_err(np_(y.float()), orc.conv_os(invn, S, X.double().numpy(), W.double().numpy())) <= 1e-2
 
 
+def test_convert_transposed_ordered_not_a_partition(dev):
+    """A k = 2 map whose targets are a subset of the down-sampled sources
+    leaves some sources in no entry: the inverse made with its row order must
+    still be exact (those rows all -1), its order a permutation of the
+    sources, and a transposed layer walking it must match the oracle on
+    every row (the uncovered rows get a zero sum)."""
+    from spira_amd.nn.functional._native import _C
+    c = scenes.spheres_planes(n=20000, grid=64, seed=9)
+    k, _ = orc.flatten_sort(c, True)
+    kc = orc.downsample(k, (2, 2, 2))[::3].copy()     # every third coarse voxel
+    m = orc.build_kmap(k, kc, (2, 2, 2), (1, 1, 1), 0)[2]
+    S, T = len(k), len(kc)
+    assert int((m >= 0).sum()) < S
+    print(f"[non-partition inverse] S={S} T={T}", flush=True)
+    md = torch.from_numpy(np.ascontiguousarray(m)).to(dev)
+    inv = F.convert_transposed_os_ordered(md, T, S)
+    ref = orc.convert_transposed_os(m, S)
+    assert np.array_equal(np_(inv), ref)
+    order, masks, omap = (np_(t) for t in _C.kmap_row_order(inv, S))
+    assert np.array_equal(np.sort(order), np.arange(S))
+    assert np.array_equal(omap, ref[:S][order])
+    g = torch.Generator().manual_seed(4)
+    X = torch.randn(T, 32, generator=g).half()
+    W = (torch.randn(8, 32, 32, generator=g) / 16).half()
+    y = F.sparse_convolution_forward_os(T, S, inv, X.to(dev), W.to(dev))
+    assert rel_err(np_(y.float()), orc.conv_os(ref, S, X.double().numpy(), W.double().numpy())) <= 1e-2
+
+
 def test_downsample_chain_large(dev):
     """An input above 1024 compaction tiles (2.3M keys): the chained
     downsample takes the device-wide scan at every level (the levels are

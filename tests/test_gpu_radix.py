@@ -21,6 +21,7 @@ def _lib():
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     lib.spira_hip_radix_sort_workspace.argtypes = [i64, i32, ctypes.POINTER(ctypes.c_size_t)]
     lib.spira_hip_radix_sort_pairs.argtypes = [vp, vp, vp, vp, i64, i32, vp, ctypes.c_size_t, vp]
+    lib.spira_hip_radix_sort_status.argtypes = [vp, i64, i32, vp]
     lib.spira_hip_last_error.restype = ctypes.c_char_p
     return lib
 
@@ -36,6 +37,10 @@ def _sort(lib, keys: np.ndarray, vals: np.ndarray, dev):
     ws = torch.empty(max(wsb.value, 1), dtype=torch.uint8, device=dev)
     rc = lib.spira_hip_radix_sort_pairs(kd.data_ptr(), vd.data_ptr(), ko.data_ptr(), vo.data_ptr(), n, bits,
                                         ws.data_ptr(), wsb.value, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, lib.spira_hip_last_error()
+    # no tile's look-back wait ran out (else the output would be incomplete)
+    rc = lib.spira_hip_radix_sort_status(ws.data_ptr(), n, bits,
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 0, lib.spira_hip_last_error()
     torch.cuda.synchronize()
     kin = kd.cpu().numpy().view(keys.dtype)

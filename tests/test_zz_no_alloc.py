@@ -72,3 +72,17 @@ def test_noalloc_rejects_oversize(dev):
     rc = lib.spira_hip_flatten_sort_noalloc(None, MAX_POINTS + 1, 64, None, None, stream)
     assert rc != 0
     assert b"1048576" in lib.spira_hip_last_error()
+
+
+@pytest.mark.parametrize("bits", [64, 32])
+def test_noalloc_at_the_maximum(dev, bits):
+    """Exactly the documented maximum of 1048576 points (the workspace of
+    both key widths fits the fixed scratch), then a smaller call."""
+    lib = _lib()
+    rng = np.random.default_rng(33 + bits)
+    hi = 4000 if bits == 64 else 250
+    big = rng.integers(0, hi, size=(MAX_POINTS, 3)).astype(np.int32)
+    small = rng.integers(0, hi, size=(777, 3)).astype(np.int32)
+    for coords in (big, small):
+        k1, p1, k2, p2 = _sort_both(lib, coords, bits, dev)
+        assert torch.equal(k1, k2) and torch.equal(p1, p2), f"{bits}-bit, n={coords.shape[0]}"
