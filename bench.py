@@ -367,7 +367,10 @@ def kmap_leg(torch, keys):
             api_ms = event_time(torch, lambda: F.build_kmap(keys, tgt, k, 1, 0), reps=20, warmup=3)
             kern_ms = _native._C.time_kmap_search(keys, tgt, (k, k, k), (1, 1, 1), 50)
             nbytes = 8 * S + 8 * T + 4 * k ** 3 * T
+            # valid (target, offset) pairs per target: the scene's neighbour density
+            P = int((F.build_kmap(keys, tgt, k, 1, 0)[2][:T] >= 0).sum().item())
             out[f"k{k}s{s}"] = {"api_us": api_ms * 1e3, "kernel_us": kern_ms * 1e3, "S": S, "T": T,
+                                "P_over_T": round(P / max(T, 1), 3),
                                 "algorithmic_bytes": nbytes, "gbs": nbytes / (kern_ms * 1e-3) / 1e9,
                                 "frac": nbytes / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
@@ -418,7 +421,7 @@ def layer_leg(torch, keys, channels=(16, 32, 64, 128, 256), reps=10):
         out[str(C)] = {"dataflows": res, "selector_pick": pick, "selector_ms": res[pick]["ms"],
                        "os_kernel_ms": kern, "os_kernel_mfma_frac": flops / (kern * 1e-3) / 1e12 /
                        MFMA_F16_PEAK_TFLOPS, "os_kernel_hbm_frac": nbytes / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    return {"pairs": P, "voxels": S, "per_C": out}
+    return {"pairs": P, "voxels": S, "P_over_T": round(P / max(T, 1), 3), "per_C": out}
 
 
 def family_leg(torch, indoor_np, rows, fams):

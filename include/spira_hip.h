@@ -63,9 +63,11 @@ int spira_hip_radix_sort_workspace(int64_t n, int key_bits, size_t *bytes);
 
 /* Stable ascending sort of n (key, int32 value) pairs, keys unsigned 32- or
  * 64-bit: (keys_in, vals_in) -> (keys_out, vals_out); the inputs are left
- * unchanged, n < 2^30.  A hand-written LSD radix sort (8-bit digits,
- * digits shared by every key skipped, decoupled look-back); flatten_sort
- * keeps rocPRIM's sort, which is faster at the benchmark sizes (reference:
+ * unchanged, n < 2^30; vals_in may be null (the values are then the input
+ * indices).  A hand-written LSD radix sort (digits of up to 9 bits over the
+ * bits in which the keys differ, decoupled look-back, staged coalesced
+ * scatter); flatten_sort keeps rocPRIM's sort, which is faster at the
+ * benchmark sizes (reference:
  * the cub::DeviceRadixSort::SortPairs call of FlattenSort,
  * cuda/functions/arg_sort_coodrinates.cu:36-88). */
 int spira_hip_radix_sort_pairs(const void *keys_in, const int32_t *vals_in, void *keys_out, int32_t *vals_out,
