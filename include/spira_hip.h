@@ -258,6 +258,29 @@ int spira_hip_kmap_row_order(const int32_t *out_in_map, int64_t num_targets, int
                              uint64_t *group_masks, int32_t *ordered_map, void *workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
+/* One row-order job of spira_hip_kmap_row_order_batch: the arguments of
+ * spira_hip_kmap_row_order for one map (group_masks required). */
+typedef struct {
+  const int32_t *out_in_map;
+  int64_t num_targets;
+  int num_offsets;
+  int32_t *order;
+  uint64_t *group_masks;
+  int32_t *ordered_map;
+} spira_hip_row_order_job_t;
+
+/* Workspace bytes for spira_hip_kmap_row_order_batch. */
+int spira_hip_kmap_row_order_batch_workspace(int n, const spira_hip_row_order_job_t *jobs, size_t *bytes);
+
+/* spira_hip_kmap_row_order for 1 to 16 maps of at most 27 offsets in one
+ * chain of launches: the maps' rows are concatenated and sorted together
+ * (each key prefixed with its map's index), then the group unions, the group
+ * orders and the ordered rows of all maps run as one launch each.  Every
+ * map's outputs equal spira_hip_kmap_row_order's.  (No reference
+ * counterpart: the row order is this library's own.) */
+int spira_hip_kmap_row_order_batch(int n, const spira_hip_row_order_job_t *jobs, void *workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+
 /* Workspace bytes for spira_hip_voxelize. */
 int spira_hip_voxelize_workspace(int64_t num_points, size_t *bytes);
 

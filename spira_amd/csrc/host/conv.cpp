@@ -256,6 +256,71 @@ std::vector<torch::Tensor> prepare_row_order(const torch::Tensor &map, int64_t T
   return out;
 }
 
+// prepare_row_order for several maps at once: the maps that take a row
+// order and have none cached get it from one batched chain of launches
+// (spira_hip_kmap_row_order_batch: one sort over all maps' rows) when they
+// have 9 to 27 offsets, else one by one.  No reference counterpart.
+void prepare_row_orders(const std::vector<torch::Tensor> &maps, const std::vector<int64_t> &Ts,
+                        const std::vector<int64_t> &requests) {
+  SPIRA_CHECK_ARG(maps.size() == Ts.size() && maps.size() == requests.size(),
+                  "maps, target counts and requests must have the same length");
+  std::vector<size_t> batch;
+  for (size_t i = 0; i < maps.size(); ++i) {
+    const torch::Tensor &map = maps[i];
+    SPIRA_CHECK_ARG(map.dim() == 2 && map.scalar_type() == torch::kInt32, "out_in_map must be 2-D int32");
+    require_device(map, "out_in_map");
+    SPIRA_CHECK_ARG(map.size(0) >= Ts[i], "out_in_map has fewer rows than targets");
+    SPIRA_CHECK_ARG(requests[i] >= -1 && requests[i] <= 1, "row order request must be -1, 0 or 1");
+    const int64_t K = map.size(1);
+    if (!row_order_applies(Ts[i], K, static_cast<int>(requests[i])) || cached_order(map, Ts[i])) continue;
+    bool dup = false;  // (one map listed twice)
+    for (size_t j : batch) dup |= maps[j].unsafeGetTensorImpl() == map.unsafeGetTensorImpl();
+    if (dup) continue;
+    // (maps of at most 8 offsets take their own counting sort)
+    if (K > 8 && K <= 27) batch.push_back(i);
+    else row_order_of(map, Ts[i]);
+  }
+  for (size_t b0 = 0; b0 < batch.size(); b0 += 16) {
+    const size_t nb = std::min<size_t>(16, batch.size() - b0);
+    if (nb == 1) {
+      row_order_of(maps[batch[b0]], Ts[batch[b0]]);
+      continue;
+    }
+    purge_expired_orders();
+    std::vector<OrderEntry> entries;
+    std::vector<spira_hip_row_order_job_t> jobs;
+    entries.reserve(nb);
+    for (size_t q = 0; q < nb; ++q) {
+      const torch::Tensor &map = maps[batch[b0 + q]];
+      const int64_t T = Ts[batch[b0 + q]], K = map.size(1);
+      OrderEntry e(map);
+      e.data = map.data_ptr();
+      e.version = map._version();
+      e.T = T;
+      e.stream = current_stream();
+      e.order = empty_i32({T}, map.device());
+      e.masks = torch::empty({(T + 127) / 128 * 2}, torch::TensorOptions(map.device()).dtype(torch::kInt64));
+      e.ordered_map = empty_i32({T, K}, map.device());
+      jobs.push_back(spira_hip_row_order_job_t{map.data_ptr<int32_t>(), T, static_cast<int>(K),
+                                                e.order.data_ptr<int32_t>(),
+                                                reinterpret_cast<uint64_t *>(e.masks.data_ptr<int64_t>()),
+                                                e.ordered_map.data_ptr<int32_t>()});
+      entries.push_back(std::move(e));
+    }
+    size_t wsb = 0;
+    check_rc(spira_hip_kmap_row_order_batch_workspace(static_cast<int>(nb), jobs.data(), &wsb), "row_order_batch");
+    auto ws = workspace(wsb, maps[batch[b0]].device());
+    check_rc(spira_hip_kmap_row_order_batch(static_cast<int>(nb), jobs.data(), ws.data_ptr(), wsb, current_stream()),
+             "row_order_batch");
+    auto &cache = order_cache();
+    for (size_t q = 0; q < nb; ++q) {
+      const c10::TensorImpl *key = maps[batch[b0 + q]].unsafeGetTensorImpl();
+      cache.erase(key);
+      cache.emplace(key, std::move(entries[q]));
+    }
+  }
+}
+
 // The row order of an output-stationary map as the fp16 kernel uses it:
 // (order, group masks as int64 [ceil(T / 128) * 2], ordered map).  No
 // reference counterpart: exposed for tests.
@@ -838,6 +903,8 @@ void register_conv(pybind11::module_ &m) {
         pybind11::arg("tuning") = pybind11::none());
   m.def("prepare_row_order", &prepare_row_order, pybind11::arg("map"), pybind11::arg("T"),
         pybind11::arg("request") = -1);
+  m.def("prepare_row_orders", &prepare_row_orders, pybind11::arg("maps"), pybind11::arg("T"),
+        pybind11::arg("requests"));
 }
 
 }  // namespace spira_host

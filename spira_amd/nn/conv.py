@@ -122,9 +122,6 @@ class KernelMapCache:
             map_keys.append((s_prev, t_stride, as_tuple(kernel_sizes[i], size=3)))
             s_prev = t_stride
 
-        def row_order(i, kmap):
-            if self.prepare_row_orders and dataflow[i] == 0:
-                F.prepare_row_order(kmap[2], kmap[1], self.row_order_requests.get(map_keys[i], -1))
 
         # Map 0 (voxels[0] to voxels[0]) needs no downsampled level: it is
         # queued between the chained downsample and the host read of the
@@ -138,7 +135,6 @@ class KernelMapCache:
             ready = torch.cuda.Event()
             ready.record()
             kmaps = F.build_kmap_streamed([source_coordinates], kernel_sizes[:1], src_strides[:1], dataflow[:1])
-            row_order(0, kmaps[0])
             ready.synchronize()
             n = host.tolist()
             if n[-1] == 0:
@@ -151,8 +147,13 @@ class KernelMapCache:
             self._coordinates_cache[as_tuple(ts, size=3)] = voxels[i + 1]
         first = len(kmaps)
         kmaps += F.build_kmap_streamed(voxels, kernel_sizes, src_strides, dataflow, begin=first)
-        for i in range(first, len(kernel_sizes)):
-            row_order(i, kmaps[i])
+        # the row orders of the large output-stationary maps, all in one
+        # batched chain of launches
+        if self.prepare_row_orders:
+            sel = [i for i in range(len(kernel_sizes)) if dataflow[i] == 0]
+            if sel:
+                F.prepare_row_orders([kmaps[i][2] for i in sel], [kmaps[i][1] for i in sel],
+                                     [self.row_order_requests.get(map_keys[i], -1) for i in sel])
         for i in range(len(kernel_sizes)):
             t_stride = as_tuple(source_strides[i + 1], size=3)
             self._kernel_maps_cache[(s_stride, t_stride, as_tuple(kernel_sizes[i], size=3))] = [False, *kmaps[i]]

@@ -18,6 +18,7 @@ __all__ = [
     "flat_sort", "unflatten", "downsample", "build_kmap", "convert_transposed_os", "convert_transposed_os_ordered",
     "build_kmap_streamed", "streamed_output_generate", "downsample_chain_launch", "build_kmap_no_small_z", "sparse_quantize",
     "prepare_row_order",
+    "prepare_row_orders",
 ]
 
 
@@ -90,6 +91,15 @@ def prepare_row_order(kmap: torch.Tensor, num_targets: int, request: int = -1) -
     none)."""
     _require_gpu(kmap)
     return list(_C.prepare_row_order(kmap, int(num_targets), int(request)))
+
+
+def prepare_row_orders(kmaps: List[torch.Tensor], num_targets: List[int], requests: List[int]) -> None:
+    """:func:`prepare_row_order` for several maps at once: the maps of at
+    most 27 offsets that take a row order are ordered by one batched chain of
+    launches (one sort over all their rows) instead of one chain each."""
+    for m in kmaps:
+        _require_gpu(m)
+    _C.prepare_row_orders(list(kmaps), [int(t) for t in num_targets], [int(r) for r in requests])
 
 
 def downsample(coordinates: torch.Tensor, target_stride: Tuple[int, int, int]) -> torch.Tensor:

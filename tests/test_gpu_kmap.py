@@ -389,3 +389,32 @@ def test_downsample_chain_large(dev):
     outs = F.streamed_output_generate(torch.from_numpy(rk).to(dev), strides)
     for o, s in zip(outs, strides):
         assert np.array_equal(np_(o), orc.downsample(rk, s)), s
+
+
+def test_row_order_batch_matches_single(dev):
+    """The row orders of several maps made in one batched chain of launches
+    (prepare_row_orders: one sort over all their rows) equal each map's own
+    row order (kmap_row_order of a copy), for maps of 27, 8 and 7 offsets (the
+    batch takes the 27-offset maps, the others keep their own sort) and
+    sizes from 300 to 200k rows; a map listed twice is ordered once."""
+    from spira_amd.nn.functional._native import _C
+    c = scenes.indoor()
+    k, _ = orc.flatten_sort(c, True)
+    maps, Ts = [], []
+    for s in (1, 2, 4, 8):
+        kf = k if s == 1 else orc.downsample(k, (s,) * 3)
+        maps.append(torch.from_numpy(orc.build_kmap(kf, kf, (3, 3, 3), (s,) * 3, 0)[2]).to(dev))
+        Ts.append(len(kf))
+    kd = orc.downsample(k, (2, 2, 2))
+    maps.append(torch.from_numpy(orc.build_kmap(k, kd, (2, 2, 2), (1, 1, 1), 0)[2]).to(dev))
+    Ts.append(len(kd))
+    small = k[:300]
+    maps.append(torch.from_numpy(orc.build_kmap(small, small, (1, 1, 7), (1, 1, 1), 0)[2]).to(dev))
+    Ts.append(300)
+    print(f"[row order batch] T={Ts}", flush=True)
+    _C.prepare_row_orders(maps + [maps[0]], Ts + [Ts[0]], [1] * (len(maps) + 1))
+    for m, T in zip(maps, Ts):
+        got = [np_(t) for t in _C.kmap_row_order(m, T)]
+        ref = [np_(t) for t in _C.kmap_row_order(m.clone(), T)]
+        for g, r in zip(got, ref):
+            assert np.array_equal(g, r), f"T={T} K={m.shape[1]}"
