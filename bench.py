@@ -20,6 +20,9 @@ run inside one event-timed region.  Also reported on the same run:
     dataflow (output-stationary, fused weight-stationary, gather-GEMM-scatter,
     hybrids 3-8) timed per layer call (layerwise_experiment.py:100-186), the
     selector's pick (the fastest), and each against the fp16 MFMA peak;
+  * config1_fp32: config 1's fp32 layer (20k voxels, k = 3, C = 32; also
+    C = 64, 128) on the fp32 MFMA kernel, per call and kernel only, against
+    the fp32 matrix peak;
   * cpu_baseline: the same legs by the OpenMP CPU restatement (oracle/) on
     the host cores, each checked against the GPU result: config 4 end to end
     (headline), the config-2 k = 3 map and a config-3 C = 64 layer.
@@ -42,6 +45,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 # HBM bytes per launch of each submanifold family's output-stationary kernel
 # (plus the finalize kernel of a launch with offset splits), at the tuned
 # launch the selector chose in the measured run: the family leg replays every
@@ -424,6 +428,34 @@ def layer_leg(torch, keys, channels=(16, 32, 64, 128, 256), reps=10):
     return {"pairs": P, "voxels": S, "P_over_T": round(P / max(T, 1), 3), "per_C": out}
 
 
+def config1_leg(torch, reps=20):
+    """Config 1: one fp32 layer (20k voxels on spheres and planes in a 128^3
+    grid, k = 3, C_in = C_out = 32), the output-stationary fp32 MFMA kernel
+    timed through the API call and alone; also C = 64, 128 on the same map."""
+    from spira_amd import scenes
+    from spira_amd.nn import functional as F
+    from spira_amd.nn.functional import _native
+    dev = torch.device("cuda:0")
+    coords = scenes.spheres_planes()
+    keys, _ = F.flat_sort(torch.from_numpy(coords).to(dev), True)
+    S = T = keys.shape[0]
+    m = F.build_kmap(keys, keys, 3, 1, 0)[2]
+    P = int((m[:T] >= 0).sum().item())
+    out = {"voxels": S, "P_over_T": round(P / T, 3), "per_C": {}}
+    for C in (32, 64, 128):
+        g = torch.Generator().manual_seed(C)
+        X = torch.randn(S, C, generator=g).to(dev)
+        W = (torch.randn(27, C, C, generator=g) / np.sqrt(27 * C)).to(dev)
+        api = event_time(torch, lambda: F.sparse_convolution_forward_os(S, T, m, X, W), reps=reps)
+        kern = _native._C.time_conv_os(S, T, m, X, W, reps)
+        flops = 2.0 * P * C * C
+        dense = 2.0 * T * 27 * C * C
+        out["per_C"][str(C)] = {"api_ms": api, "kernel_ms": kern,
+                                "fp32_mfma_frac": flops / (kern * 1e-3) / 1e12 / MFMA_F32_PEAK_TFLOPS,
+                                "dense_fp32_mfma_frac": dense / (kern * 1e-3) / 1e12 / MFMA_F32_PEAK_TFLOPS}
+    return out
+
+
 def family_leg(torch, indoor_np, rows, fams):
     """Every submanifold family's layer shape alone (random features and
     weights on the config-4 map of its stride, the in-network layer's tuned
@@ -485,7 +517,7 @@ def main():
     if args.concurrent_maps:
         from spira_amd.nn.functional import _native
         _native._C.set_concurrent_maps(True)
-    legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer", "config5"}
+    legs = set(args.only.split(",")) if args.only else {"e2e", "kmap", "layer", "config5", "config1"}
     with open(os.path.join(ROOT, "BASELINE.json")) as f:
         baseline = json.load(f)
     dev = torch.device("cuda:0")
@@ -589,6 +621,10 @@ def main():
             cpu["layer_c64"] = {"value": cpu_ms, "unit": "ms", "cores": orc.threads(), "kind": "port",
                                 "sample": "one config-3 C=64 layer (fp32 sums)", "max_err_vs_gpu_x_rms":
                                 rel_err(got, ref)}
+    if "config1" in legs:
+        c1 = config1_leg(torch)
+        res["config1_fp32"] = c1
+        res["config1_fp32_ms"] = c1["per_C"]["32"]["api_ms"]
     if cpu:
         res["cpu_baselines"] = cpu
     if "calib" in legs:

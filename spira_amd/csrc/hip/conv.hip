@@ -1186,33 +1186,137 @@ __device__ __forceinline__ void put(void *Y, int64_t i, float v) {
   else atomicAdd(static_cast<float *>(Y) + i, v);
 }
 
-template <typename FT, int MODE>
-__global__ __launch_bounds__(256) void os_generic_kernel(const int32_t *__restrict__ map, int64_t T, int Kc,
-                                                         const FT *__restrict__ X, int Cin,
-                                                         const FT *__restrict__ W, int Cout, void *Y, Epilogue epi) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= T * Cout) return;
-  const int64_t t = i / Cout;
-  const int c = static_cast<int>(i % Cout);
-  // two-level sum (per offset, then across offsets) keeps the fp32 rounding
-  // error at O((Cin + K) eps) instead of O(Cin K eps)
-  float acc = 0.f;
-  for (int j = 0; j < Kc; ++j) {
-    const int32_t s = map ? map[t * Kc + j] : static_cast<int32_t>(t);  // no map: identity
-    if (s < 0) continue;
-    const FT *x = X + static_cast<int64_t>(s) * Cin;
-    const FT *w = W + (static_cast<int64_t>(j) * Cin) * Cout + c;
-    float part = 0.f;
-    for (int ci = 0; ci < Cin; ++ci) part = fmaf(ld(x + ci), ld(w + static_cast<int64_t>(ci) * Cout), part);
-    acc += part;
+// Output-stationary layer in fp32 storage on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32): a block owns 64 target rows x 16 NB output
+// channels, one 16-row tile per wave, and reads its 64 map rows into LDS
+// once.  The K dimension is walked in steps of
+// (one offset, 32 input channels).  Each lane gathers the 8 channels of its
+// row that its MFMA lane group needs (channels 4 (l / 16) + i and
+// 16 + 4 (l / 16) + i for the step's two 16-channel halves) straight into
+// registers, one step ahead; the step's 32 x BN weight chunk is shared by the
+// four waves through a double-buffered LDS tile whose row pitch (BN + 4
+// floats) keeps the four lane groups on distinct banks.  A wave whose 16 rows
+// have no neighbour at the step's offset skips its MFMAs.  Sums are fp32; each
+// offset's partial sum is added to the total at the end of the offset, as
+// the per-offset sums of the reference's fp32 kernels.
+template <int NB, int MODE>
+__global__ __launch_bounds__(256) void os_f32_kernel(const int32_t *__restrict__ map, int64_t T, int Kc,
+                                                     const float *__restrict__ X, int Cin,
+                                                     const float *__restrict__ W, int Cout, void *Y, Epilogue epi) {
+  constexpr int KC = 32;                                           // input channels per step
+  constexpr int BN = 16 * NB, BS = BN + 4, BPT = KC * BN / 256;  // weight floats per thread and step
+  constexpr int kMapK = 128;                                       // map columns held in LDS
+  __shared__ float Bs[2][KC * BS];
+  __shared__ int32_t Ms[64 * kMapK];  // the block's map rows (kernels of <= 128 offsets)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, kk = lane >> 4;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int n0 = blockIdx.y * BN;
+  const int64_t arow = row0 + 16 * w + l16;  // the row this lane gathers
+  const bool rvalid = arow < T;
+  const int nchunk = (Cin + KC - 1) / KC;
+  const int nsteps = Kc * nchunk;
+  const bool map_lds = map && Kc <= kMapK;
+  if (map_lds) {  // one coalesced read of the block's map rows: the gathers then wait on one load, not two
+    const int64_t rows = T - row0 < 64 ? T - row0 : 64;
+    for (int e = tid; e < rows * Kc; e += 256) Ms[e] = map[row0 * Kc + e];
+    __syncthreads();
   }
-  if constexpr (MODE == kStoreNative) {
-    if (epi.scale) acc *= epi.scale[c];
-    if (epi.shift) acc += epi.shift[c];
-    if (epi.residual) acc += ld(static_cast<const FT *>(epi.residual) + i);
-    if (epi.relu) acc = acc > 0.f ? acc : 0.f;
+  // returns whether any row of the wave's tile has a neighbour at the step's offset
+  auto load_a = [&](int step, float (&a)[8]) {
+    const int k = step / nchunk, c0 = (step - k * nchunk) * KC + 4 * kk;
+    int32_t src = -1;
+    if (rvalid)  // (no map: the identity)
+      src = map_lds ? Ms[(16 * w + l16) * Kc + k] : (map ? map[arow * Kc + k] : static_cast<int32_t>(arow));
+    const bool any = __ballot(src >= 0) != 0;
+    const float *x = X + static_cast<int64_t>(src) * Cin;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + 16 * h + i;
+        a[4 * h + i] = (src >= 0 && c < Cin) ? x[c] : 0.f;
+      }
+    return any;
+  };
+  auto load_b = [&](int step, float (&r)[BPT]) {
+    const int k = step / nchunk, c0 = (step - k * nchunk) * KC;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      const int e = q * 256 + tid, cr = e / BN, cn = e - cr * BN;
+      const int c = c0 + cr, n = n0 + cn;
+      r[q] = (c < Cin && n < Cout) ? W[(static_cast<int64_t>(k) * Cin + c) * Cout + n] : 0.f;
+    }
+  };
+  auto store_b = [&](int buf, const float (&r)[BPT]) {
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      const int e = q * 256 + tid, cr = e / BN, cn = e - cr * BN;
+      Bs[buf][cr * BS + cn] = r[q];
+    }
+  };
+  floatx4 acc[NB], part[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = part[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float ra[8], rbv[BPT];
+  bool act = load_a(0, ra);
+  load_b(0, rbv);
+  store_b(0, rbv);
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const bool more = step + 1 < nsteps;
+    float na[8], nbv[BPT];
+    bool nact = false;
+    if (more) {
+      nact = load_a(step + 1, na);
+      load_b(step + 1, nbv);
+    }
+    const float *bs = Bs[step & 1];
+    // (a tile with no neighbour at this offset adds zeros: skipped)
+    if (act)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          part[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[4 * h + i],
+                                                          bs[(16 * h + 4 * kk + i) * BS + nb * 16 + l16], part[nb],
+                                                          0, 0, 0);
+    if ((step + 1) % nchunk == 0) {  // the offset's partial sum into the total
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[nb] += part[nb];
+        part[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    if (more) store_b((step + 1) & 1, nbv);
+    __syncthreads();
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ra[i] = na[i];
+      act = nact;
+    }
   }
-  put<FT, MODE>(Y, i, acc);
+  // lane l holds rows 4 (l / 16) + i of the wave's tile, column l % 16
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int c = n0 + nb * 16 + l16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t t = row0 + 16 * w + 4 * kk + i;
+      if (t >= T || c >= Cout) continue;
+      float v = acc[nb][i];
+      const int64_t o = t * Cout + c;
+      if constexpr (MODE == kStoreNative) {
+        if (epi.scale) v *= epi.scale[c];
+        if (epi.shift) v += epi.shift[c];
+        if (epi.residual) v += static_cast<const float *>(epi.residual)[o];
+        if (epi.relu) v = v > 0.f ? v : 0.f;
+      }
+      put<float, MODE>(Y, o, v);
+    }
+  }
 }
 
 template <typename FT>
@@ -1742,12 +1846,18 @@ static void launch_gg(int wn, dim3 grid, hipStream_t s, const GroupTable &gt, co
 #undef SPIRA_GG_CALL
 }
 
-template <typename FT, int MODE>
-static void launch_os_generic(hipStream_t s, const int32_t *map, int64_t T, int Kc, const void *X, int Cin,
-                              const void *W, int Cout, void *Y, const Epilogue &epi) {
-  const int64_t n = T * Cout;
-  hipLaunchKernelGGL((os_generic_kernel<FT, MODE>), dim3(div_up(n, 256)), dim3(256), 0, s, map, T, Kc,
-                     static_cast<const FT *>(X), Cin, static_cast<const FT *>(W), Cout, Y, epi);
+template <int MODE>
+static void launch_os_f32(hipStream_t s, const int32_t *map, int64_t T, int Kc, const void *X, int Cin,
+                          const void *W, int Cout, void *Y, const Epilogue &epi) {
+  if (T == 0 || Cout == 0) return;
+  const bool wide = Cout > 32;
+  const dim3 grid(static_cast<unsigned>(div_up(T, 64)), static_cast<unsigned>(div_up(Cout, wide ? 64 : 32)));
+  if (wide)
+    hipLaunchKernelGGL((os_f32_kernel<4, MODE>), grid, dim3(256), 0, s, map, T, Kc, static_cast<const float *>(X),
+                       Cin, static_cast<const float *>(W), Cout, Y, epi);
+  else
+    hipLaunchKernelGGL((os_f32_kernel<2, MODE>), grid, dim3(256), 0, s, map, T, Kc, static_cast<const float *>(X),
+                       Cin, static_cast<const float *>(W), Cout, Y, epi);
 }
 
 static int fill_groups(GroupTable &gt, int K, const int32_t *rows, const int64_t *row_off, int bm) {
@@ -1923,15 +2033,18 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
                            acc, num_targets, c_out, static_cast<_Float16 *>(targets), epi, 1);
     }
   } else {
+    SPIRA_HIP_REQUIRE(num_targets * num_offsets < (int64_t(1) << 31) &&
+                          num_sources * static_cast<int64_t>(c_in) < (int64_t(1) << 31),
+                      "conv_os: fp32 operands above 2^31 elements");
     if (out_mode == SPIRA_OUT_STORE)
-      launch_os_generic<float, kStoreNative>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights,
-                                             c_out, targets, epi);
+      launch_os_f32<kStoreNative>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out,
+                                  targets, epi);
     else if (out_mode == SPIRA_OUT_STORE_F32)
-      launch_os_generic<float, kStoreF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out,
-                                          targets, epi);
+      launch_os_f32<kStoreF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out, targets,
+                               epi);
     else
-      launch_os_generic<float, kAddF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out,
-                                        targets, epi);
+      launch_os_f32<kAddF32>(stream, out_in_map, num_targets, num_offsets, sources, c_in, weights, c_out, targets,
+                             epi);
   }
   SPIRA_HIP_LAUNCH_CHECK();
   return kOk;
