@@ -428,6 +428,26 @@ def layer_leg(torch, keys, channels=(16, 32, 64, 128, 256), reps=10):
     return {"pairs": P, "voxels": S, "P_over_T": round(P / max(T, 1), 3), "per_C": out}
 
 
+def kmap_floor_leg(torch, km):
+    """The write-only floor of the map search: the library's -1 fill
+    (spira_hip_fill_i32) over an int32 array of each config-2 map's size,
+    timed like the search kernel (back-to-back launches between HIP events).
+    A search must write its whole map, so this bounds its HBM fraction."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "spira_amd", "libspira_hip.so"))
+    lib.spira_hip_fill_i32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    out = {}
+    for name, e in km.items():
+        n = (e["algorithmic_bytes"] - 8 * e["S"] - 8 * e["T"]) // 4  # the map's int32 words (K T)
+        x = torch.empty(n, dtype=torch.int32, device=dev)
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        ms = event_time(torch, lambda: lib.spira_hip_fill_i32(x.data_ptr(), n, -1, s), reps=50, warmup=5)
+        out[name] = {"map_bytes": 4 * n, "fill_us": ms * 1e3,
+                     "search_frac_bound": e["algorithmic_bytes"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    return out
+
+
 def config1_leg(torch, reps=20):
     """Config 1: one fp32 layer (20k voxels on spheres and planes in a 128^3
     grid, k = 3, C_in = C_out = 32), the output-stationary fp32 MFMA kernel
@@ -585,6 +605,7 @@ def main():
     if "kmap" in legs:
         km = kmap_leg(torch, lkeys)
         res["kmap"] = km
+        res["kmap_write_floor"] = kmap_floor_leg(torch, km)
         res["kmap_build_us"] = km["k3s1"]["api_us"]
         res["kmap_kernel_us"] = km["k3s1"]["kernel_us"]
         res["kmap_roofline"] = {"bound": "hbm", "achieved": km["k3s1"]["gbs"], "peak": HBM_PEAK_GBS,
