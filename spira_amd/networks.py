@@ -15,6 +15,7 @@ import numpy as np
 from torch import nn
 
 from . import nn as spnn
+from .nn.fusion import absorbed
 from .operators import cat
 from .tensors import SparseTensor
 
@@ -24,13 +25,26 @@ __all__ = ["SparseConvBlock", "SparseConvTransposeBlock", "SparseResBlock", "Spa
 IntOrTuple = Union[int, Tuple[int, ...], List[int]]
 
 
-class SparseConvBlock(nn.Sequential):
+class _Chain(nn.Sequential):
+    """nn.Sequential that does not call the batch norms and ReLUs a fused
+    convolution applies (they would return their input unchanged): the
+    per-module call costs host time that a small layer's kernel does not
+    cover.  Same children and state_dict keys as nn.Sequential."""
+
+    def forward(self, x):
+        for m in self:
+            if not absorbed(m):
+                x = m(x)
+        return x
+
+
+class SparseConvBlock(_Chain):
     def __init__(self, cin: int, cout: int, kernel_size: IntOrTuple, stride: IntOrTuple = 1):
         super().__init__(spnn.SparseConv(cin, cout, kernel_size, stride=stride), spnn.BatchNorm(cout),
                          spnn.ReLU(True))
 
 
-class SparseConvTransposeBlock(nn.Sequential):
+class SparseConvTransposeBlock(_Chain):
     def __init__(self, cin: int, cout: int, kernel_size: IntOrTuple, stride: IntOrTuple = 1):
         super().__init__(spnn.SparseConv(cin, cout, kernel_size, stride=stride, transposed=True),
                          spnn.BatchNorm(cout), spnn.ReLU(True))
@@ -39,22 +53,29 @@ class SparseConvTransposeBlock(nn.Sequential):
 class SparseResBlock(nn.Module):
     def __init__(self, cin: int, cout: int, kernel_size: IntOrTuple, stride: IntOrTuple = 1):
         super().__init__()
-        self.main = nn.Sequential(
+        self.main = _Chain(
             spnn.SparseConv(cin, cout, kernel_size, stride=stride), spnn.BatchNorm(cout), spnn.ReLU(True),
             spnn.SparseConv(cout, cout, kernel_size), spnn.BatchNorm(cout))
         if cin != cout or np.prod(stride) != 1:
-            self.shortcut = nn.Sequential(spnn.SparseConv(cin, cout, 1, stride=stride), spnn.BatchNorm(cout))
+            self.shortcut = _Chain(spnn.SparseConv(cin, cout, 1, stride=stride), spnn.BatchNorm(cout))
         else:
             self.shortcut = nn.Identity()
         self.relu = spnn.ReLU(True)
         self._fused = False  # set by spira_amd.nn.fuse_epilogues
 
     def forward(self, x: SparseTensor) -> SparseTensor:
-        if self._fused and self.main[3]._fused_active():
-            # the shortcut's output is the residual of the second conv's epilogue
-            sc = self.shortcut(x)
-            h = self.main[2](self.main[1](self.main[0](x)))
-            return self.main[4](self.main[3](h, residual=sc))
+        if self._fused:
+            c0, n0, r0, c1, n1 = self.main
+            if c1._fused_active():
+                # the shortcut's output is the residual of the second conv's epilogue
+                sc = self.shortcut(x)
+                h = c0(x)
+                if not absorbed(n0):
+                    h = n0(h)
+                if not absorbed(r0):
+                    h = r0(h)
+                h = c1(h, residual=sc)
+                return h if absorbed(n1) else n1(h)
         return self.relu(self.main(x) + self.shortcut(x))
 
 
@@ -63,7 +84,7 @@ class _SparseResUNet(nn.Module):
                  in_channels: int = 4, width_multiplier: float = 1.0):
         super().__init__()
         ch = [int(width_multiplier * c) for c in [stem_channels] + encoder_channels + decoder_channels]
-        self.stem = nn.Sequential(
+        self.stem = _Chain(
             spnn.SparseConv(in_channels, ch[0], 3), spnn.BatchNorm(ch[0]), spnn.ReLU(True),
             spnn.SparseConv(ch[0], ch[0], 3), spnn.BatchNorm(ch[0]), spnn.ReLU(True))
         self.encoders = nn.ModuleList(
@@ -78,16 +99,21 @@ class _SparseResUNet(nn.Module):
             })
             for k in range(4))
 
-    def _level(self, x: SparseTensor, encoders, decoders) -> List[SparseTensor]:
-        if len(encoders) == 0:
+    def _level(self, x: SparseTensor, k: int) -> List[SparseTensor]:
+        """Encoder level k and everything below it; decoder n - 1 - k joins
+        its output with x (module lists indexed, not sliced: a slice builds
+        a new ModuleList on every call)."""
+        n = len(self.encoders)
+        if k == n:
             return [x]
-        outputs = self._level(encoders[0](x), encoders[1:], decoders[:-1])
-        up = decoders[-1]["upsample"](outputs[-1])
-        y = decoders[-1]["fuse"](cat([up, x]))
+        outputs = self._level(self.encoders[k](x), k + 1)
+        dec = self.decoders[n - 1 - k]
+        up = dec["upsample"](outputs[-1])
+        y = dec["fuse"](cat([up, x]))
         return [x] + outputs + [y]
 
     def forward(self, x: SparseTensor) -> List[SparseTensor]:
-        return self._level(self.stem(x), self.encoders, self.decoders)
+        return self._level(self.stem(x), 0)
 
 
 class SparseResUNet42(_SparseResUNet):

@@ -26,6 +26,7 @@ from ..tensors import SparseTensor
 from ..utils.helpers import as_tuple
 from ..utils.typing import ScalarOrTuple
 from . import functional as F
+from .fusion import bn_affine
 
 __all__ = ["SparseConv", "KernelMapCache"]
 
@@ -198,6 +199,8 @@ class SparseConv(Module):
         # norm (plain attribute, not a submodule) and ReLU
         object.__setattr__(self, "_epi_bn", None)
         self._epi_relu = False
+        # output stride per (input stride, stride, transposed)
+        self._out_strides: Dict[tuple, tuple] = {}
 
     def _fused_active(self) -> bool:
         """The fused epilogue applies: autograd off and, with a batch norm,
@@ -222,7 +225,7 @@ class SparseConv(Module):
 
     @property
     def is_trivial(self) -> bool:
-        return all(x == 1 for x in self.stride) and all(x == 1 for x in self.kernel_size)
+        return self.stride == (1, 1, 1) and self.kernel_size == (1, 1, 1)
 
     @contextlib.contextmanager
     def tune_gs(self, free_buffers: bool = True):
@@ -279,52 +282,57 @@ class SparseConv(Module):
     def forward(self, inputs: SparseTensor, residual: Optional[SparseTensor] = None) -> SparseTensor:
         """residual (fused res blocks only): features added after the batch
         norm and before the ReLU of the fused epilogue."""
+        # (attributes read once: a module's parameters are looked up through
+        # nn.Module.__getattr__, and this runs once per layer and step)
+        cfg = self._tunable_config
+        d = cfg["map_dataflow"]
+        force_os = cfg["force_os"]
+        trivial = self.is_trivial
+        kernel, bias = self.kernel, self.bias
         # an unmaterialised channel concatenation (spira_amd.cat) goes to the
         # output-stationary kernels as its two parts
         parts = inputs._parts
-        if parts is not None and (self.is_trivial or self._tunable_config["map_dataflow"] == 0
-                                  or self._tunable_config["force_os"]):
+        if parts is not None and (trivial or d == 0 or force_os):
             x, x2 = parts
         else:
             x, x2 = inputs._features, None
         epilogue = None
         epilogue_done = False
         if self._fused_active():
-            from .fusion import bn_affine
             scale, shift = bn_affine(self._epi_bn) if self._epi_bn is not None else (None, None)
-            if self.bias is not None:
-                b = self.bias.float()
+            if bias is not None:
+                b = bias.float()
                 shift = b * scale + shift if scale is not None else b
             epilogue = (scale, shift, None if residual is None else residual._features, self._epi_relu)
         elif residual is not None:
             raise ValueError("a residual is only taken by a conv with an active fused epilogue")
-        if self.is_trivial:
+        if trivial:
             if x.is_cuda:
-                y = F.dense_forward(x, self.kernel, epilogue=epilogue, sources2=x2,
-                                    tuning=self._tunable_config.get("os_tuning"))
+                y = F.dense_forward(x, kernel, epilogue=epilogue, sources2=x2, tuning=cfg.get("os_tuning"))
                 if self._os_tuning_data is not None:
                     self._os_tuning_data.append((x.shape[0], x.shape[0], None, x, x2, None))
                 epilogue_done = True
             else:
-                y = torch.mm(x, self.kernel.view(self.in_channels, self.out_channels))
+                y = torch.mm(x, kernel.view(self.in_channels, self.out_channels))
             coords, stride = inputs._coordinates, inputs._stride
         else:
             if self._kernel_map_cache is None:
                 raise ValueError("Kernel map cache must be specified")
-            op = operator.floordiv if self.transposed else operator.mul
-            stride = tuple(op(a, b) for a, b in zip(inputs._stride, self.stride))
+            skey = (inputs._stride, self.stride, self.transposed)
+            stride = self._out_strides.get(skey)
+            if stride is None:
+                op = operator.floordiv if self.transposed else operator.mul
+                stride = tuple(op(a, b) for a, b in zip(inputs._stride, self.stride))
+                self._out_strides[skey] = stride
             cache = self._kernel_map_cache
             coords = cache.get_target_coordinates(inputs._coordinates, inputs._stride, stride, self.transposed)
-            d = self._tunable_config["map_dataflow"]
-            force_os = self._tunable_config["force_os"]
             m = cache.get_kernel_map(inputs._coordinates, inputs._stride, coords, stride, self.kernel_size, d,
                                      force_os, self.transposed)
             # m = (S, T, map, t3, t4, t5, t6, mapsize, qmapsize) of the forward
             # (non-transposed) layer; a transposed layer swaps S and T
             S, T = (m[1], m[0]) if self.transposed else (m[0], m[1])
-            cfg = self._tunable_config
             if d == 0 or force_os:
-                y = F.sparse_convolution_forward_os(S, T, m[2], x, self.kernel, epilogue=epilogue, sources2=x2,
+                y = F.sparse_convolution_forward_os(S, T, m[2], x, kernel, epilogue=epilogue, sources2=x2,
                                                     tuning=cfg.get("os_tuning"))
                 if self._os_tuning_data is not None:
                     mkey = (tuple(inputs._stride), tuple(stride), self.kernel_size)
@@ -332,26 +340,26 @@ class SparseConv(Module):
                         mkey = ("transposed",) + mkey
                     self._os_tuning_data.append((S, T, m[2], x, x2, mkey))
             elif d == 1:
-                y = F.sparse_convolution_forward_ws_merged(S, T, x, self.kernel, m[5], m[6], m[3], m[7], m[8],
+                y = F.sparse_convolution_forward_ws_merged(S, T, x, kernel, m[5], m[6], m[3], m[7], m[8],
                                                            self.transposed, epilogue=epilogue)
             elif d == 2:
                 sm, tm = (m[4], m[3]) if self.transposed else (m[3], m[4])
                 if self._tuning_data is not None:
                     self._tuning_data.append((sm, tm, m[5]))
-                y = F.sparse_convolution_forward_ws(S, T, x, self.kernel, sm, tm, m[5], cfg["gather_tile_size"],
+                y = F.sparse_convolution_forward_ws(S, T, x, kernel, sm, tm, m[5], cfg["gather_tile_size"],
                                                     cfg["scatter_tile_size"], None, cfg["threshold"],
                                                     epilogue=epilogue)
             elif d % 2 == 1:
                 dense = None if d == 3 else m[2]
-                y = F.sparse_convolution_forward_hs_merged(S, T, x, self.kernel, m[5], m[6], m[3], dense, m[7],
+                y = F.sparse_convolution_forward_hs_merged(S, T, x, kernel, m[5], m[6], m[3], dense, m[7],
                                                            m[8], self.transposed, epilogue=epilogue)
             else:
                 sm, tm = (m[4], m[3]) if self.transposed else (m[3], m[4])
                 dense = None if d == 4 else m[2]
-                y = F.sparse_convolution_forward_hs(S, T, x, self.kernel, sm, tm, m[5], dense,
+                y = F.sparse_convolution_forward_hs(S, T, x, kernel, sm, tm, m[5], dense,
                                                     cfg["gather_tile_size"], cfg["scatter_tile_size"], None,
                                                     cfg["threshold"], epilogue=epilogue)
-        if self.is_trivial and epilogue is not None and not epilogue_done:
+        if trivial and epilogue is not None and not epilogue_done:
             scale, shift, res, relu = epilogue
             y = y.float()
             if scale is not None:
@@ -363,8 +371,8 @@ class SparseConv(Module):
             if relu:
                 y = torch.relu(y)
             y = y.to(x.dtype)
-        elif self.bias is not None and epilogue is None:
-            y += self.bias
+        elif bias is not None and epilogue is None:
+            y += bias
         return SparseTensor(features=y, coordinates=coords, stride=stride)
 
 

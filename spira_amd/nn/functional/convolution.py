@@ -119,10 +119,20 @@ def _tuning(tuning) -> Optional[tuple]:
     of at most 16 input channels)."""
     if tuning is None:
         return None
+    if type(tuning) is tuple:
+        t = _TUNINGS.get(tuning)
+        if t is not None:
+            return t
     t = tuple(int(v) for v in tuning)
     if len(t) not in (6, 7):
         raise ValueError(f"an output-stationary tuning has 6 or 7 fields, got {len(t)}")
+    if type(tuning) is tuple and len(_TUNINGS) < 4096:
+        _TUNINGS[tuning] = t
     return t
+
+
+# tunings already checked (a layer passes the same tuple on every call)
+_TUNINGS: dict = {}
 
 
 def dense_forward(sources, weights, *, epilogue=None, sources2=None, tuning=None):

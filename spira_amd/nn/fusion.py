@@ -27,10 +27,13 @@ def bn_affine(bn: nn.BatchNorm1d) -> Tuple[torch.Tensor, torch.Tensor]:
     """(scale, shift) fp32 of an eval-mode batch norm, cached while its
     parameters and running statistics are unchanged:
     scale = weight / sqrt(running_var + eps), shift = bias - running_mean * scale."""
-    key = tuple(t._version if t is not None else -1
-                for t in (bn.weight, bn.bias, bn.running_mean, bn.running_var))
-    cached = getattr(bn, "_spira_affine", None)
-    if cached is not None and cached[0] == key and cached[1].device == bn.running_mean.device:
+    # (the module's dicts read directly: this runs once per fused layer and step)
+    p, b = bn._parameters, bn._buffers
+    w, bb, rm, rv = p.get("weight"), p.get("bias"), b.get("running_mean"), b.get("running_var")
+    key = (-1 if w is None else w._version, -1 if bb is None else bb._version,
+           -1 if rm is None else rm._version, -1 if rv is None else rv._version)
+    cached = bn.__dict__.get("_spira_affine")
+    if cached is not None and cached[0] == key and cached[1].device == rm.device:
         return cached[1], cached[2]
     with torch.no_grad():
         inv = torch.rsqrt(bn.running_var.float() + bn.eps)
@@ -50,7 +53,7 @@ def _absorb(mod: nn.Module, conv: nn.Module) -> None:
 
 def absorbed(mod: nn.Module) -> bool:
     """True when `mod` (a batch norm / ReLU) is applied by a fused conv."""
-    conv = getattr(mod, "_spira_absorbed_by", None)
+    conv = mod.__dict__.get("_spira_absorbed_by")  # (set with object.__setattr__)
     return conv is not None and conv._fused_active()
 
 

@@ -40,6 +40,12 @@ def set_kernel_map_cache(module: Module, cache) -> Module:
 
 
 def as_tuple(value: ScalarOrTuple, *, size: int = 3, name: Optional[str] = None) -> tuple:
+    # (the common case first: a tuple of the right size, as every per-layer
+    # call passes, costs one type and length check)
+    if type(value) is tuple and len(value) == size:
+        return value
+    if type(value) is int:
+        return (value,) * size
     if not isinstance(value, Iterable):
         return tuple(value for _ in range(size))
     value = tuple(value)
