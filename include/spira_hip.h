@@ -351,11 +351,19 @@ typedef struct {
   int row_walk; /* 1: each target walks its own valid offsets on the vector ALU (fp16,
                    c_in <= 16, no row order or concatenation, storage-dtype output;
                    otherwise ignored): for few channels and large, sparse kernels */
+  int balance_offsets; /* > 0: with a row order (group masks), a row tile with more
+                          valid offsets than this is split over ceil(valid / this)
+                          blocks (at most 8), whose fp32 partial tiles a second pass
+                          sums in a fixed order (storage-dtype output, no offset
+                          splits or packing): the longest tiles of a row-ordered map
+                          no longer set the launch's length; -1: off; 0: the
+                          library's choice */
 } spira_hip_os_tuning_t;
 
 /* Workspace bytes of spira_hip_conv_os: an fp32 [num_targets, c_out]
  * partial-sum buffer when a small layer (fewer row blocks than CUs) splits
- * its offsets over blocks.  The workspace must be zero-filled before its
+ * its offsets over blocks, or, under work balance (balance_offsets), a work
+ * list and fp32 partial tiles.  The workspace must be zero-filled before its
  * first use; every call leaves it zero-filled, so a caller keeps one buffer
  * per stream (calls that overlap on one buffer race). */
 int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, int c_out, int dtype, int out_mode,

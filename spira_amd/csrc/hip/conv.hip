@@ -58,11 +58,47 @@ constexpr int kMaxGroups = 128;
 
 enum OutMode { kStoreNative = 0, kStoreF32 = 1, kAddF32 = 2, kAtomicF32 = 3 };
 
+// Work balance of the output-stationary kernel (storage-dtype outputs).
+// A row-ordered map puts rows with many neighbours together, so its row
+// tiles need from a few to all of the kernel's offsets, and the launch lasts
+// as long as its longest tile.  With offsets > 0 a row tile with more than
+// that many valid offsets (its group mask) is split over up to zmax
+// blocks, ceil(valid / offsets) of them.  split_items_kernel lists the launch's work items
+// (row tile t, part p) in row-tile order, items[0 .. *total); grid x walks
+// them (blocks past the list exit), so that a tile's parts run together and
+// no block waits behind empty ones.  Part p of z takes the tile's valid
+// offsets of rank [p n / z, (p + 1) n / z) and writes its fp32 partial tile
+// to part[(tile * zmax + p) * BM * BN ...] (tile = row tile * gy + column
+// tile); a tile that is not split is stored by its one block.
+// split_finalize_kernel then sums each split tile's parts in order
+// 0 .. z - 1 and writes the output with the epilogue.  (Summing in the last
+// part to finish instead needs device-coherent partial tiles: an L2
+// writeback per block, or stores and loads that bypass the L2s, both
+// measured 1.5-5x slower than the separate pass.)  The list and the partial
+// tiles live in the workspace, which arrives zeroed and is left zeroed.
+struct TileSplit {
+  int offsets;  // 0: off
+  int zmax;
+  float *part;
+  int32_t *items;  // (t << 3) | p
+  int32_t *total;
+};
+
+// The number of parts of a row tile whose group mask is (lo, hi).
+__host__ __device__ __forceinline__ int split_parts(uint64_t lo, uint64_t hi, int Kc, int offsets, int zmax) {
+  const uint64_t klo = Kc >= 64 ? ~uint64_t(0) : (uint64_t(1) << Kc) - 1;
+  const uint64_t khi = Kc >= 128 ? ~uint64_t(0) : (Kc > 64 ? (uint64_t(1) << (Kc - 64)) - 1 : 0);
+  const int nact = __builtin_popcountll(lo & klo) + __builtin_popcountll(hi & khi);
+  const int want = (nact + offsets - 1) / offsets;
+  return want < 1 ? 1 : (want > zmax ? zmax : want);
+}
+
 struct Epilogue {
   const float *scale;    // [Cout] or null
   const float *shift;    // [Cout] or null
   const void *residual;  // [T, Cout] in the storage dtype, or null
   int relu;
+  TileSplit split;       // (os_kernel with storage-dtype outputs only)
 };
 
 // Gathered operands of the MMA core.  Both are addressed through buffer
@@ -827,9 +863,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   int64_t bx = blockIdx.x;
   int by = blockIdx.y, bz = blockIdx.z;
   if (xcd_order) xcd_block(bx, by, bz, xcd_order);
+  // work balance: block x takes work item x (row tile, part)
+  const bool balance = MODE == kStoreNative && OP == 1 && epi.split.offsets > 0;
+  if (balance) {
+    const int total = *epi.split.total;
+    const int item = epi.split.items[bx < total ? bx : 0];
+    if (bx >= total) return;  // (block-uniform, before any barrier)
+    bz = item & 7;
+    bx = item >> 3;
+  }
   const int64_t row0 = bx * C::BM;
   const int n0 = by * C::BN;
-  const int j0 = bz * jper;
+  const int j0 = balance ? 0 : bz * jper;
   const int jn = ((j0 + jper) < Kc ? (j0 + jper) : Kc) - j0;
   // offsets [j0, j0 + jn) used by some row of the block, relative to j0
   uint64_t ulo = jn >= 64 ? ~uint64_t(0) : (uint64_t(1) << jn) - 1;
@@ -850,8 +895,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     ulo &= slo;
     uhi &= shi;
   }
-  const int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
+  int nact = __builtin_popcountll(ulo) + __builtin_popcountll(uhi);
   const int nch = (op.CinP + C::KC - 1) / C::KC;
+  // work balance: this block is part bz of its tile's nparts
+  int nparts = 1;
+  if (balance) {
+    // (split_items_kernel counted the same parts from the same mask)
+    nparts = split_parts(ulo, uhi, Kc, epi.split.offsets, epi.split.zmax);
+    if (nparts > 1) {
+      // keep the valid offsets of rank [a0, a1)
+      const int a0 = nact * bz / nparts, a1 = nact * (bz + 1) / nparts;
+      uint64_t lo = ulo, hi = uhi, klo = 0, khi = 0;
+      for (int rk = 0; rk < a1; ++rk) {
+        const bool inlo = lo != 0;
+        const int j = inlo ? __builtin_ctzll(lo) : __builtin_ctzll(hi);
+        if (rk >= a0) {
+          if (inlo) klo |= uint64_t(1) << j;
+          else khi |= uint64_t(1) << j;
+        }
+        if (inlo) lo &= lo - 1;
+        else hi &= hi - 1;
+      }
+      ulo = klo;
+      uhi = khi;
+      nact = a1 - a0;
+    }
+  }
   // OP > 1: OP offsets per step (one channel chunk each)
   const int nsteps = OP > 1 ? (nact + OP - 1) / OP : nact * nch;
 
@@ -1002,6 +1071,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
   } else {
     ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   }
+  if (balance && nparts > 1) {
+    // the partial tile to the part's slot (lane layout of the accumulators:
+    // row 32 wave + 16 rt + 4 (lane / 16) + i, column 16 nb + lane % 16);
+    // split_finalize_kernel writes the output
+    const int64_t tile = bx * static_cast<int64_t>(gridDim.y) + by;
+    const int lq = lane >> 4;
+    float *slot = epi.split.part + (tile * epi.split.zmax + bz) * (C::BM * C::BN);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int nb = 0; nb < 2 * WN; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          slot[(wave * 32 + rt * 16 + lq * 4 + i) * C::BN + nb * 16 + l16] = acc[rt][nb][i];
+    return;
+  }
   if (kh == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -1018,6 +1103,105 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     }
   }
   store_tile<WN, MODE>(acc, orow_s[wave], n0, op.Cout, Y, epi);
+}
+
+// The work list of a balanced launch (TileSplit): one block of 1024
+// threads, each counting the parts of a contiguous run of row tiles; a
+// block-wide exclusive scan of the counts places each run's items.
+__global__ __launch_bounds__(1024) void split_items_kernel(const uint64_t *__restrict__ gmask, int64_t gx, int Kc,
+                                                           TileSplit ts) {
+  __shared__ int wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t per = (gx + 1023) / 1024;
+  const int64_t t0 = tid * per, t1 = t0 + per < gx ? t0 + per : gx;
+  int cnt = 0;
+  for (int64_t t = t0; t < t1; ++t) cnt += split_parts(gmask[2 * t], gmask[2 * t + 1], Kc, ts.offsets, ts.zmax);
+  int incl = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int pos = incl - cnt;
+  for (int q = 0; q < w; ++q) pos += wsum[q];
+  if (tid == 1023) *ts.total = pos + cnt;
+  for (int64_t t = t0; t < t1; ++t) {
+    const int np = split_parts(gmask[2 * t], gmask[2 * t + 1], Kc, ts.offsets, ts.zmax);
+    for (int p = 0; p < np; ++p) ts.items[pos++] = static_cast<int32_t>((t << 3) | p);
+  }
+}
+
+// The outputs of the work-balanced tiles (TileSplit): kFinSubs blocks per
+// (row tile, column tile) of BM = 128 rows x BN columns, block q taking rows
+// [32 q, 32 q + 32); a tile split into z > 1 parts (split_parts of its
+// group mask) sums its z partial tiles in order, re-zeroes them, and writes
+// rows order[row0 + r] (or row0 + r) with the epilogue, rounded like
+// store_tile_vec (scale and shift, fp16, then the residual and ReLU).
+constexpr int kFinSubs = 4;
+template <int BN>
+__global__ __launch_bounds__(256) void split_finalize_kernel(const uint64_t *__restrict__ gmask,
+                                                             const int32_t *__restrict__ order, int64_t T, int Kc,
+                                                             int Cout, int gy, _Float16 *__restrict__ Y,
+                                                             Epilogue epi) {
+  const int64_t tile = blockIdx.x / kFinSubs;
+  const int q = blockIdx.x % kFinSubs;
+  const int64_t t = tile / gy;
+  // (the work list back to zeros: the os_kernel launch has read it)
+  if (q == 0 && tile % gy == 0 && threadIdx.x < epi.split.zmax) epi.split.items[t * epi.split.zmax + threadIdx.x] = 0;
+  if (tile == 0 && q == 0 && threadIdx.x == 0) *epi.split.total = 0;
+  const int z = split_parts(gmask[2 * t], gmask[2 * t + 1], Kc, epi.split.offsets, epi.split.zmax);
+  if (z < 2) return;
+  const int64_t row0 = t * 128;
+  const int n0 = static_cast<int>(tile % gy) * BN;
+  constexpr int N4 = 128 * BN / 4;         // float4 per partial tile
+  constexpr int IT = N4 / kFinSubs / 256;  // per thread: 1, 2, 3 or 4
+  floatx4 *__restrict__ base = reinterpret_cast<floatx4 *>(epi.split.part + tile * epi.split.zmax * (128 * BN));
+  const _Float16 *R = static_cast<const _Float16 *>(epi.residual);
+  // every load first (partial tiles, output rows, scale and shift), then
+  // the residual rows, so that the block waits on memory twice
+  floatx4 pv[IT][8], sc[IT], sh[IT];
+  int64_t o[IT];
+  int cbase[IT];
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int e4 = (q * IT + k) * 256 + threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      if (p < z) pv[k][p] = base[p * N4 + e4];
+    const int row = (e4 * 4) / BN;
+    cbase[k] = n0 + (e4 * 4) % BN;
+    const int64_t lr = row0 + row;
+    o[k] = lr < T ? (order ? order[lr] : lr) : -1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = cbase[k] + i < Cout ? cbase[k] + i : 0;
+      sc[k][i] = epi.scale ? epi.scale[col] : 1.f;
+      sh[k][i] = epi.shift ? epi.shift[col] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int e4 = (q * IT + k) * 256 + threadIdx.x;
+    floatx4 v = pv[k][0];
+#pragma unroll
+    for (int p = 1; p < 8; ++p)
+      if (p < z) v += pv[k][p];  // parts in order 0 .. z - 1
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      if (p < z) base[p * N4 + e4] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (o[k] < 0) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = cbase[k] + i;
+      if (col >= Cout) break;
+      float f = static_cast<float>(static_cast<_Float16>(v[i] * sc[k][i] + sh[k][i]));
+      if (R) f += static_cast<float>(R[o[k] * Cout + col]);
+      if (epi.relu) f = f > 0.f ? f : 0.f;
+      Y[o[k] * Cout + col] = static_cast<_Float16>(f);
+    }
+  }
 }
 
 // Fused weight-stationary pass.  Rows of the pair list are tiled per
@@ -1717,6 +1901,8 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
                     "conv_os tuning: offset_pack must be 0, 1, 2 or 4");
   SPIRA_HIP_REQUIRE(t.block_order >= 0 && t.block_order <= 4, "conv_os tuning: block_order must be 0..4");
   SPIRA_HIP_REQUIRE(t.row_walk == 0 || t.row_walk == 1, "conv_os tuning: row_walk must be 0 or 1");
+  SPIRA_HIP_REQUIRE(t.balance_offsets >= -1 && t.balance_offsets <= 128,
+                    "conv_os tuning: balance_offsets must be -1 .. 128");
   return kOk;
 }
 
@@ -1725,8 +1911,15 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
 // offsets per step (pack: 1, 2 or 4) and the grid.
 struct OsPlan {
   int wn, bm, jper, splits, nks, pack, xcd, deep, da;
+  int bal, zmax;  // work balance: offsets per part (0: off) and parts per tile at most
   bool aligned;
   int64_t gx, gy;
+  // workspace of the work balance: the work list and its length, then the
+  // partial tiles
+  size_t bal_items_bytes() const { return static_cast<size_t>(gx * zmax * 4 + 4 + 255) / 256 * 256; }
+  size_t bal_bytes() const {
+    return bal ? bal_items_bytes() + static_cast<size_t>(gx * gy) * zmax * bm * (32 * wn) * sizeof(float) : 0;
+  }
 };
 
 static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, bool has_map, bool native_store,
@@ -1776,6 +1969,18 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
            Kc <= ring::kMapTileK)
               ? 1
               : 0;
+  // work balance: parts of at most bal offsets, up to 8 per tile
+  pl.bal = 0;
+  pl.zmax = 1;
+  if (native_store && has_map && pl.splits == 1 && pl.pack == 1 && pl.aligned && tn.balance_offsets > 0 &&
+      Kc <= 128 && pl.bm == 128) {
+    const int z = static_cast<int>(std::min<int64_t>(8, div_up(Kc, tn.balance_offsets)));
+    if (z > 1) {
+      pl.bal = tn.balance_offsets;
+      pl.zmax = z;
+      pl.xcd = 0;  // (the work list sets the block order)
+    }
+  }
   return pl;
 }
 
@@ -1880,7 +2085,7 @@ static int fill_f32(float *p, int64_t n, float v, hipStream_t s) {
 }
 
 static Epilogue make_epi(const float *scale, const float *shift, const void *residual, int relu) {
-  Epilogue e;
+  Epilogue e{};
   e.scale = scale;
   e.shift = shift;
   e.residual = residual;
@@ -1923,6 +2128,7 @@ int spira_hip_conv_os_workspace(int64_t num_targets, int num_offsets, int c_in, 
   const OsPlan pl = plan_os(num_targets, num_offsets, c_in, pad_in(c_in), false, c_out, true, true, tn);
   if (pl.splits > 1)
     *bytes = static_cast<size_t>(num_targets) * c_out * sizeof(float);
+  *bytes = std::max(*bytes, pl.bal_bytes());
   return kOk;
 }
 
@@ -2006,7 +2212,33 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
     int rc0 = make_operands(op, sources, num_sources, c_in, prepared, num_offsets, c_out, sources2, c_in2);
     if (rc0) return rc0;
     if (splits == 1) {
-      if (out_mode == SPIRA_OUT_STORE)
+      if (out_mode == SPIRA_OUT_STORE && pl.bal && group_masks) {
+        SPIRA_HIP_REQUIRE(workspace && workspace_bytes >= pl.bal_bytes(),
+                          "conv_os: workspace too small (spira_hip_conv_os_workspace)");
+        Epilogue eb = epi;
+        char *w = static_cast<char *>(workspace);
+        eb.split.offsets = pl.bal;
+        eb.split.zmax = pl.zmax;
+        eb.split.items = reinterpret_cast<int32_t *>(w);
+        eb.split.total = eb.split.items + pl.gx * pl.zmax;
+        eb.split.part = reinterpret_cast<float *>(w + pl.bal_items_bytes());
+        hipLaunchKernelGGL(split_items_kernel, dim3(1), dim3(1024), 0, stream, group_masks, pl.gx, num_offsets,
+                           eb.split);
+        SPIRA_HIP_LAUNCH_CHECK();
+        grid.x = static_cast<unsigned>(pl.gx * pl.zmax);
+        launch_os_any<kStoreNative>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op,
+                                    targets, eb);
+        SPIRA_HIP_LAUNCH_CHECK();
+        const dim3 fg(static_cast<unsigned>(pl.gx * pl.gy * kFinSubs));
+        auto *Yh = static_cast<_Float16 *>(targets);
+        const int gy = static_cast<int>(pl.gy);
+#define SPIRA_FIN_CALL(W)                                                                                       \
+  hipLaunchKernelGGL(split_finalize_kernel<32 * W>, fg, dim3(256), 0, stream, group_masks, row_order, num_targets, \
+                     num_offsets, c_out, gy, Yh, eb)
+        SPIRA_WN_SWITCH(pl.wn, SPIRA_FIN_CALL)
+#undef SPIRA_FIN_CALL
+
+      } else if (out_mode == SPIRA_OUT_STORE)
         launch_os_any<kStoreNative>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op, targets, epi);
       else if (out_mode == SPIRA_OUT_STORE_F32)
         launch_os_any<kStoreF32>(pl, grid, stream, out_in_map, row_order, group_masks, num_targets, num_offsets, op, targets, epi);

@@ -403,7 +403,8 @@ static torch::Tensor zeroed_workspace(size_t bytes, const torch::Device &dev) {
 // A layer's output-stationary launch choices: the kernel's
 // (spira_hip_os_tuning_t, 0 = automatic) and the row order (-1 automatic,
 // 0 off, 1 on).  From Python: a 6-tuple (col_tile, step_channels,
-// offset_splits, offset_pack, block_order, row_order).
+// offset_splits, offset_pack, block_order, row_order), optionally followed
+// by row_walk and balance_offsets.
 struct OsTune {
   spira_hip_os_tuning_t k{};
   int row_order = -1;
@@ -413,7 +414,7 @@ static OsTune tune_of(const TuneArg &t) {
   OsTune r;
   if (!t.has_value()) return r;
   const auto &v = *t;
-  SPIRA_CHECK_ARG(v.size() == 6 || v.size() == 7, "tuning must have 6 or 7 fields");
+  SPIRA_CHECK_ARG(v.size() >= 6 && v.size() <= 8, "tuning must have 6, 7 or 8 fields");
   r.k.col_tile = static_cast<int>(v[0]);
   r.k.step_channels = static_cast<int>(v[1]);
   r.k.offset_splits = static_cast<int>(v[2]);
@@ -421,6 +422,7 @@ static OsTune tune_of(const TuneArg &t) {
   r.k.block_order = static_cast<int>(v[4]);
   r.row_order = static_cast<int>(v[5]);
   r.k.row_walk = v.size() > 6 ? static_cast<int>(v[6]) : 0;
+  r.k.balance_offsets = v.size() > 7 ? static_cast<int>(v[7]) : 0;
   SPIRA_CHECK_ARG(r.row_order >= -1 && r.row_order <= 1, "row_order must be -1, 0 or 1");
   return r;
 }

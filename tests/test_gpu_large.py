@@ -323,3 +323,70 @@ def test_two_step_gathers_concat(dev, indoor):
                                             sources2=Xd[:, 128:].contiguous(), tuning=(128, 128, 0, 0, 0, 1)).float())
     ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
     assert rel_err(y, ref) <= 1e-2
+
+
+# Work balance (tuning balance_offsets, the eighth field): on a row-ordered
+# map, a row tile with more valid offsets than the field is split over
+# several blocks whose fp32 partial tiles a second pass sums.  Checked
+# against the oracle at the benchmark's stride-8 level (the most neighbours
+# per row) and at stride 1, with the fused epilogue and a channel
+# concatenation; repeated calls give identical outputs (the parts are summed
+# in a fixed order), and the workspace comes back zeroed (an offset-split
+# call on the same workspace right after still matches the oracle).
+@pytest.fixture(scope="module")
+def indoor_s8():
+    k, _ = orc.flatten_sort(scenes.indoor(), True)
+    k8 = orc.downsample(k, (8, 8, 8))
+    m = orc.build_kmap(k8, k8, (3, 3, 3), (8, 8, 8), 0)[2]
+    return k8, m
+
+
+@pytest.mark.parametrize("cin,cout,tuning", [
+    (256, 256, (128, 128, 0, 0, 0, 1, 0, 9)),
+    (256, 256, (96, 128, 0, 0, 0, 1, 0, 5)),
+    (128, 128, (0, 64, 0, 0, 2, 1, 0, 9)),
+    (64, 96, (0, 0, 0, 0, 0, 1, 0, 3)),
+])
+def test_balanced_layer(dev, indoor_s8, cin, cout, tuning):
+    k, m = indoor_s8
+    S = T = len(k)
+    X, W = _case(S, cin, cout, dev, seed=cin + 3 * cout)
+    md = torch.from_numpy(m).to(dev)
+    y = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=tuning)
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(np_(y.float()), ref) <= 1e-2
+    y2 = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=tuning)
+    assert torch.equal(y, y2)
+    # the same layer with its offsets split over blocks (fp32 atomics into
+    # the workspace, which must have come back zeroed)
+    y3 = F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=(0, 0, 4, 0, 0, 1, 0, -1))
+    assert rel_err(np_(y3.float()), ref) <= 1e-2
+
+
+def test_balanced_layer_epilogue_concat(dev, indoor_s8):
+    k, m = indoor_s8
+    S = T = len(k)
+    cout = 256
+    X, W = _case(S, 384, cout, dev, seed=21)
+    g = torch.Generator().manual_seed(22)
+    scale = 0.5 + torch.rand(cout, generator=g)
+    shift = 0.1 * torch.randn(cout, generator=g)
+    res = torch.randn(T, cout, generator=g).half()
+    md = torch.from_numpy(m).to(dev)
+    Xd = X.to(dev)
+    y = F.sparse_convolution_forward_os(S, T, md, Xd[:, :256].contiguous(), W.to(dev),
+                                        epilogue=(scale.to(dev), shift.to(dev), res.to(dev), True),
+                                        sources2=Xd[:, 256:].contiguous(), tuning=(128, 128, 0, 0, 0, 1, 0, 9))
+    conv = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    ref = np.maximum(conv * scale.double().numpy() + shift.double().numpy() + res.double().numpy(), 0)
+    assert rel_err(np_(y.float()), ref) <= 1e-2
+
+
+def test_balanced_layer_full_size(dev, indoor):
+    k, m = indoor
+    S = T = len(k)
+    X, W = _case(S, 96, 96, dev, seed=31)
+    md = torch.from_numpy(m).to(dev)
+    y = np_(F.sparse_convolution_forward_os(S, T, md, X.to(dev), W.to(dev), tuning=(0, 0, 0, 0, 0, 1, 0, 3)).float())
+    ref = orc.conv_os(m, T, X.double().numpy(), W.double().numpy())
+    assert rel_err(y, ref) <= 1e-2
