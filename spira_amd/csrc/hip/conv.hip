@@ -121,6 +121,27 @@ constexpr int kRsrcWord3 = 0x00020000;         // raw (untyped) buffer, 32-bit d
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), kRsrcWord3);
 }
+// The same descriptor as four words (base address, stride 0, size, flags),
+// for the inline-assembly loads of load16.
+__device__ __forceinline__ uint32x4 rsrc_words(const void *p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  uint32x4 r;
+  r[0] = static_cast<uint32_t>(a);
+  r[1] = static_cast<uint32_t>(a >> 32) & 0xffffu;
+  r[2] = bytes;
+  r[3] = static_cast<uint32_t>(kRsrcWord3);
+  return r;
+}
+// 16 bytes at byte offset `off` of buffer `r` into v, in place: the
+// register is v's own (tied operand), so the compiler neither waits for the
+// load nor moves the value while it is in flight.  The caller waits
+// (vmcnt) before reading v and ties the value after the wait with pin().
+// (With the compiler's own buffer loads, its register allocation reused the
+// registers of loads still in flight and the inserted waits drained every
+// load of the pipeline at the start of 4 of the 6 unrolled steps.)
+__device__ __forceinline__ void load16(half8 &v, uint32x4 r, uint32_t off) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(v) : "v"(off), "s"(r) : "memory");
+}
 
 
 namespace ring {
@@ -168,8 +189,18 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
 
 // Tile shape per column-tile width and step: one 32-row tile per wave (the
 // kernels are latency-bound: more resident waves beat larger wave tiles),
-// the ring depth, and the waves per SIMD the register budget targets: 4 for
-// up to 96 columns (<= 128 VGPRs, four 40 KiB blocks per CU), 3 for 128.
+// the ring depth, and the blocks per CU the launch planning counts on
+// (WAVES: 4 for up to 96 columns, 3 for 128).  The compiler's occupancy
+// target (OCC) is 4 waves per SIMD for 32-column tiles and 2 for wider ones:
+// a tighter register budget made the wider tiles spill inside the step loop
+// (their double-buffered weight fragments and gathered rows need more than
+// 128 VGPRs).  The DA = 2 build of the two-step-gather kernel targets
+// one wave per SIMD (its accumulators then sit in AGPRs and its loop is
+// scheduled with room to spare), for launches of about one block per CU.
+// (Measured, kernel only: s8 256 -> 256 row-ordered, 128-column tiles and
+// 128-channel steps, 84.7 -> 66.3 us; s8 384 -> 256 124.9 -> 95.8 us; the
+// 529-block s4 128 -> 128 layer at the same tile went 51.1 -> 58.5 us, as
+// it needs two blocks per CU.)
 // (32-column tiles of 32-channel steps take 3 stages, not 4: measured on the
 // config-4 32 -> 32 layers, s1 18.0 -> 17.4 us, s2 20.2 -> 18.9 us.)
 // DS = 1: one more ring stage for 64-channel steps of wide tiles (chosen
@@ -179,6 +210,7 @@ template <int WN, int NKS = 2, int DS = 0> struct TileOf {
   static_assert(DS == 0 || NKS == 4 || (NKS == 8 && WN <= 2), "no room for an extra ring stage");
   static constexpr int NS = (NKS == 2 ? (WN == 2 ? 4 : 3) : (NKS == 8 || WN >= 3 ? 2 : 3)) + DS;
   static constexpr int WAVES = WN <= 3 ? 4 : 3;
+  static constexpr int OCC = WN == 1 ? (NKS == 8 && DS == 1 ? 3 : 4) : 2;
   using C = Cfg<WN, MT, NS, NKS>;
 };
 
@@ -404,40 +436,51 @@ __device__ __forceinline__ void issue(const IssueCtx<C> &cx, const StepIn &st, c
 
 // MFMAs of stage S (rows without a neighbour hold zeros): per 32-channel
 // block kq, the weight fragments of the BN / 16 column tiles, then
-// v_mfma_f32_16x16x32_f16 for both row tiles.  between(KQ) runs after block
-// kq's weight reads are issued and before their wait: the next step's loads
-// issued there overlap the LDS latency and the previous block's MFMAs,
-// instead of all waves of the block issuing them in one burst after the
-// barrier.  acc[rt][nb]: lane l holds rows 4 (l / 16) + i (i < 4) of row tile
-// rt, column l % 16 of column tile nb.
+// v_mfma_f32_16x16x32_f16 for both row tiles.  Wide tiles take their weight
+// fragments in two halves (fewer live registers), so a step is a sequence
+// of phases (kq, half).  The fragments are double-buffered: a phase's LDS
+// reads are issued before the previous phase's MFMAs, and each phase waits
+// only for its own reads (lgkmcnt = the reads issued after them; LDS reads
+// complete in order), so that a wave's LDS reads overlap its MFMAs instead of
+// alternating with them.  between(KQ) runs after block kq's first weight
+// reads are issued: the next step's loads issued there overlap the LDS
+// latency and the MFMAs, instead of all waves of the block issuing them in
+// one burst after the barrier.  acc[rt][nb]: lane l holds rows 4 (l / 16) +
+// i (i < 4) of row tile rt, column l % 16 of column tile nb.
+template <int N> __device__ __forceinline__ void lds_wait_n() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+}
 template <class C, int S, class Between>
 __device__ __forceinline__ void compute(floatx4 (&acc)[2][C::BN / 16], const ReadBase<C::NKS> &rb,
                                         const half8 (&a)[1][C::NKS], Between between) {
   constexpr int NB = C::BN / 16;
-  // wide tiles read their weight fragments in two halves (fewer live
-  // registers); the second half's reads overlap the first half's MFMAs
   constexpr int NH = NB > 4 ? 2 : 1, NBH = NB / NH;
+  constexpr int NP = (C::NKS / 2) * NH;  // phases (kq, half)
   static_assert(NB % NH == 0, "column tiles split evenly");
-  unroll<C::NKS / 2>([&](auto KQ) {
-    constexpr int kq = decltype(KQ)::value;
-    unroll<NH>([&](auto H) {
-      constexpr int h = decltype(H)::value;
-      half8 b[NBH];
-      unroll<NBH>([&](auto B) {
-        constexpr int nb = decltype(B)::value;
-        b[nb] = rd16<S * C::STAGE + (h * NBH + nb) * 16 * C::ROWB>(rb.b[kq]);
-      });
-      if constexpr (h == 0) between(KQ);
-      lds_wait();
-#pragma unroll
-      for (int nb = 0; nb < NBH; ++nb) pin(b[nb]);
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int nb = 0; nb < NBH; ++nb)
-          acc[rt][h * NBH + nb] =
-              __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][2 * kq + rt], b[nb], acc[rt][h * NBH + nb], 0, 0, 0);
+  half8 b[2][NBH];
+  auto rd = [&](auto P) {
+    constexpr int p = decltype(P)::value, kq = p / NH, h = p % NH;
+    unroll<NBH>([&](auto B) {
+      constexpr int nb = decltype(B)::value;
+      b[p & 1][nb] = rd16<S * C::STAGE + (h * NBH + nb) * 16 * C::ROWB>(rb.b[kq]);
     });
+  };
+  rd(std::integral_constant<int, 0>{});
+  unroll<NP>([&](auto P) {
+    constexpr int p = decltype(P)::value, kq = p / NH, h = p % NH;
+    if constexpr (p + 1 < NP) rd(std::integral_constant<int, p + 1>{});
+    if constexpr (h == 0) between(std::integral_constant<int, kq>{});
+    if constexpr (p + 1 < NP) lds_wait_n<NBH>();
+    else lds_wait();
+#pragma unroll
+    for (int nb = 0; nb < NBH; ++nb) pin(b[p & 1][nb]);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int nb = 0; nb < NBH; ++nb)
+        acc[rt][h * NBH + nb] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][2 * kq + rt], b[p & 1][nb], acc[rt][h * NBH + nb], 0, 0, 0);
   });
 }
 
@@ -579,12 +622,27 @@ __device__ __forceinline__ void issue_b(const IssueCtx<C> &cx, const StepIn &st,
 // channel offset are kept one step for its weights.  The loop's unrolled
 // period is 6 (stage v % 2, register slot v % 3); steps past nsteps are
 // skipped (block-uniform).
+// The A loads (gathered rows, slice KS) of a step for aligned rows of one
+// source, as issue_a issues them, through load16.
+template <class C, int KS>
+__device__ __forceinline__ void issue_a16(const IssueCtx<C> &cx, const StepIn &st, const Operands &op, uint32x4 xw,
+                                          half8 (&a)[1][C::NKS]) {
+  constexpr int rt = KS & 1;
+  const int k0 = st.kb + (KS >> 1) * 32;
+  const int32_t ix = st.idx[rt];
+  const bool ok = st.live & (ix >= 0) & (cx.kh8 < op.Cin - k0);
+  const uint32_t rb1 = static_cast<uint32_t>(ix) * static_cast<uint32_t>(op.C1 * 2);
+  load16(a[0][KS], xw, ok ? rb1 + static_cast<uint32_t>(k0 * 2) + cx.kh16 : kOutOfRange);
+}
+
 template <class C, bool ALIGNED, bool CAT, class Resolve>
 __device__ __forceinline__ void run_da(floatx4 (&acc)[2][C::BN / 16], int nsteps, Resolve resolve,
                                        const Operands &op, int n0, char *ring) {
   static_assert(C::NS == 2 && C::BM == 128, "two LDS stages, one row tile per wave");
   constexpr int LA = C::NKS;  // gathered-row loads per wave and step
+  constexpr bool A16 = ALIGNED && !CAT;  // gathers through load16
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const uint32x4 xw = rsrc_words(op.X, op.xbytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(op.X, op.xbytes);
   const __amdgpu_buffer_rsrc_t xr2 = make_rsrc(op.X2 ? op.X2 : op.X, op.X2 ? op.x2bytes : 0u);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(op.WT, op.wbytes);
@@ -606,33 +664,55 @@ __device__ __forceinline__ void run_da(floatx4 (&acc)[2][C::BN / 16], int nsteps
     if (st.live) resolve(u, std::integral_constant<int, 0>{}, st);
     return st;
   };
+  auto gather = [&](auto KS, const StepIn &st, half8(&a)[1][C::NKS]) {
+    if constexpr (A16) issue_a16<C, decltype(KS)::value>(cx, st, op, xw, a);
+    else issue_a<C, ALIGNED, CAT, decltype(KS)::value>(cx, st, op, xr, xr2, a);
+  };
+  if constexpr (A16) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int k = 0; k < C::NKS; ++k) areg[q][0][k] = half8{};
+  }
   // prologue: A(0), B(0), A(1)
   StepIn st0 = prepare(0);
-  unroll<C::NKS>([&](auto KS) { issue_a<C, ALIGNED, CAT, decltype(KS)::value>(cx, st0, op, xr, xr2, areg[0]); });
+  unroll<C::NKS>([&](auto KS) { gather(KS, st0, areg[0]); });
   issue_b<C, 0>(cx, st0, op, wr);
   StepIn nb = prepare(1);  // step v + 1: its weights are issued in step v
   // (the map-tile read that resolve(2) takes was issued by resolve(1), with
   // no compute, and so no LDS wait, in between)
   lds_wait();
-  unroll<C::NKS>([&](auto KS) { issue_a<C, ALIGNED, CAT, decltype(KS)::value>(cx, nb, op, xr, xr2, areg[1]); });
+  unroll<C::NKS>([&](auto KS) { gather(KS, nb, areg[1]); });
   for (int s = 0; s < nsteps; s += 6) {
     unroll<6>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if (s + i < nsteps) {
         wait_vm<LA>();
         __builtin_amdgcn_s_barrier();
+        if constexpr (A16) {
+#pragma unroll
+          for (int k = 0; k < C::NKS; ++k) pin(areg[i % 3][0][k]);  // (loaded: the wait covers them)
+        }
         const StepIn na = prepare(s + i + 2);
         compute<C, i % 2>(acc, rb, areg[i % 3], [&](auto KQ) {
           constexpr int kq = decltype(KQ)::value;
           if constexpr (kq == 0) issue_b<C, (i + 1) % 2>(cx, nb, op, wr);
-          issue_a<C, ALIGNED, CAT, 2 * kq>(cx, na, op, xr, xr2, areg[(i + 2) % 3]);
-          issue_a<C, ALIGNED, CAT, 2 * kq + 1>(cx, na, op, xr, xr2, areg[(i + 2) % 3]);
+          gather(std::integral_constant<int, 2 * kq>{}, na, areg[(i + 2) % 3]);
+          gather(std::integral_constant<int, 2 * kq + 1>{}, na, areg[(i + 2) % 3]);
         });
         nb = na;
       }
     });
   }
   wait_vm<0>();
+  if constexpr (A16) {
+    // the last steps' loads (past nsteps) land in their registers only now:
+    // the registers stay reserved until this wait
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int k = 0; k < C::NKS; ++k) pin(areg[q][0][k]);
+  }
 }
 
 // Scalar iterator over the set bits of a 128-bit offset set, nch channel
@@ -842,7 +922,7 @@ __device__ __forceinline__ void xcd_block(int64_t &bx, int &by, int &bz, int ord
 // `gmask` (2 words per 128 logical rows: the union of their valid columns)
 // lets the block skip offsets none of its rows uses.
 template <int WN, int MODE, bool ALIGNED, int NKS, bool CAT, int OP, int DS = 0, int DA = 0>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileOf<WN, NKS, DS>::WAVES))) void os_kernel(const int32_t *__restrict__ map,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DA == 2 ? 1 : ring::TileOf<WN, NKS, DS>::OCC))) void os_kernel(const int32_t *__restrict__ map,
                                                     const int32_t *__restrict__ order,
                                                     const uint64_t *__restrict__ gmask, int64_t T, int Kc, int jper,
                                                     Operands op, void *Y, Epilogue epi, int xcd_order) {
@@ -1064,7 +1144,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ring::TileO
     pit.step(nch);
     if (tiled) read_tile();
   };
-  if constexpr (DA == 1) {
+  if constexpr (DA >= 1) {
     // gathered rows two steps ahead (maps held in LDS only)
     if (tiled) ring::run_da<C, ALIGNED, CAT>(acc, nsteps, resolve, op, n0, ring_lds);
     else ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
@@ -1812,7 +1892,9 @@ static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, cons
 #define SPIRA_OS_CALL(W)                                                                                             \
   hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS, DA>), grid, dim3(256), 0, s, map, order, rowmask, T, \
                      Kc, jper, op, Y, epi, xcd)
-  if constexpr ((DS == 1 && NKS == 4) || DA == 1) {  // (96- and 128-column tiles only)
+  if constexpr (DA == 2) {  // (128-column tiles only)
+    SPIRA_OS_CALL(4);
+  } else if constexpr ((DS == 1 && NKS == 4) || DA == 1) {  // (96- and 128-column tiles only)
     if (wn == 3) SPIRA_OS_CALL(3);
     else SPIRA_OS_CALL(4);
   } else if constexpr (DS == 1) {  // (32- and 64-column tiles only)
@@ -1969,6 +2051,8 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
            Kc <= ring::kMapTileK)
               ? 1
               : 0;
+  // the one-wave-per-SIMD build where the grid is about one block per CU
+  if (pl.da && pl.wn == 4 && pl.nks == 8 && pl.gx * pl.gy * pl.splits * 4 <= static_cast<int64_t>(cus) * 5) pl.da = 2;
   // work balance: parts of at most bal offsets, up to 8 per tile
   pl.bal = 0;
   pl.zmax = 1;
@@ -2009,6 +2093,8 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
       if (nks == 8 && pl.deep)
         launch_os<MODE, true, 8, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      else if (nks == 8 && pl.da == 2)
+        launch_os<MODE, true, 8, true, 1, 0, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 8 && pl.da)
         launch_os<MODE, true, 8, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
       else if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
@@ -2021,6 +2107,8 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
     }
   } else if (nks == 8 && pl.deep)
     launch_os<MODE, true, 8, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  else if (nks == 8 && pl.da == 2)
+    launch_os<MODE, true, 8, false, 1, 0, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 8 && pl.da)
     launch_os<MODE, true, 8, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
   else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
