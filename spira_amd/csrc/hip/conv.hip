@@ -191,10 +191,11 @@ template <int WN, int MT, int NS_, int NKS_> struct Cfg {
 // kernels are latency-bound: more resident waves beat larger wave tiles),
 // the ring depth, and the blocks per CU the launch planning counts on
 // (WAVES: 4 for up to 96 columns, 3 for 128).  The compiler's occupancy
-// target (OCC) is 4 waves per SIMD for 32-column tiles and 2 for wider ones:
-// a tighter register budget made the wider tiles spill inside the step loop
-// (their double-buffered weight fragments and gathered rows need more than
-// 128 VGPRs).  The DA = 2 build of the two-step-gather kernel targets
+// target (OCC) is the most waves per SIMD that each tile reaches without
+// spilling inside the step loop: 4 for 32-column tiles, 3 for 64 and 96
+// columns and 2 for 128 with 32- and 64-channel steps; 2 for the tiles
+// wider than 32 columns with 128-channel steps, whose weight fragments are
+// double-buffered (compute).  The DA = 2 build of the two-step-gather kernel targets
 // one wave per SIMD (its accumulators then sit in AGPRs and its loop is
 // scheduled with room to spare), for launches of about one block per CU.
 // (Measured, kernel only: s8 256 -> 256 row-ordered, 128-column tiles and
@@ -210,7 +211,8 @@ template <int WN, int NKS = 2, int DS = 0> struct TileOf {
   static_assert(DS == 0 || NKS == 4 || (NKS == 8 && WN <= 2), "no room for an extra ring stage");
   static constexpr int NS = (NKS == 2 ? (WN == 2 ? 4 : 3) : (NKS == 8 || WN >= 3 ? 2 : 3)) + DS;
   static constexpr int WAVES = WN <= 3 ? 4 : 3;
-  static constexpr int OCC = WN == 1 ? (NKS == 8 && DS == 1 ? 3 : 4) : 2;
+  // (only 128-channel steps double-buffer their weight fragments)
+  static constexpr int OCC = NKS == 8 ? (WN == 1 ? (DS == 1 ? 3 : 4) : 2) : (WN == 1 ? 4 : (WN <= 3 ? 3 : 2));
   using C = Cfg<WN, MT, NS, NKS>;
 };
 
@@ -438,11 +440,12 @@ __device__ __forceinline__ void issue(const IssueCtx<C> &cx, const StepIn &st, c
 // block kq, the weight fragments of the BN / 16 column tiles, then
 // v_mfma_f32_16x16x32_f16 for both row tiles.  Wide tiles take their weight
 // fragments in two halves (fewer live registers), so a step is a sequence
-// of phases (kq, half).  The fragments are double-buffered: a phase's LDS
-// reads are issued before the previous phase's MFMAs, and each phase waits
-// only for its own reads (lgkmcnt = the reads issued after them; LDS reads
-// complete in order), so that a wave's LDS reads overlap its MFMAs instead of
-// alternating with them.  between(KQ) runs after block kq's first weight
+// of phases (kq, half).  With 128-channel steps the fragments are
+// double-buffered: a phase's LDS reads are issued before the previous
+// phase's MFMAs, and each phase waits only for its own reads (lgkmcnt = the
+// reads issued after them; LDS reads complete in order), so that a wave's
+// LDS reads overlap its MFMAs instead of alternating with them.  (Shorter
+// steps keep one buffer: the second cost them a wave per SIMD.)  between(KQ) runs after block kq's first weight
 // reads are issued: the next step's loads issued there overlap the LDS
 // latency and the MFMAs, instead of all waves of the block issuing them in
 // one burst after the barrier.  acc[rt][nb]: lane l holds rows 4 (l / 16) +
@@ -457,30 +460,33 @@ __device__ __forceinline__ void compute(floatx4 (&acc)[2][C::BN / 16], const Rea
   constexpr int NB = C::BN / 16;
   constexpr int NH = NB > 4 ? 2 : 1, NBH = NB / NH;
   constexpr int NP = (C::NKS / 2) * NH;  // phases (kq, half)
+  constexpr bool DB = C::NKS == 8;        // double-buffered fragments
   static_assert(NB % NH == 0, "column tiles split evenly");
-  half8 b[2][NBH];
+  half8 b[DB ? 2 : 1][NBH];
   auto rd = [&](auto P) {
     constexpr int p = decltype(P)::value, kq = p / NH, h = p % NH;
     unroll<NBH>([&](auto B) {
       constexpr int nb = decltype(B)::value;
-      b[p & 1][nb] = rd16<S * C::STAGE + (h * NBH + nb) * 16 * C::ROWB>(rb.b[kq]);
+      b[DB ? (p & 1) : 0][nb] = rd16<S * C::STAGE + (h * NBH + nb) * 16 * C::ROWB>(rb.b[kq]);
     });
   };
-  rd(std::integral_constant<int, 0>{});
+  if constexpr (DB) rd(std::integral_constant<int, 0>{});
   unroll<NP>([&](auto P) {
     constexpr int p = decltype(P)::value, kq = p / NH, h = p % NH;
-    if constexpr (p + 1 < NP) rd(std::integral_constant<int, p + 1>{});
+    constexpr int cur = DB ? (p & 1) : 0;
+    if constexpr (!DB) rd(P);
+    else if constexpr (p + 1 < NP) rd(std::integral_constant<int, p + 1>{});
     if constexpr (h == 0) between(std::integral_constant<int, kq>{});
-    if constexpr (p + 1 < NP) lds_wait_n<NBH>();
+    if constexpr (DB && p + 1 < NP) lds_wait_n<NBH>();
     else lds_wait();
 #pragma unroll
-    for (int nb = 0; nb < NBH; ++nb) pin(b[p & 1][nb]);
+    for (int nb = 0; nb < NBH; ++nb) pin(b[cur][nb]);
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
       for (int nb = 0; nb < NBH; ++nb)
         acc[rt][h * NBH + nb] =
-            __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][2 * kq + rt], b[p & 1][nb], acc[rt][h * NBH + nb], 0, 0, 0);
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][2 * kq + rt], b[cur][nb], acc[rt][h * NBH + nb], 0, 0, 0);
   });
 }
 
@@ -2289,8 +2295,11 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
   if (mfma_path(dtype)) {
     SPIRA_HIP_REQUIRE(prepared != nullptr, "conv_os: fp16 needs prepared weights (spira_hip_prepare_weights)");
     const int cin_all = c_in + c_in2;
-    const OsPlan pl = plan_os(num_targets, num_offsets, cin_all, pad_in(cin_all), c_in2 > 0, c_out,
-                              out_in_map != nullptr, out_mode == SPIRA_OUT_STORE, tn);
+    OsPlan pl = plan_os(num_targets, num_offsets, cin_all, pad_in(cin_all), c_in2 > 0, c_out,
+                        out_in_map != nullptr, out_mode == SPIRA_OUT_STORE, tn);
+    // (the one-wave-per-SIMD build only for row-ordered maps: their longest
+    // tiles come first, so blocks past the first round are short ones)
+    if (pl.da == 2 && !group_masks) pl.da = 1;
     const int jper = pl.jper;
     const int splits = pl.splits;
     dim3 grid(static_cast<unsigned>(pl.gx), static_cast<unsigned>(pl.gy), static_cast<unsigned>(splits));
