@@ -358,6 +358,10 @@ typedef struct {
                           splits or packing): the longest tiles of a row-ordered map
                           no longer set the launch's length; -1: off; 0: the
                           library's choice */
+  int blocks_per_cu; /* 1 .. 8: at most this many resident blocks per CU (dynamic
+                        LDS reserves the rest), so that a small grid spreads over
+                        all CUs; -1: no cap; 0: the library's choice (with a row
+                        order: the grid's blocks per CU, rounded down, at least 1) */
 } spira_hip_os_tuning_t;
 
 /* Workspace bytes of spira_hip_conv_os: an fp32 [num_targets, c_out]

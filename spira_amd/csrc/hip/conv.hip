@@ -40,6 +40,8 @@
 #include "../../../include/spira_hip.h"
 
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -1882,6 +1884,33 @@ static int make_operands(Operands &op, const void *X, int64_t xrows, int Cin, co
   return kOk;
 }
 
+// Dynamic LDS that caps a launch at `bpc` resident blocks per CU (0: no
+// cap): the hardware places the blocks of a small grid unevenly, several on
+// some CUs while others idle, and a row-ordered map's blocks past the first
+// round are its short ones.  The kernel's static LDS is read once per kernel.
+static size_t os_lds_pad(const void *fn, int bpc) {
+  if (bpc <= 0) return 0;
+  static std::mutex mu;
+  static std::unordered_map<const void *, long> lds;
+  long st;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = lds.find(fn);
+    if (it == lds.end()) {
+      hipFuncAttributes at;
+      st = hipFuncGetAttributes(&at, fn) == hipSuccess ? static_cast<long>(at.sharedSizeBytes) : -1;
+      lds.emplace(fn, st);
+    } else {
+      st = it->second;
+    }
+  }
+  if (st < 0) return 0;
+  constexpr long kLdsPerCu = 160 * 1024;
+  const long need = kLdsPerCu / (bpc + 1) - st + 256;  // bpc + 1 blocks no longer fit
+  const long room = kLdsPerCu / bpc - st - 256;        // bpc blocks still do
+  return (need > 0 && need <= room) ? static_cast<size_t>(need) : 0;
+}
+
 // launch `K<WN, ...>` for the column-tile width chosen at run time
 #define SPIRA_WN_SWITCH(wn, CALL) \
   switch (wn) {                   \
@@ -1895,9 +1924,12 @@ template <int MODE, bool AL, int NKS, bool CAT = false, int OP = 1, int DS = 0, 
 static void launch_os(int wn, dim3 grid, hipStream_t s, const int32_t *map, const int32_t *order,
                       const uint64_t *rowmask, int64_t T, int Kc, int jper, const Operands &op,
                       void *Y, const Epilogue &epi, int xcd = 0) {
-#define SPIRA_OS_CALL(W)                                                                                             \
-  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS, DA>), grid, dim3(256), 0, s, map, order, rowmask, T, \
-                     Kc, jper, op, Y, epi, xcd)
+  // (xcd: the block order in bits 0-7, the blocks-per-CU cap above them)
+#define SPIRA_OS_CALL(W)                                                                                       \
+  hipLaunchKernelGGL((os_kernel<W, MODE, AL, NKS, CAT, OP, DS, DA>), grid, dim3(256),                           \
+                     os_lds_pad(reinterpret_cast<const void *>(&os_kernel<W, MODE, AL, NKS, CAT, OP, DS, DA>), \
+                                xcd >> 8),                                                                   \
+                     s, map, order, rowmask, T, Kc, jper, op, Y, epi, xcd & 0xff)
   if constexpr (DA == 2) {  // (128-column tiles only)
     SPIRA_OS_CALL(4);
   } else if constexpr ((DS == 1 && NKS == 4) || DA == 1) {  // (96- and 128-column tiles only)
@@ -1991,6 +2023,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
   SPIRA_HIP_REQUIRE(t.row_walk == 0 || t.row_walk == 1, "conv_os tuning: row_walk must be 0 or 1");
   SPIRA_HIP_REQUIRE(t.balance_offsets >= -1 && t.balance_offsets <= 128,
                     "conv_os tuning: balance_offsets must be -1 .. 128");
+  SPIRA_HIP_REQUIRE(t.blocks_per_cu >= -1 && t.blocks_per_cu <= 8, "conv_os tuning: blocks_per_cu must be -1 .. 8");
   return kOk;
 }
 
@@ -2000,6 +2033,7 @@ static int check_tuning(const spira_hip_os_tuning_t &t) {
 struct OsPlan {
   int wn, bm, jper, splits, nks, pack, xcd, deep, da;
   int bal, zmax;  // work balance: offsets per part (0: off) and parts per tile at most
+  int bpc;        // resident blocks per CU at most (0: no cap)
   bool aligned;
   int64_t gx, gy;
   // workspace of the work balance: the work list and its length, then the
@@ -2059,6 +2093,7 @@ static OsPlan plan_os(int64_t T, int Kc, int Cin, int CinP, bool cat, int Cout, 
               : 0;
   // the one-wave-per-SIMD build where the grid is about one block per CU
   if (pl.da && pl.wn == 4 && pl.nks == 8 && pl.gx * pl.gy * pl.splits * 4 <= static_cast<int64_t>(cus) * 5) pl.da = 2;
+  pl.bpc = tn.blocks_per_cu > 0 ? tn.blocks_per_cu : 0;
   // work balance: parts of at most bal offsets, up to 8 per tile
   pl.bal = 0;
   pl.zmax = 1;
@@ -2082,48 +2117,48 @@ static void launch_os_any(const OsPlan &pl, dim3 grid, hipStream_t s, const int3
   const bool cat = op.X2 != nullptr;
   if constexpr (MODE == kStoreNative) {
     if (pl.pack == 4) {
-      if (nks == 4) launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-      else launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      if (nks == 4) launch_os<MODE, true, 4, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+      else launch_os<MODE, true, 8, false, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
       return;
     }
     if (pl.pack == 2) {
-      if (nks == 2) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-      else if (nks == 4) launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-      else launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+      if (nks == 2) launch_os<MODE, true, 2, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+      else if (nks == 4) launch_os<MODE, true, 4, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+      else launch_os<MODE, true, 8, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
       return;
     }
   }
-  if (!pl.aligned) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+  if (!pl.aligned) launch_os<MODE, false, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
   else if (cat) {
     // channel concatenations: storage-dtype outputs (split or not)
     if constexpr (MODE == kStoreNative || MODE == kAtomicF32) {
       if (nks == 8 && pl.deep)
-        launch_os<MODE, true, 8, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+        launch_os<MODE, true, 8, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
       else if (nks == 8 && pl.da == 2)
-        launch_os<MODE, true, 8, true, 1, 0, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+        launch_os<MODE, true, 8, true, 1, 0, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
       else if (nks == 8 && pl.da)
-        launch_os<MODE, true, 8, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-      else if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+        launch_os<MODE, true, 8, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+      else if (nks == 8) launch_os<MODE, true, 8, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
       else if (nks == 4 && pl.deep)
-        launch_os<MODE, true, 4, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+        launch_os<MODE, true, 4, true, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
       else if (nks == 4 && pl.da)
-        launch_os<MODE, true, 4, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-      else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-      else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+        launch_os<MODE, true, 4, true, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+      else if (nks == 4) launch_os<MODE, true, 4, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+      else launch_os<MODE, true, 2, true>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
     }
   } else if (nks == 8 && pl.deep)
-    launch_os<MODE, true, 8, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+    launch_os<MODE, true, 8, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
   else if (nks == 8 && pl.da == 2)
-    launch_os<MODE, true, 8, false, 1, 0, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+    launch_os<MODE, true, 8, false, 1, 0, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
   else if (nks == 8 && pl.da)
-    launch_os<MODE, true, 8, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-  else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+    launch_os<MODE, true, 8, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+  else if (nks == 8) launch_os<MODE, true, 8>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
   else if (nks == 4 && pl.deep)
-    launch_os<MODE, true, 4, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+    launch_os<MODE, true, 4, false, 1, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
   else if (nks == 4 && pl.da)
-    launch_os<MODE, true, 4, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-  else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
-  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd);
+    launch_os<MODE, true, 4, false, 1, 0, 1>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+  else if (nks == 4) launch_os<MODE, true, 4>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
+  else launch_os<MODE, true, 2>(wn, grid, s, map, order, rowmask, T, Kc, jper, op, Y, epi, pl.xcd | (pl.bpc << 8));
 }
 
 template <bool AL>
@@ -2300,6 +2335,19 @@ static int conv_os_impl(int64_t num_targets, int num_offsets, const int32_t *out
     // (the one-wave-per-SIMD build only for row-ordered maps: their longest
     // tiles come first, so blocks past the first round are short ones)
     if (pl.da == 2 && !group_masks) pl.da = 1;
+    // blocks per CU: for row-ordered maps (longest blocks first), as many as
+    // fill every CU in the first round, so that no CU runs two long blocks
+    // while another idles.  (Measured, kernel only, row-ordered config-4
+    // layers: s8 128 -> 128 40.1 -> 32.4 us and s8 256 -> 256 at 96-column
+    // tiles 101.8 -> 82.2 us at one block per CU; the 529-block s4 128 -> 128
+    // 58.2 -> 53.2 us and s4 192 -> 128 89.4 -> 77.4 us at two.  Index-order
+    // grids, whose blocks are all alike, keep no cap: s8 256 -> 256 went
+    // 84.8 -> 93.9 us at one.)
+    if (tn.blocks_per_cu == 0 && group_masks) {
+      const int64_t blocks = pl.gx * pl.gy * pl.splits;
+      const int cus = device_cu_count();
+      pl.bpc = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(8, blocks / cus)));
+    }
     const int jper = pl.jper;
     const int splits = pl.splits;
     dim3 grid(static_cast<unsigned>(pl.gx), static_cast<unsigned>(pl.gy), static_cast<unsigned>(splits));

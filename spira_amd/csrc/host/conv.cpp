@@ -404,7 +404,7 @@ static torch::Tensor zeroed_workspace(size_t bytes, const torch::Device &dev) {
 // (spira_hip_os_tuning_t, 0 = automatic) and the row order (-1 automatic,
 // 0 off, 1 on).  From Python: a 6-tuple (col_tile, step_channels,
 // offset_splits, offset_pack, block_order, row_order), optionally followed
-// by row_walk and balance_offsets.
+// by row_walk, balance_offsets and blocks_per_cu.
 struct OsTune {
   spira_hip_os_tuning_t k{};
   int row_order = -1;
@@ -414,7 +414,7 @@ static OsTune tune_of(const TuneArg &t) {
   OsTune r;
   if (!t.has_value()) return r;
   const auto &v = *t;
-  SPIRA_CHECK_ARG(v.size() >= 6 && v.size() <= 8, "tuning must have 6, 7 or 8 fields");
+  SPIRA_CHECK_ARG(v.size() >= 6 && v.size() <= 9, "tuning must have 6 to 9 fields");
   r.k.col_tile = static_cast<int>(v[0]);
   r.k.step_channels = static_cast<int>(v[1]);
   r.k.offset_splits = static_cast<int>(v[2]);
@@ -423,6 +423,7 @@ static OsTune tune_of(const TuneArg &t) {
   r.row_order = static_cast<int>(v[5]);
   r.k.row_walk = v.size() > 6 ? static_cast<int>(v[6]) : 0;
   r.k.balance_offsets = v.size() > 7 ? static_cast<int>(v[7]) : 0;
+  r.k.blocks_per_cu = v.size() > 8 ? static_cast<int>(v[8]) : 0;
   SPIRA_CHECK_ARG(r.row_order >= -1 && r.row_order <= 1, "row_order must be -1, 0 or 1");
   return r;
 }

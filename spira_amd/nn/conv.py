@@ -382,9 +382,10 @@ def os_candidates(c_in: int, c_out: int, volume: int) -> List[List[int]]:
     width, offset splits, offset packing where it applies (16-, 32- and
     64-channel inputs of kernels above 27 offsets), the block order (dispatch
     order, one range per XCD, or runs of 4 / 8 / 16 blocks per XCD), and the
-    row walk (inputs of at most 16 channels with a map), and the work balance
+    row walk (inputs of at most 16 channels with a map), the work balance
     (a row tile of a row-ordered map with more valid offsets than a third or
-    a half of the kernel's split over blocks)."""
+    a half of the kernel's split over blocks), and the cap on resident
+    blocks per CU (the library's rule, none, one or two)."""
     cin_p = (c_in + 15) // 16 * 16
     cols = [0] + [c for c in (32, 64, 96, 128) if c <= (c_out + 31) // 32 * 32]
     steps = [0, 32] + ([64] if cin_p >= 64 else []) + ([128] if cin_p >= 96 else [])
@@ -392,7 +393,7 @@ def os_candidates(c_in: int, c_out: int, volume: int) -> List[List[int]]:
     packs = [0, 1, 2, 4] if (volume > 27 and cin_p in (16, 32, 64)) else [0]
     walks = [0, 1] if (c_in <= 16 and volume > 1) else [0]
     balance = [0, (volume + 2) // 3, (volume + 1) // 2] if volume >= 8 else [0]
-    return [cols, steps, splits, packs, [0, 1, 2, 3, 4], walks, balance]
+    return [cols, steps, splits, packs, [0, 1, 2, 3, 4], walks, balance, [0, -1, 1, 2]]
 
 
 def time_os_calls(layer: "SparseConv", calls, tuning: tuple, reps: int) -> float:

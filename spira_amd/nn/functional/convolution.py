@@ -114,11 +114,12 @@ def sparse_convolution_forward_hs_merged(num_sources: int, num_targets: int, sou
 def _tuning(tuning) -> Optional[tuple]:
     """An output-stationary launch choice: None (automatic) or a tuple
     (col_tile, step_channels, offset_splits, offset_pack, block_order,
-    row_order[, row_walk[, balance_offsets]]); 0 (and -1 for row_order) in
-    a field = automatic; row_walk 1 sums each target's valid pairs on the
-    vector ALU (fp16 layers of at most 16 input channels); balance_offsets
-    > 0 splits a row tile of a row-ordered map with more valid offsets than
-    that over several blocks (-1: never)."""
+    row_order[, row_walk[, balance_offsets[, blocks_per_cu]]]); 0 (and -1
+    for row_order) in a field = automatic; row_walk 1 sums each target's
+    valid pairs on the vector ALU (fp16 layers of at most 16 input
+    channels); balance_offsets > 0 splits a row tile of a row-ordered map
+    with more valid offsets than that over several blocks (-1: never);
+    blocks_per_cu 1..8 caps the resident blocks per CU (-1: no cap)."""
     if tuning is None:
         return None
     if type(tuning) is tuple:
@@ -126,8 +127,8 @@ def _tuning(tuning) -> Optional[tuple]:
         if t is not None:
             return t
     t = tuple(int(v) for v in tuning)
-    if len(t) not in (6, 7, 8):
-        raise ValueError(f"an output-stationary tuning has 6, 7 or 8 fields, got {len(t)}")
+    if len(t) not in (6, 7, 8, 9):
+        raise ValueError(f"an output-stationary tuning has 6 to 9 fields, got {len(t)}")
     if type(tuning) is tuple and len(_TUNINGS) < 4096:
         _TUNINGS[tuning] = t
     return t

@@ -96,11 +96,12 @@ def test_os_tuning_changes_the_launch():
 
 def test_os_candidates():
     from spira_amd.nn.conv import os_candidates
-    cols, steps, splits, packs, orders, walks, balance = os_candidates(256, 256, 27)
+    cols, steps, splits, packs, orders, walks, balance, bpc = os_candidates(256, 256, 27)
     assert cols == [0, 32, 64, 96, 128] and steps == [0, 32, 64, 128] and packs == [0] and orders == [0, 1, 2, 3, 4]
     assert walks == [0]  # the row walk is for inputs of at most 16 channels
     assert balance == [0, 9, 14]  # a third or a half of the offsets per part
-    cols, steps, splits, packs, orders, walks, balance = os_candidates(16, 16, 125)
+    assert bpc == [0, -1, 1, 2]
+    cols, steps, splits, packs, orders, walks, balance, bpc = os_candidates(16, 16, 125)
     assert cols == [0, 32] and steps == [0, 32] and packs == [0, 1, 2, 4] and walks == [0, 1]
     assert balance == [0, 42, 63]
     assert os_candidates(3, 32, 1)[2] == [0] and os_candidates(3, 32, 1)[5] == [0]  # no map: no walk
