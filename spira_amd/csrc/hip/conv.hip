@@ -1024,8 +1024,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DA == 2 ? 1
   // per-row reads of one column are conflict-free) and every step reads its
   // column there.  Larger kernels: lane L of a wave fetches the entry of row
   // L % 32 of the wave's rows for step u into the stage's index slot, NS
-  // steps ahead (lane l then reads the entries of rows l % 16 and 16 + l % 16).  Rows past T read nothing (out of
-  // range) and are masked when resolved.  No map: the identity (logical row
+  // steps ahead (lane l then reads the entries of rows l % 16 and 16 + l % 16);
+  // with offset packing each fetch serves two offsets of the step, one per
+  // half-wave, so a step costs OP / 2 fetch loads (measured on the 125-offset
+  // layers of 16 to 64 channels: the map fetches cost as much as the gathers'
+  // request slots).  Rows past T read nothing (out of range) and are masked
+  // when resolved.  No map: the identity (logical row
   // i reads source i); the fetches then load nothing (out of range) but keep
   // the vmcnt arithmetic.
   const bool ident = map == nullptr;
@@ -1041,6 +1045,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DA == 2 ? 1
   fit.init(ulo, uhi);
   pit = fit;
   int fu = 0;
+  constexpr int kFetchOps = OP > 1 ? OP / 2 : 1;  // map-fetch loads per step
   const int KP = Kc | 1;
   int32_t *tile = reinterpret_cast<int32_t *>(ring_lds + C::RING);
   if (tiled) {
@@ -1067,14 +1072,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DA == 2 ? 1
     (void)u;
     // (tiled: out-of-range fetches that only keep the vmcnt arithmetic)
     const bool none = tiled || fbase == kOutOfRange || fu >= nsteps;
-    const uint32_t off = none ? kOutOfRange : fbase + fit.j * 4u;
-    ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP][uwave * 64]);
-    if constexpr (OP > 1) {
-#pragma unroll
-      for (int q = 0; q < OP - 1; ++q) {
-        const uint32_t offq = (none || fit.jp[q] < 0) ? kOutOfRange : fbase + fit.jp[q] * 4u;
-        ring::dma4(mr, offq, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP + 1 + q][uwave * 64]);
-      }
+    if constexpr (OP == 1) {
+      const uint32_t off = none ? kOutOfRange : fbase + fit.j * 4u;
+      ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value][uwave * 64]);
+    } else {
+      // two offset parts per fetch: lanes 0-31 take part 2p, lanes 32-63
+      // part 2p + 1 (rows lane % 32), into slots 0-31 / 32-63 of index
+      // slot St * OP + 2p
+      ring::unroll<OP / 2>([&](auto P) {
+        constexpr int p = decltype(P)::value;
+        const int ja = p == 0 ? fit.j : fit.jp[2 * p - 1];
+        const int jj = kh == 0 ? ja : fit.jp[2 * p];
+        const uint32_t off = (none || jj < 0) ? kOutOfRange : fbase + jj * 4u;
+        ring::dma4(mr, off, tiled ? &orow_s[uwave][0] : &idx_lds[decltype(St)::value * OP + 2 * p][uwave * 64]);
+      });
     }
     ++fu;
     fit.step(nch);
@@ -1116,13 +1127,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DA == 2 ? 1
         }
       }
     } else {
+      // (part m of the step: index slot St * OP + 2 (m / 2), rows from
+      // 32 (m % 2); tile rt's rows from 16 rt)
       idx[0] = ring::rd4<decltype(St)::value * OP * 1024>(ibase);
       idx[1] = ring::rd4<decltype(St)::value * OP * 1024 + 64>(ibase);
       if constexpr (OP > 1) {
         ring::unroll<OP - 1>([&](auto Q) {
-          constexpr int q = decltype(Q)::value;
-          st.idxp[q][0] = ring::rd4<(decltype(St)::value * OP + 1 + q) * 1024>(ibase);
-          st.idxp[q][1] = ring::rd4<(decltype(St)::value * OP + 1 + q) * 1024 + 64>(ibase);
+          constexpr int m = decltype(Q)::value + 1;
+          constexpr int at = (decltype(St)::value * OP + 2 * (m / 2)) * 1024 + (m % 2) * 128;
+          st.idxp[m - 1][0] = ring::rd4<at>(ibase);
+          st.idxp[m - 1][1] = ring::rd4<at + 64>(ibase);
         });
       }
       ring::lds_wait();
@@ -1155,9 +1169,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DA == 2 ? 1
   if constexpr (DA >= 1) {
     // gathered rows two steps ahead (maps held in LDS only)
     if (tiled) ring::run_da<C, ALIGNED, CAT>(acc, nsteps, resolve, op, n0, ring_lds);
-    else ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+    else ring::run<C, ALIGNED, CAT, kFetchOps, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   } else {
-    ring::run<C, ALIGNED, CAT, OP, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
+    ring::run<C, ALIGNED, CAT, kFetchOps, OP>(acc, nsteps, fetch, resolve, op, n0, ring_lds);
   }
   if (balance && nparts > 1) {
     // the partial tile to the part's slot (lane layout of the accumulators:
