@@ -200,7 +200,7 @@ def test_os_tuning_keeps_results(dev, tmp_path):
                    n_samples=2, save_dir=str(tmp_path), tune_tag="os", allow_gs_tuning=False)
     tuned = [m for m in model.modules() if isinstance(m, spira_amd.nn.SparseConv)
              and m._tunable_config["os_tuning"] is not None]
-    assert len(tuned) >= 20 and all(len(m._tunable_config["os_tuning"]) == 7 for m in tuned)
+    assert len(tuned) >= 20 and all(len(m._tunable_config["os_tuning"]) == 9 for m in tuned)
     after = run()
     for a, b in zip(before, after):
         rms = float(a.pow(2).mean().sqrt()) or 1.0
