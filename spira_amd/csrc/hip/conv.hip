@@ -301,8 +301,10 @@ __device__ __forceinline__ IssueCtx<C> issue_ctx(const char *ring, int wave, int
     const int c8 = ((v % C::CPR) ^ C::swz(n)) * 8;
     const int part = OP > 1 ? c8 / op.CinP : 0;
     const int ch = c8 - part * op.CinP;
-    cx.wlane[i] = (n < C::BN && n0 + n < op.CoutP) ? static_cast<uint32_t>(((n0 + n) * op.CinP + ch) * 2)
-                                                     : kOutOfRange;
+    // (columns past C_out: their prepared weights are zero padding, and the
+    // out-of-range DMA writes the same zeros without reading them)
+    cx.wlane[i] = (n < C::BN && n0 + n < op.Cout) ? static_cast<uint32_t>(((n0 + n) * op.CinP + ch) * 2)
+                                                    : kOutOfRange;
     cx.c8[i] = OP > 1 ? part : c8;
   }
   cx.ldsw = __builtin_amdgcn_readfirstlane(lds_addr(ring) + wave * 64 * 16);
