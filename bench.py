@@ -92,7 +92,8 @@ def parse():
     p.add_argument("--no-fuse", action="store_true", help="run batch norm / ReLU / residual adds unfused")
     p.add_argument("--no-tune", action="store_true", help="skip the selector (library default launch choices)")
     p.add_argument("--only", default="", help="comma list of legs: e2e, config5, kmap, layer, family (the "
-                                              "dominant family's layers alone, for counters), calib (a plain "
+                                              "dominant family's layers alone, for counters), c5family (config 5's "
+                                              "125-offset layer shapes alone, for counters), calib (a plain "
                                               "256 MiB device copy: the reference point of the HBM counters)")
     p.add_argument("--concurrent-maps", action="store_true",
                    help="build every layer map on a side stream of its own (the library's opt-in fan-out)")
@@ -506,6 +507,33 @@ def family_leg(torch, indoor_np, rows, fams):
     return out
 
 
+def c5family_leg(torch, blobs_np):
+    """Config 5's 125-offset submanifold layer shapes, one per level (16, 32,
+    64, 128 channels at strides 1, 2, 4, 8), each alone on the config-5 map of
+    its stride with random features and weights at the library's default
+    launch: 1 warm launch and 20 back-to-back launches each, in that order
+    (the runs of identical dispatches the rocprofv3 counter passes read)."""
+    from spira_amd.nn import functional as F
+    from spira_amd.nn.functional import _native
+    dev = torch.device("cuda:0")
+    out = {}
+    keys, _ = F.flat_sort(torch.from_numpy(blobs_np).to(dev), True)
+    for stride, c in ((1, 16), (2, 32), (4, 64), (8, 128)):
+        ks = keys if stride == 1 else F.downsample(keys, (stride,) * 3)
+        m = F.build_kmap(ks, ks, 5, stride, 0)[2]
+        T = int(ks.shape[0])
+        P = int((m >= 0).sum())
+        X = torch.randn(T, c, device=dev).half()
+        W = (torch.randn(125, c, c, device=dev) / np.sqrt(125 * c)).half()
+        ms = _native._C.time_conv_os(T, T, m, X, W, 20)
+        plan = _native._C.conv_os_plan(T, 125, c, 0, c, True, None)
+        flops = 2.0 * P * c * c
+        out[f"s{stride} {c}->{c} K125"] = {"kernel_ms": ms, "T": T, "P_over_T": round(P / T, 2),
+                                           "plan": list(plan), "mfma_frac": flops / (ms * 1e-3) / 1e12 /
+                                           MFMA_F16_PEAK_TFLOPS}
+    return out
+
+
 def calib_leg(torch, mib=256, reps=5):
     """A plain device-to-device copy of a known size: reads and writes
     `mib` MiB per launch.  Run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
@@ -598,6 +626,8 @@ def main():
         res["config5_ms"], _, _ = c5.time(10, 5)
         cfg["config5_voxels"] = int(blobs.shape[0])
         del c5
+    if "c5family" in legs:
+        res["config5_families"] = c5family_leg(torch, scenes.lidar_blobs())
     if "kmap" in legs or "layer" in legs:
         lidar = scenes.lidar()
         lkeys, _ = F.flat_sort(torch.from_numpy(lidar).to(dev), True)
