@@ -419,11 +419,12 @@ __device__ __forceinline__ void issue_slice(const IssueCtx<C> &cx, const StepIn 
       }
     }
   }
-  // weights: chunk c8 of the lane's row is real while c8 < CinP - kb; an
-  // out-of-range lane offset stays out of range after adding the step's
-  // (wstep < wbytes < 2^31)
+  // weights: chunk c8 of the lane's row holds input channels while c8 <
+  // Cin - kb (the chunks past it are zero padding, which the out-of-range
+  // DMA writes without reading); an out-of-range lane offset stays out of
+  // range after adding the step's (wstep < wbytes < 2^31)
   const uint32_t wstep = static_cast<uint32_t>((st.wrow * op.CoutP * op.CinP + st.kb) * 2);
-  const int wlim = st.live ? op.CinP - st.kb : 0;
+  const int wlim = st.live ? op.Cin - st.kb : 0;
 #pragma unroll
   for (int i = KS; i < C::BVEC; i += C::NKS) {
     const uint32_t off = cx.c8[i] < wlim ? cx.wlane[i] + wstep : kOutOfRange;
@@ -612,7 +613,7 @@ template <class C, int S>
 __device__ __forceinline__ void issue_b(const IssueCtx<C> &cx, const StepIn &st, const Operands &op,
                                         __amdgpu_buffer_rsrc_t wr) {
   const uint32_t wstep = static_cast<uint32_t>((st.wrow * op.CoutP * op.CinP + st.kb) * 2);
-  const int wlim = st.live ? op.CinP - st.kb : 0;
+  const int wlim = st.live ? op.Cin - st.kb : 0;  // (chunks past C_in: zero padding)
 #pragma unroll
   for (int i = 0; i < C::BVEC; ++i) {
     const uint32_t off = cx.c8[i] < wlim ? cx.wlane[i] + wstep : kOutOfRange;
