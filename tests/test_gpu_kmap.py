@@ -39,6 +39,21 @@ def test_flatten_sort_and_unflatten(dev, scene_small):
         assert np.array_equal(np_(F.unflatten(keys)), orc.unflatten(rk))
 
 
+@pytest.mark.parametrize("double", [True, False])
+def test_flatten_sort_large(dev, double):
+    """A large shuffled input (over 300k rows, a third of them repeated):
+    keys and the stable permutation against the oracle (equal keys keep
+    their input order)."""
+    rng = np.random.default_rng(5)
+    c = np.unique(rng.integers(0, 250, size=(420000, 3)), axis=0).astype(np.int32)
+    c = rng.permutation(np.concatenate([c, c[::3]]))
+    assert c.shape[0] > 250000
+    keys, perm = F.flat_sort(torch.from_numpy(c).to(dev), double)
+    rk, rp = orc.flatten_sort(c, double)
+    assert np.array_equal(np_(keys), rk)
+    assert np.array_equal(np_(perm), rp.astype(np.int64))
+
+
 def test_flatten_sort_duplicates_are_stable(dev):
     rng = np.random.default_rng(3)
     c = rng.integers(0, 6, size=(5000, 3)).astype(np.int32)  # many duplicates
