@@ -26,6 +26,9 @@ run inside one event-timed region.  Also reported on the same run:
   * cpu_baseline: the same legs by the OpenMP CPU restatement (oracle/) on
     the host cores, each checked against the GPU result: config 4 end to end
     (headline), the config-2 k = 3 map and a config-3 C = 64 layer.
+Opt-in legs for counter passes (--only): family (config 4's families, each
+layer alone at its tuned launch), c5family (config 5's 125-offset layer
+shapes alone) and calib (a plain 256 MiB copy, the HBM counters' reference).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only legs]
 """
